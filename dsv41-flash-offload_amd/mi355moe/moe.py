@@ -1,0 +1,145 @@
+"""Routed-expert MoE layer on MI355X: routing prep, decode expert path and fixed-order combine.
+
+Every computation runs in libmi355moe.so; this module allocates buffers and launches on the current stream.
+"""
+import torch
+
+from . import _lib
+
+# Routes per expert served by the decode path (larger groups belong to the fat-expert path).
+GEMV_MAX_ROWS = 256
+
+
+def _i(t):
+    return _lib.ptr(t)
+
+
+def permute(ids, w, topk, E, stream=None):
+    """Routing prep (patches/vllm-exl3-host-dma.patch:204-236,296-312), stable by (expert, route index).
+    Returns dict of device tensors: counts [E+1], offsets [E+2], order, token_sorted, weight_sorted, inv_order,
+    active [E], nactive [1]."""
+    ids = ids.reshape(-1).contiguous().long()
+    n = ids.numel()
+    dev = ids.device
+    w = None if w is None else w.reshape(-1).contiguous().float()
+    o = {
+        "counts": torch.empty(E + 1, dtype=torch.int32, device=dev),
+        "offsets": torch.empty(E + 2, dtype=torch.int32, device=dev),
+        "order": torch.empty(max(n, 1), dtype=torch.int32, device=dev),
+        "token_sorted": torch.empty(max(n, 1), dtype=torch.int32, device=dev),
+        "weight_sorted": torch.empty(max(n, 1), dtype=torch.float32, device=dev),
+        "inv_order": torch.empty(max(n, 1), dtype=torch.int32, device=dev),
+        "active": torch.empty(E, dtype=torch.int32, device=dev),
+        "nactive": torch.empty(1, dtype=torch.int32, device=dev),
+    }
+    wsb = _lib.load().mm_permute_workspace(n, E)
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+    _lib.call("mm_permute", _i(ids), _i(w), n, topk, E, _i(o["counts"]), _i(o["offsets"]), _i(o["order"]),
+              _i(o["token_sorted"]), _i(o["weight_sorted"]), _i(o["inv_order"]), _i(o["active"]), _i(o["nactive"]),
+              _i(ws), wsb, _lib.stream_ptr(stream))
+    return o
+
+
+def expert_gemv(store, x16, routes, T, n, topk, max_rows, stream=None):
+    """Per-route expert outputs Y fp32 [n, H] (flat route order) on the decode path."""
+    dev = x16.device
+    E, H, I = store.E, store.H, store.I
+    wsb = _lib.load().mm_gemv_workspace(n, E, H, I)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+    Y = torch.zeros((n, H), dtype=torch.float32, device=dev)
+    _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), T, n, topk, _i(routes["offsets"]), _i(routes["order"]),
+              _i(routes["active"]), _i(routes["nactive"]), int(max_rows), _i(Y), _i(ws), wsb, _lib.stream_ptr(stream))
+    return Y
+
+
+def combine(Y, ids, w, T, k, H, E, out=None, stream=None):
+    ids = ids.reshape(-1).contiguous().long()
+    w = w.reshape(-1).contiguous().float()
+    acc = out is not None
+    if out is None:
+        out = torch.empty((T, H), dtype=torch.float32, device=Y.device)
+    _lib.call("mm_combine", _i(out), _i(Y), _i(ids), _i(w), T, k, H, E, 1 if acc else 0, _lib.stream_ptr(stream))
+    return out
+
+
+def to_expert_input(x):
+    """Expert input fp16 [T, H] from a bf16 / fp16 / fp32 activation (bf16 -> fp16 is exact in range)."""
+    if x.dtype == torch.float16:
+        return x.contiguous()
+    if x.dtype == torch.float32:
+        xf = x.contiguous()
+        x16 = torch.empty(x.shape, dtype=torch.float16, device=x.device)
+        _lib.call("mm_prepare_input", _i(xf), x.shape[0], x.shape[1], 0, None, _i(x16), _lib.stream_ptr())
+        return x16
+    return x.contiguous().to(torch.float16)
+
+
+def moe_forward(store, x, ids, w, shared_expert=None, stream=None):
+    """out fp32 [T, H] = sum_j w[t, j] * expert_{ids[t, j]}(x_t) (+ expert `shared_expert` with weight 1).
+
+    Routes with ids outside [0, E) contribute nothing. The decode path serves up to GEMV_MAX_ROWS routes
+    per expert."""
+    T = x.shape[0]
+    ids = ids.reshape(T, -1).long()
+    w = w.reshape(T, -1).float()
+    if shared_expert is not None:
+        ids = torch.cat([ids, torch.full((T, 1), int(shared_expert), dtype=torch.long, device=ids.device)], 1)
+        w = torch.cat([w, torch.ones((T, 1), dtype=torch.float32, device=w.device)], 1)
+    k = ids.shape[1]
+    n = T * k
+    routes = permute(ids, w, k, store.E, stream)
+    max_rows = int(routes["counts"][: store.E].max().item()) if n else 0
+    if max_rows > GEMV_MAX_ROWS:
+        raise NotImplementedError(f"expert with {max_rows} routes: the fat-expert path is required (> {GEMV_MAX_ROWS})")
+    x16 = to_expert_input(x)
+    Y = expert_gemv(store, x16, routes, T, n, k, max(1, max_rows), stream)
+    return combine(Y, ids, w, T, k, store.H, store.E, stream=stream)
+
+
+class DecodeRunner:
+    """Fixed-shape decode MoE layer with every buffer preallocated: no allocation and no host sync per call,
+    so a sequence of layers can be captured in one HIP graph."""
+
+    def __init__(self, E, H, I, T, k, device="cuda", shared=True):
+        self.E, self.H, self.I, self.T, self.k0 = E, H, I, T, k
+        self.shared = shared
+        self.Eall = E + (1 if shared else 0)
+        self.k = k + (1 if shared else 0)
+        self.n = T * self.k
+        dev = torch.device(device)
+        self.ids = torch.zeros((T, self.k), dtype=torch.long, device=dev)
+        self.w = torch.zeros((T, self.k), dtype=torch.float32, device=dev)
+        if shared:
+            self.ids[:, -1] = E
+            self.w[:, -1] = 1.0
+        n, Ea = self.n, self.Eall
+        self.counts = torch.empty(Ea + 1, dtype=torch.int32, device=dev)
+        self.offsets = torch.empty(Ea + 2, dtype=torch.int32, device=dev)
+        self.order = torch.empty(n, dtype=torch.int32, device=dev)
+        self.active = torch.empty(Ea, dtype=torch.int32, device=dev)
+        self.nactive = torch.empty(1, dtype=torch.int32, device=dev)
+        self.pws_bytes = _lib.load().mm_permute_workspace(n, Ea)
+        self.pws = torch.empty(max(self.pws_bytes, 1), dtype=torch.uint8, device=dev)
+        self.gws_bytes = _lib.load().mm_gemv_workspace(n, Ea, H, I)
+        self.gws = torch.zeros(self.gws_bytes, dtype=torch.uint8, device=dev)
+        self.Y = torch.zeros((n, H), dtype=torch.float32, device=dev)
+        self.x16 = torch.empty((T, H), dtype=torch.float16, device=dev)
+        self.out = torch.empty((T, H), dtype=torch.float32, device=dev)
+
+    def set_routes(self, ids, w):
+        self.ids[:, : self.k0].copy_(ids)
+        self.w[:, : self.k0].copy_(w)
+
+    def run(self, store, x16=None, ids=None, w=None, out=None, stream=None):
+        """One layer: permute -> fused decode expert MLP -> combine. ids/w default to the runner's buffers."""
+        s = _lib.stream_ptr(stream)
+        ids = self.ids if ids is None else ids
+        w = self.w if w is None else w
+        x16 = self.x16 if x16 is None else x16
+        out = self.out if out is None else out
+        _lib.call("mm_permute", _i(ids), _i(w), self.n, self.k, self.Eall, _i(self.counts), _i(self.offsets),
+                  _i(self.order), None, None, None, _i(self.active), _i(self.nactive), _i(self.pws), self.pws_bytes, s)
+        _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), self.T, self.n, self.k, _i(self.offsets), _i(self.order),
+                  _i(self.active), _i(self.nactive), self.T, _i(self.Y), _i(self.gws), self.gws_bytes, s)
+        _lib.call("mm_combine", _i(out), _i(self.Y), _i(ids), _i(w), self.T, self.k, self.H, self.Eall, 0, s)
+        return out

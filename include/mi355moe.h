@@ -1,0 +1,146 @@
+/*
+ * mi355moe -- C ABI of the MI355X-native routed-expert MoE layer.
+ *
+ * Conventions for every entry point:
+ *   - All pointers are caller-owned: device memory, or host memory allocated with mm_host_alloc (mapped,
+ *     coherent) where a parameter says "host-mapped". The library allocates nothing per call.
+ *   - `stream` is a hipStream_t (0 = the null stream). Work is enqueued on it; no entry point synchronises
+ *     the host, so every call can be captured into a HIP graph.
+ *   - Return 0 on success or a negative MM_ERR_* code; mm_last_error() gives a thread-local message.
+ *   - Calls on distinct streams with distinct buffers are independent; calls sharing a workspace race.
+ *
+ * Trellis layout (EXL3 3 bpw, identical to the reference's storage): a K x N matrix is tiles
+ * [K/16][N/16] of 48 uint16 words (96 bytes); gate/up are K=H, N=I; down is K=I, N=H.
+ * Scales (fp16): suh13 [E][2][H], svh13 [E][2][I], suh2 [E][I], svh2 [E][H] (reference parameter shapes,
+ * patches/vllm-exl3-host-dma.patch:660-690).
+ */
+#ifndef MI355MOE_H
+#define MI355MOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MM_OK 0
+#define MM_ERR_ARG (-1)      /* invalid argument (shape, size, null pointer) */
+#define MM_ERR_HIP (-2)      /* HIP runtime error (launch, copy, allocation of host memory) */
+#define MM_ERR_UNSUP (-3)    /* unsupported configuration (e.g. codebook other than mul1) */
+
+typedef void* mm_stream_t;
+
+/* Library version (major*10000 + minor*100 + patch). */
+int mm_version(void);
+
+/* Thread-local message of the last failing call on this thread ("" if none). */
+const char* mm_last_error(void);
+
+/* Pinned, device-mapped, coherent host memory for the host mailbox and host-resident expert copies
+ * (replaces the reference's torch pin_memory() mailbox, ct/ct_vllm.py:62-65, and the cudaHostRegister'd
+ * home store, patches/vllm-exl3-host-dma.patch:609-617). */
+int mm_host_alloc(void** ptr, size_t bytes);
+int mm_host_free(void* ptr);
+
+/* ----------------------------------------------------------------------------------------- routing */
+
+/* Router top-k (vLLM FusedMoE semantics at the boundary patches/vllm-exl3-host-dma.patch:496-507):
+ * logits[t][e] = sum_h x[t][h] * gate[e][h] (x bf16 [T][H], gate fp32 [E][H], fp32 sums);
+ * ids[t][:k] = the k largest logits (ties -> lower expert id), w[t][:k] = softmax over those k logits.
+ * logits may be NULL. Requires E <= 1024, k <= 32. */
+int mm_router_topk(const void* x_bf16, int T, int H, const float* gate, int E, int k, float* logits, int64_t* ids,
+                   float* w, mm_stream_t stream);
+
+/* Decode-tier split; replaces ft_split (ct/ft_tier_cu_v.cu:129-143), same buffers and semantics:
+ * sel int64 [n], w fp32 [n], z fp16 [bsz][H] (n = bsz * topk), slotof int32 [E], score fp32 [E], pol fp32 [9];
+ * ctrl int64 [16], hx fp16 [bsz*H] and hpicks int32 [n*3] are host-mapped; seqc, dflag int64 [1] and
+ * stats int64 [8] are device counters; counts int32 [E] (may be NULL) accumulates routed counts.
+ * Outputs sel_out int64 [n], w_out fp32 [n]. Extra optional outputs (NULL to skip): hits int32 [E] (resident
+ * touched experts, ascending id), misses int32 [E] (non-resident, stable by score), nhnm int32 [2].
+ * Requires E <= 1024, H % 8 == 0. Scores must not be NaN. */
+int mm_split(const int64_t* sel, const float* w, const void* z_fp16, int n, int bsz, int H, int E, const int32_t* slotof,
+             const float* score, const float* pol, int64_t* ctrl, void* hx, int32_t* hpicks, int64_t* seqc, int li,
+             int64_t* sel_out, float* w_out, int64_t* dflag, int64_t* stats, int32_t* counts, int32_t* hits,
+             int32_t* misses, int32_t* nhnm, mm_stream_t stream);
+
+/* Host-partial add; replaces ft_combine (ct/ft_tier_cu_v.cu:145-153): if dflag[0] != 0, wait (bounded by
+ * timeout_ns, measured on the GPU's constant-rate clock) until host-mapped ctrl[1] >= dflag[0], then
+ * out[i] += hout[i] for i < n. On timeout the partial is dropped and stats[6]++; stats[4] += wait ns,
+ * stats[5]++ as in the reference. */
+int mm_combine_host(float* out, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout, int64_t* stats,
+                    int64_t timeout_ns, mm_stream_t stream);
+
+/* Bytes of device workspace mm_permute needs for n routes over E experts. */
+size_t mm_permute_workspace(int n, int E);
+
+/* Routing prep (patches/vllm-exl3-host-dma.patch:204-236,296-312), made deterministic: ids int64 [n]
+ * (ids outside [0, E) go to the sentinel bin E); counts int32 [E+1]; offsets int32 [E+2] (exclusive sums,
+ * offsets[E+1] = n); order int32 [n] = flat route index at each sorted position, stable by (expert, index);
+ * token_sorted int32 [n] = order / topk; weight_sorted fp32 [n] = w[order] (NULL w or NULL output skips it);
+ * inv_order int32 [n] (may be NULL) = sorted position of each flat index; active int32 [E] (may be NULL) =
+ * experts with count > 0 in ascending id and nactive int32 [1] their number. */
+int mm_permute(const int64_t* ids, const float* w, int n, int topk, int E, int32_t* counts, int32_t* offsets,
+               int32_t* order, int32_t* token_sorted, float* weight_sorted, int32_t* inv_order, int32_t* active,
+               int32_t* nactive, void* workspace, size_t workspace_bytes, mm_stream_t stream);
+
+/* Weighted combine of per-route expert outputs in a fixed order (replaces the fused kernel's atomic
+ * accumulation, patches/vllm-exl3-host-dma.patch:327-342): for every token t and column h,
+ * out[t][h] = (accumulate ? out[t][h] : 0) + sum_{j<k, 0<=ids[t*k+j]<E} w[t*k+j] * Y[t*k+j][h], fp32 fma in
+ * ascending j. Y fp32 [T*k][H] in flat route order. */
+int mm_combine(float* out, const float* Y, const int64_t* ids, const float* w, int T, int k, int H, int E,
+               int accumulate, mm_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ expert layer */
+
+/* Device-side description of one MoE layer's experts (the reference's per-layer pointer tables
+ * layer._exl3_ptrs["gate_trellis"/"up_trellis"/"down_trellis"], patches/vllm-exl3-host-dma.patch:727-751,
+ * and its stacked scale parameters). Every pointer is a device address. */
+typedef struct mm_layer
+{
+    const int64_t* gate_ptr;    /* [E] address of expert e's gate trellis [H/16][I/16][48] */
+    const int64_t* up_ptr;      /* [E] address of expert e's up trellis   [H/16][I/16][48] */
+    const int64_t* down_ptr;    /* [E] address of expert e's down trellis [I/16][H/16][48] */
+    const uint16_t* suh13;      /* fp16 [E][2][H] */
+    const uint16_t* svh13;      /* fp16 [E][2][I] */
+    const uint16_t* suh2;       /* fp16 [E][I] */
+    const uint16_t* svh2;       /* fp16 [E][H] */
+    int E, H, I;
+    float limit;                /* SwiGLU clamp (0 = off); reference default 10 */
+} mm_layer_t;
+
+/* Bytes of device workspace mm_expert_gemv needs; the first mm_gemv_counter_bytes(...) bytes of it must be
+ * zero before the first call (the kernels leave them zero again). */
+size_t mm_gemv_workspace(int n, int E, int H, int I);
+size_t mm_gemv_counter_bytes(int n, int E, int H, int I);
+
+/* Decode expert path (replaces exllamav3 exl3_moe on the decode split, patches/vllm-exl3-host-dma.patch:323-445):
+ * routes come from mm_permute (offsets, order, active, nactive over the same n routes and E experts). For every
+ * routed (token, expert) pair with 0 <= expert < E, computes the expert SwiGLU MLP on x fp16 [T][H] with fused
+ * EXL3 trellis decode and writes Y fp32 [n][H] at the route's flat index (rows of sentinel routes are left
+ * untouched). max_rows bounds the routes of any one expert (<= 256). */
+int mm_expert_gemv(const mm_layer_t* layer, const void* x_fp16, int T, int n, int topk, const int32_t* offsets,
+                   const int32_t* order, const int32_t* active, const int32_t* nactive, int max_rows, float* Y,
+                   void* workspace, size_t workspace_bytes, mm_stream_t stream);
+
+/* ----------------------------------------------------------------------------------------- utility */
+
+/* Synthetic trellis words: word i of a stream with `seed` is bits 16*(i%4)..+15 of
+ * splitmix64(seed + (i/4 + 1) * 0x9E3779B97F4A7C15). Fills dst[j] = word(start + j) for j < n. */
+int mm_synth_u16(uint16_t* dst, uint64_t n, uint64_t seed, uint64_t start, mm_stream_t stream);
+
+/* Expert-store fill: for experts e in [0, E) of one layer whose trellis lives at gate_ptr/up_ptr/down_ptr,
+ * writes the synthetic words of stream mm_expert_seed(layer_seed, e) (gate, then up, then down). */
+int mm_synth_layer(const mm_layer_t* layer, uint64_t layer_seed, mm_stream_t stream);
+uint64_t mm_expert_seed(uint64_t layer_seed, uint64_t expert);
+
+/* Convert an fp32 [T][H] activation to the expert input fp16 [T][H] through bf16, optionally rescaling each
+ * row to unit RMS first (the decode-chain workload's between-layer step): x16 = fp16(bf16(x * s_t)),
+ * s_t = 1/sqrt(mean(x_t^2)) if rescale else 1. Also writes bf16 [T][H] if x_bf16 != NULL. */
+int mm_prepare_input(const float* x, int T, int H, int rescale, void* x_bf16, void* x_fp16, mm_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355MOE_H */

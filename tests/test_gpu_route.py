@@ -1,0 +1,188 @@
+"""GPU parity of the routing kernels against the oracle (bit-exact for every integer output)."""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+@pytest.mark.parametrize("n,E,topk", [(1, 8, 1), (36, 385, 9), (4096, 384, 8), (8192, 385, 8), (8193, 384, 8),
+                                      (131072, 384, 8), (40000, 1024, 4)])
+def test_permute_bitexact(dev, n, E, topk):
+    import torch
+    from mi355moe import moe
+    rng = np.random.default_rng(n + E)
+    ids = rng.integers(0, E, n).astype(np.int64)
+    ids[rng.random(n) < 0.01] = -1                                  # masked routes -> sentinel
+    w = rng.normal(0, 1, n).astype(np.float32)
+    print(f"permute n={n} E={E}", flush=True)
+    r = moe.permute(_t(ids, dev), _t(w, dev), topk, E)
+    torch.cuda.synchronize()
+    counts, offsets, order, tok, ws = O.permute(ids, w, topk, E)
+    assert np.array_equal(r["counts"].cpu().numpy(), counts)
+    assert np.array_equal(r["offsets"].cpu().numpy(), offsets)
+    assert np.array_equal(r["order"].cpu().numpy()[:n], order)
+    assert np.array_equal(r["token_sorted"].cpu().numpy()[:n], tok)
+    assert np.array_equal(r["weight_sorted"].cpu().numpy()[:n], ws)
+    inv = np.empty(n, np.int32)
+    inv[order] = np.arange(n, dtype=np.int32)
+    assert np.array_equal(r["inv_order"].cpu().numpy()[:n], inv)
+    act = np.nonzero(counts[:E])[0]
+    assert int(r["nactive"].item()) == act.size
+    assert np.array_equal(r["active"].cpu().numpy()[: act.size], act)
+
+
+def _split_case(seed, pol, score_kind="zero"):
+    from mi355moe import workload
+    ids, w = workload.zipf_routing(4, 8, 384, seed=seed)
+    slotof = workload.cache_map(ids, 384, slots=709, frac_resident=0.4, seed=seed)
+    z = np.random.default_rng(seed).normal(0, 1, (4, 4096)).astype(np.float16)
+    score = np.zeros(384, np.float32) if score_kind == "zero" else np.random.default_rng(seed + 1).permutation(384).astype(np.float32)
+    return ids, w, z, slotof, score, np.asarray(pol, np.float32)
+
+
+POL_DEFAULT = [0.58, 0.03, 0.11, 0.20, 0.35, 384, -1, 0, 0]   # image defaults (cost model)
+POL_CHEAP = [0.58, 0.03, 0.01, 0.05, 0.35, 384, -1, 0, 0]     # cheap CPU: several picks
+
+
+@pytest.mark.parametrize("seed,pol,score_kind", [(1, POL_DEFAULT, "zero"), (2, POL_CHEAP, "zero"),
+                                                 (3, POL_CHEAP, "perm"), (4, [0.58, 0.03, 0.11, 0.2, 0.35, 384, 2, 0, 0], "zero"),
+                                                 (5, [0.58, 0.03, 0.11, 0.2, 0.35, 384, 0, 1, 0], "zero")])
+def test_split_bitexact(dev, seed, pol, score_kind):
+    import torch
+    from mi355moe import _lib
+    from mi355moe.hostmem import HostBuffer
+    ids, w, z, slotof, score, pol = _split_case(seed, pol, score_kind)
+    n, bsz, H, E = ids.size, 4, 4096, 384
+    ref = O.split(ids, w, z, E, slotof, score, pol, seqc=5, li=7)
+    hb = HostBuffer(16 * 8 + bsz * H * 2 + n * 3 * 4)
+    ctrl = hb.array(np.int64, (16,), 0)
+    hx = hb.array(np.uint16, (bsz * H,), 128)
+    hp = hb.array(np.int32, (n * 3,), 128 + bsz * H * 2)
+    ctrl[:] = 0
+    d = {k: _t(v, dev) for k, v in dict(sel=ids.ravel(), w=w.ravel(), z=z.view(np.uint16), slotof=slotof, score=score,
+                                        pol=pol).items()}
+    seqc = torch.tensor([5], dtype=torch.int64, device=dev)
+    sel_out = torch.empty(n, dtype=torch.int64, device=dev)
+    w_out = torch.empty(n, dtype=torch.float32, device=dev)
+    dflag = torch.full((1,), -7, dtype=torch.int64, device=dev)
+    stats = torch.zeros(8, dtype=torch.int64, device=dev)
+    counts = torch.zeros(E, dtype=torch.int32, device=dev)
+    hits = torch.full((E,), -1, dtype=torch.int32, device=dev)
+    misses = torch.full((E,), -1, dtype=torch.int32, device=dev)
+    nhnm = torch.zeros(2, dtype=torch.int32, device=dev)
+    print(f"split seed={seed}", flush=True)
+    _lib.call("mm_split", d["sel"].data_ptr(), d["w"].data_ptr(), d["z"].data_ptr(), n, bsz, H, E, d["slotof"].data_ptr(),
+              d["score"].data_ptr(), d["pol"].data_ptr(), hb.data_ptr(0), hb.data_ptr(128), hb.data_ptr(128 + bsz * H * 2),
+              seqc.data_ptr(), 7, sel_out.data_ptr(), w_out.data_ptr(), dflag.data_ptr(), stats.data_ptr(),
+              counts.data_ptr(), hits.data_ptr(), misses.data_ptr(), nhnm.data_ptr(), _lib.stream_ptr())
+    torch.cuda.synchronize()
+    nh, nm = nhnm.cpu().tolist()
+    assert nh == len(ref["hits"]) and nm == len(ref["misses"])
+    assert np.array_equal(hits.cpu().numpy()[:nh], ref["hits"])
+    assert np.array_equal(misses.cpu().numpy()[:nm], ref["misses"])
+    assert np.array_equal(sel_out.cpu().numpy(), ref["sel_out"])
+    assert np.array_equal(w_out.cpu().numpy().view(np.uint32), ref["w_out"].view(np.uint32))
+    assert np.array_equal(stats.cpu().numpy(), ref["stats"])
+    assert np.array_equal(counts.cpu().numpy(), ref["counts"])
+    assert int(dflag.item()) == int(ref["dflag"][0]) and int(seqc.item()) == int(ref["seqc"][0])
+    if ref["dflag"][0]:
+        assert np.array_equal(ctrl[[0, 2, 3, 4]], ref["ctrl"][[0, 2, 3, 4]])
+        npk = int(ref["ctrl"][4])
+        assert np.array_equal(hp[: 3 * npk], ref["hpicks"][: 3 * npk])
+        assert np.array_equal(hx, ref["hx"])
+
+
+def test_combine_host_paths(dev):
+    """Host-partial add: no job, job done, and the bounded timeout path (the host never answers)."""
+    import torch
+    from mi355moe import _lib
+    from mi355moe.hostmem import HostBuffer
+    n = 4 * 4096
+    hb = HostBuffer(128 + n * 4)
+    ctrl = hb.array(np.int64, (16,), 0)
+    hout = hb.array(np.float32, (n,), 128)
+    hout[:] = np.arange(n, dtype=np.float32) * 0.5
+    base = torch.randn(n, device=dev)
+    stats = torch.zeros(8, dtype=torch.int64, device=dev)
+    dflag = torch.zeros(1, dtype=torch.int64, device=dev)
+    s = _lib.stream_ptr()
+    # no job published: out unchanged
+    out = base.clone()
+    print("combine_host: no job", flush=True)
+    _lib.call("mm_combine_host", out.data_ptr(), n, dflag.data_ptr(), hb.data_ptr(0), hb.data_ptr(128), stats.data_ptr(), 10**9, s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    # job 3 published and already done by the host: out += hout
+    dflag.fill_(3)
+    ctrl[1] = 3
+    out = base.clone()
+    print("combine_host: done job", flush=True)
+    _lib.call("mm_combine_host", out.data_ptr(), n, dflag.data_ptr(), hb.data_ptr(0), hb.data_ptr(128), stats.data_ptr(), 10**9, s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base + torch.from_numpy(hout.copy()).to(dev))
+    st = stats.cpu().numpy()
+    assert st[5] == 1 and st[6] == 0
+    # job 4 never answered: 2 ms bounded wait, partial dropped, timeout counted
+    dflag.fill_(4)
+    out = base.clone()
+    print("combine_host: timeout path (2 ms)", flush=True)
+    _lib.call("mm_combine_host", out.data_ptr(), n, dflag.data_ptr(), hb.data_ptr(0), hb.data_ptr(128), stats.data_ptr(), 2_000_000, s)
+    torch.cuda.synchronize()
+    assert torch.equal(out, base)
+    st = stats.cpu().numpy()
+    assert st[6] == 1 and st[5] == 2 and st[4] >= 2_000_000
+
+
+@pytest.mark.parametrize("T,k", [(4, 9), (33, 8)])
+def test_combine_matches_oracle(dev, T, k):
+    import torch
+    from mi355moe import moe
+    rng = np.random.default_rng(T)
+    H, E = 4096, 385
+    Y = rng.normal(0, 1, (T * k, H)).astype(np.float32)
+    ids = rng.integers(0, E, (T, k)).astype(np.int64)
+    ids[0, 1] = -1
+    w = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    out = moe.combine(_t(Y, dev), _t(ids, dev), _t(w, dev), T, k, H, E)
+    torch.cuda.synchronize()
+    wm = np.where((ids >= 0) & (ids < E), w, 0).astype(np.float32)
+    ref = O.combine(np.zeros((T, H), np.float32), np.nan_to_num(Y), wm)
+    assert np.array_equal(out.cpu().numpy(), ref)     # same fp32 fma chain in ascending j
+
+
+@pytest.mark.parametrize("T", [1, 4, 300])
+def test_router_matches_oracle(dev, T):
+    import torch
+    from mi355moe import _lib, workload
+    H, E, k = 4096, 384, 8
+    x = workload.activations(T, H, seed=T)
+    G = np.random.default_rng(5).normal(0, 0.02, (E, H)).astype(np.float32)
+    xb = _t((x.view(np.uint32) >> 16).astype(np.uint16), dev)
+    Gd = _t(G, dev)
+    ids = torch.empty((T, k), dtype=torch.int64, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+    print(f"router T={T}", flush=True)
+    _lib.call("mm_router_topk", xb.data_ptr(), T, H, Gd.data_ptr(), E, k, logits.data_ptr(), ids.data_ptr(), w.data_ptr(),
+              _lib.stream_ptr())
+    torch.cuda.synchronize()
+    rid, rw, rl = O.router(x, G, k)
+    lg = logits.cpu().numpy()
+    assert np.allclose(lg, rl, rtol=0, atol=5e-5)
+    gi = ids.cpu().numpy()
+    for t in range(T):
+        if not np.array_equal(gi[t], rid[t]):
+            # only a near-tie (|gap| below fp32 summation noise) may reorder the selection
+            srt = np.sort(rl[t])[::-1]
+            assert np.min(np.abs(np.diff(srt[: k + 1]))) < 1e-5, t
+        else:
+            assert np.allclose(w.cpu().numpy()[t], rw[t], rtol=1e-5, atol=1e-6)

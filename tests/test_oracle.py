@@ -1,0 +1,292 @@
+"""Pins the CPU oracle: golden vectors from the compiled reference, closed forms, brute force and library
+routines. None of these re-types the oracle's formula; each would fail on a dropped term, a wrong sign,
+index or bit order."""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLD = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def gold(name):
+    return np.load(os.path.join(GOLD, name), allow_pickle=False)
+
+
+def sha(a):
+    import hashlib
+    return hashlib.sha256(np.ascontiguousarray(a).tobytes()).hexdigest()
+
+
+# ------------------------------------------------------------------------------------------------ fp16
+def test_h2f_all_patterns():
+    L = O.lib()
+    bits = np.arange(65536, dtype=np.uint16)
+    ref = bits.view(np.float16).astype(np.float32)
+    got = np.array([L.mmo_h2f(int(b)) for b in bits], dtype=np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan], ref[~nan])
+
+
+def test_f2h_matches_numpy_rne():
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.normal(0, 1, 20000), rng.normal(0, 3e-5, 5000), rng.normal(0, 3e4, 5000),
+        # exact ties between adjacent fp16 values (round half to even)
+        (np.arange(-2048, 2048) + 0.5) * 2.0 ** -10, (np.arange(0, 1024) + 0.5) * 2.0 ** -24,
+        [65504.0, 65519.9, 65520.0, 1e9, -1e9, 0.0, -0.0, 2.0 ** -25, 2.0 ** -26, 6.1e-5],
+    ]).astype(np.float32)
+    got = O.f2h_bits(vals)
+    ref = vals.astype(np.float16).view(np.uint16)
+    assert np.array_equal(got, ref)
+
+
+# ------------------------------------------------------------------------------------------------ format
+def test_perm_structure():
+    p = O.perm()
+    assert sorted(p.tolist()) == list(range(256))            # bijection onto the 16x16 tile
+    for t in range(32):
+        rc = p[t * 8:(t + 1) * 8]
+        rows, cols = rc // 16, rc % 16
+        r0, c0 = (t % 4) * 2, t // 4
+        assert sorted(set(rows.tolist())) == [r0, r0 + 1, r0 + 8, r0 + 9]
+        assert list(cols[:4]) == [c0] * 4 and list(cols[4:]) == [c0 + 8] * 4
+
+
+def test_state_window_single_bit():
+    # A tile with one set stream bit P (MSB-first within little-endian 32-bit words) must appear in exactly
+    # the states i with P in [3i-13, 3i+2] (mod 768), at bit (3i+2-P) of the state.
+    for P in (0, 1, 13, 31, 32, 95, 400, 755, 767):
+        words = np.zeros(24, np.uint32)
+        words[P // 32] = np.uint32(1) << np.uint32(31 - P % 32)
+        tile = words.view(np.uint16)
+        for i in range(256):
+            st = O.state(tile, i)
+            d = (3 * i + 2 - P) % 768
+            assert st == ((1 << d) if d < 16 else 0), (P, i, st)
+
+
+def _weights_closed_form():
+    st = np.arange(65536, dtype=np.uint64)
+    x = (st * np.uint64(0x83DCD12D)) & np.uint64(0xFFFFFFFF)
+    s = sum(((x >> np.uint64(8 * b)) & np.uint64(0xFF)).astype(np.int64) for b in range(4))
+    # KINV = 1774 * 2^-18 (fp16 0x1eee), KBIAS = -1329 * 2^-7 (fp16 0xc931): exact value, one fp16 rounding
+    exact = (1774.0 * (1024 + s) - 1329.0 * 2048) * 2.0 ** -18
+    return exact.astype(np.float16).astype(np.float32)
+
+
+def test_weight_table_closed_form():
+    assert np.float16(np.uint16(0x1eee).view(np.float16)) == np.float16(1774 * 2.0 ** -18)
+    assert np.float16(np.uint16(0xc931).view(np.float16)) == np.float16(-1329 * 2.0 ** -7)
+    tab = O.weight_table()
+    ref = _weights_closed_form()
+    assert np.array_equal(tab, ref)
+    assert tab.min() == np.float32(np.float16(-3.453125)) and tab.max() <= 3.4492
+
+
+def test_dense_matches_reference_golden():
+    g = gold("dense_256x256.npz")
+    tr = O.synth_u16(int(g["seed"]), 0, 256 * 256 * 3 // 16)
+    assert sha(tr) == str(g["trellis_sha256"])
+    W = O.dense(tr, 256, 256)
+    assert np.array_equal(W.astype(np.float16), g["W"])
+
+
+def test_synth_known_value():
+    # splitmix64 with state 0: first output 0xE220A8397B1DCDAF (published test value)
+    w = O.synth_u16(0, 0, 4).astype(np.uint64)
+    v = int(w[0] | (w[1] << np.uint64(16)) | (w[2] << np.uint64(32)) | (w[3] << np.uint64(48)))
+    assert v == 0xE220A8397B1DCDAF
+    a = O.synth_u16(7, 0, 1000)
+    b = O.synth_u16(7, 123, 877)
+    assert np.array_equal(a[123:], b)
+
+
+# ------------------------------------------------------------------------------------------------ transforms
+def test_had128_is_sylvester_hadamard():
+    from scipy.linalg import hadamard
+    Hm = hadamard(128).astype(np.float64)
+    rng = np.random.default_rng(1)
+    for _ in range(5):
+        v = rng.normal(0, 1, 128).astype(np.float32)
+        got = O.had128(v)
+        assert np.allclose(got, Hm @ v.astype(np.float64), rtol=0, atol=1e-4)
+
+
+def test_prep_and_out_block_rounding_points():
+    rng = np.random.default_rng(2)
+    x = rng.normal(0, 1, 128).astype(np.float16).astype(np.float32)
+    suh = np.where(rng.integers(0, 2, 128) == 0, -1.0, 1.0).astype(np.float16)
+    xt = O.prep_block(x, suh)
+    assert np.array_equal(xt, xt.astype(np.float16).astype(np.float32))          # fp16-valued
+    from scipy.linalg import hadamard
+    ref = (hadamard(128) @ (x * suh.astype(np.float32))) * 0.088388347648
+    assert np.allclose(xt, ref, rtol=2e-3, atol=2e-3)
+    y = rng.normal(0, 30, 128).astype(np.float32)
+    svh = np.abs(rng.normal(0, 0.02, 128)).astype(np.float16)
+    yo = O.out_block(y, svh)
+    ref = (hadamard(128) @ y.astype(np.float16).astype(np.float64)) * 0.088388347648 * svh.astype(np.float64)
+    assert np.array_equal(yo, yo.astype(np.float16).astype(np.float32))
+    assert np.allclose(yo, ref, rtol=2e-3, atol=1e-3)
+
+
+def test_act_clamp():
+    assert O.act(1.0, 2.0, 0.0) == pytest.approx(2.0 / (1 + np.exp(-1.0)), rel=1e-6)
+    assert O.act(50.0, 30.0, 10.0) == pytest.approx(10.0 * 10.0)          # silu clamped above, u clamped
+    assert O.act(-50.0, -30.0, 10.0) == pytest.approx((-50.0 / (1 + np.exp(50.0))) * -10.0, rel=1e-5)
+
+
+# ------------------------------------------------------------------------------------------------ expert
+@pytest.mark.parametrize("j", [0, 1])
+def test_expert_matches_reference_golden(j):
+    g = gold("expert_4096x2048.npz")
+    H, I = int(g["H"]), int(g["I"])
+    tg, tu, td = O.synth_expert_trellis(int(g["layer_seed"]), int(g[f"e{j}"]), H, I)
+    assert sha(np.concatenate([tg.ravel(), tu.ravel(), td.ravel()])) == str(g[f"trellis_sha256_{j}"])
+    sc = [g[f"{n}{j}"] for n in ("suh_g", "svh_g", "suh_u", "svh_u", "suh_d", "svh_d")]
+    DE = O.DenseExpert(tg, tu, td, *sc, H, I)
+    for lim in (10, 0):
+        y = DE(g[f"x{j}"], float(lim))[0]
+        assert np.array_equal(y, g[f"y{j}_lim{lim}"]), lim
+
+
+def test_cpu_tier_exact_mode_vs_oracle():
+    g = gold("tier_t4.npz")
+    H, I, E = int(g["H"]), int(g["I"]), int(g["E"])
+    out = np.zeros((4, H), np.float64)
+    for e in range(E):
+        sel = g["exp"] == e
+        if not sel.any():
+            continue
+        tr = O.synth_expert_trellis(int(g["layer_seed"]), e, H, I)
+        DE = O.DenseExpert(*tr, *[g[k][e] for k in ("suh_g", "svh_g", "suh_u", "svh_u", "suh_d", "svh_d")], H, I)
+        y = DE(g["x"][g["tok"][sel]], 10.0)
+        for row, t, w in zip(y, g["tok"][sel], g["w"][sel]):
+            out[t] += np.float64(w) * row
+    mx, mean = O.tolerance_metrics(g["out_mode1"], out)
+    assert mx <= 2e-2 and mean <= 2e-3, (mx, mean)
+    # the production modes (AFFINE, I16) are reported, not gated: they must stay in the same ballpark
+    for mode in (0, 2):
+        mx, mean = O.tolerance_metrics(g[f"out_mode{mode}"], out)
+        assert mean < 2e-2, (mode, mean)
+
+
+# ------------------------------------------------------------------------------------------------ split
+POL = np.array([0.58, 0.03, 0.11, 0.20, 0.35, 384, -1, 0, 0], np.float32)
+
+
+def _case(rng, T=4, k=8, E=384, frac_res=0.4):
+    sel = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
+    w = rng.uniform(0.01, 1.0, (T, k)).astype(np.float32)
+    touched = np.unique(sel)
+    slotof = np.full(E, -1, np.int32)
+    res = rng.choice(touched, int(frac_res * touched.size), replace=False)
+    slotof[res] = np.arange(res.size)
+    z = rng.normal(0, 1, (T, 4096)).astype(np.float16)
+    return sel, w, z, slotof
+
+
+def _brute_best(cnt, hits, misses, p):
+    nh, nm = len(hits), len(misses)
+    if p[6] >= 0:
+        return min(int(p[6]), nm)
+    best, bt = 0, None
+    for k in range(0, min(int(p[5]), nm) + 1):
+        c = sum(p[3] * (1.0 + p[4] * (cnt[m] - 1)) for m in misses[:k])
+        gpu = p[1] * (nh + nm - k) + p[0] * (nm - k)
+        tt = max(gpu, p[2] + c if k else 0.0)
+        if bt is None or tt < bt - 1e-6:
+            best, bt = k, tt
+    return best
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_split_invariants_and_bruteforce(seed):
+    rng = np.random.default_rng(seed)
+    sel, w, z, slotof = _case(rng)
+    w[0, 1] = 0.0                                              # zero-weight route: not counted, never a pick
+    score = np.zeros(384, np.float32) if seed % 2 == 0 else rng.permutation(384).astype(np.float32)
+    pol = POL.copy()
+    if seed == 5:
+        pol[2] = 0.01                                          # cheap CPU: many picks
+    r = O.split(sel, w, z, 384, slotof, score, pol, seqc=10, li=3)
+    flat, wf = sel.ravel(), w.ravel()
+    cnt = np.bincount(flat[wf != 0], minlength=384)
+    touched = np.nonzero(cnt)[0]
+    assert np.array_equal(np.sort(np.concatenate([r["hits"], r["misses"]])), touched)
+    assert np.array_equal(r["hits"], touched[slotof[touched] >= 0])
+    exp_miss = sorted(touched[slotof[touched] < 0].tolist(), key=lambda e: (score[e], e))
+    assert r["misses"].tolist() == exp_miss
+    best = _brute_best(cnt, r["hits"].tolist(), exp_miss, pol.astype(np.float64))
+    cpu = set(exp_miss[:best])
+    assert int(r["stats"][2]) == best and int(r["stats"][0]) == len(r["hits"]) and int(r["stats"][1]) == len(exp_miss)
+    assert np.array_equal(r["counts"], cnt.astype(np.int32))
+    masked = np.array([e in cpu for e in flat])
+    assert np.array_equal(r["sel_out"], np.where(masked, -1, flat))
+    assert np.array_equal(r["w_out"], np.where(masked, 0.0, wf).astype(np.float32))
+    picks = [(s // 8, int(flat[s]), float(wf[s])) for s in range(flat.size) if flat[s] in cpu and wf[s] != 0]
+    if best > 0:
+        assert int(r["dflag"][0]) == 11 and int(r["ctrl"][0]) == 11 and int(r["ctrl"][4]) == len(picks)
+        hp = r["hpicks"][: 3 * len(picks)].reshape(-1, 3)
+        assert [(a, b, np.int32(c).view(np.float32).item()) for a, b, c in hp] == picks
+        assert np.array_equal(r["hx"].view(np.float16).reshape(z.shape), z)
+        assert int(r["ctrl"][2]) == 3 and int(r["ctrl"][3]) == 4
+    else:
+        assert int(r["dflag"][0]) == 0 and int(r["seqc"][0]) == 10
+
+
+def test_split_force_and_handshake():
+    rng = np.random.default_rng(11)
+    sel, w, z, slotof = _case(rng)
+    pol = POL.copy()
+    pol[6] = 3
+    r = O.split(sel, w, z, 384, slotof, np.zeros(384, np.float32), pol)
+    assert int(r["stats"][2]) == min(3, len(r["misses"]))
+    pol = POL.copy()
+    pol[6] = 0
+    pol[7] = 1                                                   # publish even an empty job
+    r = O.split(sel, w, z, 384, slotof, np.zeros(384, np.float32), pol)
+    assert int(r["dflag"][0]) == 1 and int(r["ctrl"][4]) == 0
+
+
+# ------------------------------------------------------------------------------------------------ permute / combine
+@pytest.mark.parametrize("n,E", [(0, 8), (1, 8), (36, 385), (5000, 384), (20000, 1024)])
+def test_permute_is_stable_counting_sort(n, E):
+    rng = np.random.default_rng(n)
+    ids = rng.integers(-2, E + 3, n).astype(np.int64)           # includes out-of-range ids -> sentinel
+    w = rng.normal(0, 1, n).astype(np.float32)
+    counts, offsets, order, tok, ws = O.permute(ids, w, 8, E)
+    b = np.where((ids >= 0) & (ids < E), ids, E)
+    assert np.array_equal(counts, np.bincount(b, minlength=E + 1))
+    assert np.array_equal(order, np.argsort(b, kind="stable"))
+    assert np.array_equal(offsets, np.concatenate([[0], np.cumsum(counts)]))
+    assert np.array_equal(tok, order // 8) and np.array_equal(ws, w[order])
+
+
+def test_combine_closed_form():
+    rng = np.random.default_rng(3)
+    T, k, H = 5, 9, 256
+    Y = rng.normal(0, 1, (T * k, H)).astype(np.float32)
+    w = rng.uniform(0, 1, (T, k)).astype(np.float32)
+    base = rng.normal(0, 1, (T, H)).astype(np.float32)
+    hout = rng.normal(0, 1, (T, H)).astype(np.float32)
+    got = O.combine(base, Y, w, hout)
+    ref = base.astype(np.float64) + np.einsum("tk,tkh->th", w.astype(np.float64), Y.reshape(T, k, H).astype(np.float64)) + hout
+    assert np.allclose(got, ref, rtol=1e-5, atol=1e-5)
+
+
+def test_router_matches_library_topk_softmax():
+    import torch
+    rng = np.random.default_rng(4)
+    T, H, E, k = 6, 512, 384, 8
+    x = rng.normal(0, 1, (T, H)).astype(np.float32)
+    G = rng.normal(0, 0.02, (E, H)).astype(np.float32)
+    ids, w, logits = O.router(x, G, k)
+    lt = torch.from_numpy(x).double() @ torch.from_numpy(G).double().T
+    top = torch.topk(lt, k, dim=1)
+    assert np.array_equal(ids, top.indices.numpy())
+    assert np.allclose(w, torch.softmax(top.values, dim=1).numpy(), rtol=1e-6, atol=1e-7)
+    assert np.allclose(logits, lt.float().numpy(), rtol=1e-5, atol=1e-6)
