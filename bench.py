@@ -1,0 +1,238 @@
+#!/usr/bin/env python3
+"""Benchmark: a decode step through 40 routed-expert MoE layers on one MI355X.
+
+Workload (one "step"): T = 4 tokens through 40 MoE layers of H 4096 / I 2048, 384 routed experts (top-8) plus
+1 shared expert per layer, all EXL3 3.0 bpw and resident in HBM (40 x 385 experts, 146 GB). Routing per layer
+is Zipf(1.1) over a seeded permutation (seed 2000 + layer); weights are seeded synthetic (1000 + layer); the
+input is bf16 N(0, 1) and each layer's output is rescaled to unit RMS (bf16) before the next layer. Each layer
+runs routing prep, the fused decode expert kernels (trellis decode + GEMV + SwiGLU + Hadamard transforms) and
+the fixed-order combine; the 40-layer step is replayed as one HIP graph.
+
+Prints one JSON line. `value` is MoE tok/s = T / step time. `roofline` is measured live on the dominant kernel
+(the gate/up decode GEMV) with HIP events on its stream; `cpu_baseline` times the reference's own CPU expert tier
+(compiled from its sources into oracle/_ref) on this host for one layer of the same step.
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "dsv41-flash-offload_amd"))
+
+METRIC = "MoE tok/s (decode T=1/4, prefill 16k) + HBM GB/s & MFMA util vs peak"
+HBM_PEAK_GBS = 8000.0
+BYTES_TRELLIS = 3145728             # one 4096 x 2048 matrix at 3 bpw
+BYTES_GU = 2 * BYTES_TRELLIS + (2 * 4096 + 2 * 2048) * 2 + 2048 * 2   # gate+up trellis, suh13, svh13, suh2
+BYTES_D = BYTES_TRELLIS + 4096 * 2                                  # down trellis, svh2
+BYTES_EXPERT = BYTES_GU + BYTES_D                                   # 9,474,048
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(routes, T, H, I, E, layer_seed, budget_s=15.0):
+    """Time the reference CPU tier (ft_core.h moe_forward, auto mode) on one layer of the step."""
+    import numpy as np
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    from mi355moe.store import synth_scales
+    ref = os.path.join(ROOT, "oracle", "_ref", "libftref.so")
+    if not os.path.exists(ref):
+        return None
+    R = ctypes.CDLL(ref)
+    ids, w = routes
+    experts = sorted(set(ids.ravel().tolist()))
+    keep = []
+    ptrs = np.zeros((E + 1, 3), np.int64)
+    for e in experts:
+        mats = []
+        for m in O.synth_expert_trellis(layer_seed, e, H, I):
+            b = np.zeros(m.size + 2048, np.uint16)      # tail pad: the AVX2 decode reads past a tile's end
+            b[: m.size] = m.ravel()
+            mats.append(b)
+        keep.append(mats)
+        ptrs[e] = [mm.ctypes.data for mm in mats]
+    sc = synth_scales(layer_seed, E + 1, H, I)
+    arrs = [np.ascontiguousarray(a) for a in (sc["w13_suh"][:, 0], sc["w13_svh"][:, 0], sc["w13_suh"][:, 1],
+                                               sc["w13_svh"][:, 1], sc["w2_suh"], sc["w2_svh"])]
+    P = lambda a: ctypes.c_void_p(a.ctypes.data)
+    cpus = sorted(os.sched_getaffinity(0))[:16]
+    carr = (ctypes.c_int * len(cpus))(*cpus)
+    R.ref_pool_start(len(cpus), carr, len(cpus))
+    R.ref_set_limit(ctypes.c_float(10.0))
+    R.ref_add_layer(0, E + 1, H, I, P(ptrs), *[P(a.view(np.uint16)) for a in arrs])
+    x = np.random.default_rng(7).normal(0, 1, (T, H)).astype(np.float16).astype(np.float32)
+    tok = np.repeat(np.arange(T, dtype=np.int32), ids.shape[1])
+    exp = ids.ravel().astype(np.int32)
+    wt = w.ravel().astype(np.float32)
+    out = np.zeros((T, H), np.float32)
+    for _ in range(3):
+        mode = R.ref_moe_forward(0, P(x), T, P(tok), P(exp), P(wt), tok.size, P(out), -1)
+    ts = []
+    t_end = time.perf_counter() + budget_s
+    while len(ts) < 300 and time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        R.ref_moe_forward(0, P(x), T, P(tok), P(exp), P(wt), tok.size, P(out), -1)
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    p50 = ts[len(ts) // 2]
+    return {"p50_layer_ms": p50 * 1e3, "p90_layer_ms": ts[int(len(ts) * 0.9)] * 1e3, "calls": len(ts), "cores": len(cpus),
+            "mode": {0: "AFFINE", 1: "EXACT", 2: "I16"}.get(mode, str(mode)), "experts": len(experts)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--layers", type=int, default=40)
+    ap.add_argument("--tokens", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(f"bench.py: this build measures one MI355X (got --gpus {args.gpus}, WORLD_SIZE {world}); the multi-GPU "
+              "expert-parallel design is documented but not built, so N > 1 is not run.", flush=True)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    from mi355moe import _lib, workload
+    from mi355moe.moe import DecodeRunner
+    from mi355moe.store import ExpertStore
+
+    dev = torch.device("cuda", 0)
+    H, I, E, K_TOP, T, L = 4096, 2048, 384, 8, args.tokens, args.layers
+    t0 = time.time()
+    stores = []
+    for l in range(L):
+        stores.append(ExpertStore(E + 1, H, I, device=dev, limit=10.0).synthesize(1000 + l))
+        if l % 10 == 9 or l == L - 1:
+            torch.cuda.synchronize()
+            log(f"stores: {l + 1}/{L} layers resident ({(l + 1) * (E + 1) * BYTES_EXPERT / 1e9:.1f} GB) {time.time() - t0:.1f}s")
+    routes = [workload.zipf_routing(T, K_TOP, E, seed=2000 + l) for l in range(L)]
+    ids_ext = [np.concatenate([r[0], np.full((T, 1), E, np.int64)], 1) for r in routes]
+    w_ext = [np.concatenate([r[1], np.ones((T, 1), np.float32)], 1) for r in routes]
+    uniq = [len(np.unique(r[0])) for r in routes]
+    ids_d = [torch.from_numpy(a).to(dev) for a in ids_ext]
+    w_d = [torch.from_numpy(a).to(dev) for a in w_ext]
+    R = DecodeRunner(E, H, I, T, K_TOP, device=dev)
+    x0 = torch.from_numpy(workload.activations(T, H, seed=7)).to(dev)
+    outs = [torch.empty((T, H), dtype=torch.float32, device=dev) for _ in range(2)]
+    L_ = _lib.load()
+
+    def layer(l, phase_events=None):
+        # expert kernels read R.x16; combine_prepare writes this layer's output and the next layer's input
+        if phase_events is None:
+            R.experts(stores[l], ids=ids_d[l], phases=3)
+        else:
+            e0, e1, e2 = phase_events
+            e0.record()
+            R.experts(stores[l], ids=ids_d[l], phases=1)
+            e1.record()
+            R.experts(stores[l], ids=ids_d[l], phases=2)
+            e2.record()
+        return R.combine_prepare(ids_d[l], w_d[l], out=outs[l % 2], x16_next=R.x16, rescale=True)
+
+    def step():
+        _lib.check(L_.mm_prepare_input(x0.data_ptr(), T, H, 1, None, R.x16.data_ptr(), _lib.stream_ptr()), "prepare")
+        src = x0
+        for l in range(L):
+            src = layer(l)
+        return src
+
+    # eager warm-up, then capture the 40-layer step as one graph
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        final = step()
+    torch.cuda.synchronize()
+    log("graph captured")
+
+    for _ in range(args.warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_start = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    ms_step = ev0.elapsed_time(ev1) / args.steps
+    ms_wall = wall * 1e3 / args.steps
+    out_rms = float(final.float().pow(2).mean().sqrt())
+    log(f"step {ms_step:.3f} ms (wall {ms_wall:.3f} ms), final output rms {out_rms:.4f}")
+
+    # live roofline of the dominant kernel (gate/up decode GEMV), HIP events on its stream
+    reps = 3
+    evs = [[tuple(torch.cuda.Event(enable_timing=True) for _ in range(3)) for _ in range(L)] for _ in range(reps)]
+    for r in range(reps):
+        _lib.check(L_.mm_prepare_input(x0.data_ptr(), T, H, 1, None, R.x16.data_ptr(), _lib.stream_ptr()), "prepare")
+        for l in range(L):
+            layer(l, evs[r][l])
+    torch.cuda.synchronize()
+    t_gu = np.array([[evs[r][l][0].elapsed_time(evs[r][l][1]) for l in range(L)] for r in range(reps)]).mean(0)
+    t_d = np.array([[evs[r][l][1].elapsed_time(evs[r][l][2]) for l in range(L)] for r in range(reps)]).mean(0)
+    bytes_gu = np.array([(u + 1) * BYTES_GU for u in uniq], np.float64)
+    bytes_d = np.array([(u + 1) * BYTES_D for u in uniq], np.float64)
+    gu_gbs = bytes_gu.sum() / (t_gu.sum() * 1e-3) / 1e9
+    d_gbs = bytes_d.sum() / (t_d.sum() * 1e-3) / 1e9
+    step_bytes = float(sum((u + 1) * BYTES_EXPERT for u in uniq))
+    step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
+    log(f"gate/up kernel: {t_gu.mean() * 1e3:.1f} us avg, {gu_gbs:.0f} GB/s; down kernel: {t_d.mean() * 1e3:.1f} us avg, "
+        f"{d_gbs:.0f} GB/s; step {step_gbs:.0f} GB/s")
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        log("cpu baseline: reference CPU tier, one layer")
+        cpu = cpu_baseline((ids_ext[0], w_ext[0]), T, H, I, E, 1000)
+
+    res = {
+        "metric": METRIC,
+        "value": round(T / (ms_step * 1e-3), 2),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic: seeded EXL3 3-bpw trellis + fp16 scales, Zipf(1.1) routing, bf16 N(0,1) input",
+        "config": {"workload": f"decode step through {L} MoE layers, T={T} tokens, H=4096, I=2048, 384 routed experts "
+                               "top-8 + 1 shared, EXL3 3.0 bpw, all experts HBM-resident",
+                   "layers": L, "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": K_TOP,
+                   "shared_experts": 1, "mean_distinct_experts_per_layer": round(float(np.mean(uniq)), 2)},
+        "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "k_expert_gemv<0,*> (gate/up decode GEMV)",
+                     "avg_launch_us": round(float(t_gu.mean()) * 1e3, 2),
+                     "bytes_per_launch": round(float(bytes_gu.mean()), 1)},
+        "step_hbm": {"bytes_per_step": step_bytes, "achieved_gbs": round(step_gbs, 1),
+                     "frac_of_peak": round(step_gbs / HBM_PEAK_GBS, 4),
+                     "down_kernel_gbs": round(d_gbs, 1), "down_avg_launch_us": round(float(t_d.mean()) * 1e3, 2)},
+        "ms_per_step_wall": round(ms_wall, 4),
+    }
+    if cpu is not None:
+        res["cpu_baseline"] = {"value": round(T / (L * cpu["p50_layer_ms"] * 1e-3), 3), "unit": "tok/s",
+                               "cores": cpu["cores"], "kind": "reference",
+                               "sample": f"one layer of the same step ({cpu['experts']} experts, T={T}) x {cpu['calls']} "
+                                         f"calls, reference CPU tier mode {cpu['mode']}, p50 {cpu['p50_layer_ms']:.3f} ms "
+                                         f"(p90 {cpu['p90_layer_ms']:.3f}) per layer, scaled to {L} layers"}
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

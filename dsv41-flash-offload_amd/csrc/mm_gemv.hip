@@ -1,12 +1,16 @@
 // Decode expert path: EXL3 3-bpw trellis decode fused into a multi-token GEMV on gfx950.
 //
-// Work unit = (active expert, 128-column output block, 1024-row K part). Each workgroup of 4 waves streams
-// its unit's tiles straight from HBM with coalesced 12-byte loads: a wave covers one tile row of the
-// block (8 tiles x 96 B = 768 B contiguous), 8 lanes per tile, and each lane decodes 32 consecutive trellis
-// states = 16 rows x 2 columns of its tile. The input Hadamard transform of the unit's K part is computed
-// in the prologue into LDS; partial sums of the K parts go to a workspace and the last workgroup of a unit
-// (atomic ticket) adds them in fixed order and runs the epilogue (output transform, SwiGLU, down-input
-// transform / output transform). Results are deterministic.
+// Work unit = (active expert, 128-column output block), full K. A workgroup of 8 waves streams its unit's tiles
+// straight from HBM: a wave covers one tile row of the block per step (8 tiles x 96 B = 768 B contiguous, one
+// 12-byte load per lane, 4 tile rows in flight), 8 lanes per tile, each lane decoding 32 consecutive trellis
+// states = 16 input rows x 2 output columns of its tile. Waves split K; their partial sums meet in LDS in fixed
+// order and the same workgroup runs the epilogue (output Hadamard transform, SwiGLU, down-input transform or
+// the down output transform). No cross-workgroup communication: every launch is self-contained and the
+// results are deterministic.
+//
+// Routing: for decode-sized calls the workgroup finds its expert and that expert's routes directly from the
+// route ids (n <= 1024): the a-th active expert in ascending id, its routes in ascending route index -- the
+// same stable order as the permutation. Larger calls pass the permutation (offsets/order/active).
 //
 // Numerics follow the reference's EXACT expert (kernels/cpu_avx2/ft_core.h:977-1011): fp16 weights
 // fp16(fma(1024 + bytesum, KINV, KBIAS)) (one rounding, v_pk_fma_f16), fp16 transformed activations,
@@ -15,14 +19,13 @@
 
 namespace mm {
 
-constexpr int GV_WAVES = 4;
+constexpr int GV_WAVES = 8;
 constexpr int GV_THREADS = 64 * GV_WAVES;
 constexpr int GV_COLS = 128;         // output columns per unit (8 tiles)
-constexpr int GV_KPART = 1024;       // input rows per unit (64 tile rows)
 constexpr int GV_MAX_ROWS = 256;     // routes per expert on this path
+constexpr int GV_ROUTE_MAX = 1024;   // in-kernel routing limit (routes per call)
+constexpr int GV_PF = 4;             // tile rows in flight per wave
 
-// Trellis words are read through the global address space (global_load, not flat_load): the pointer tables
-// hold plain device addresses.
 typedef const __attribute__((address_space(1))) uint32_t gu32;
 
 struct GemvArgs
@@ -33,313 +36,393 @@ struct GemvArgs
     const uint16_t* svh13;    // [E][2][I]
     const uint16_t* suh2;     // [E][I]
     const uint16_t* svh2;     // [E][H]
-    const uint16_t* xin;      // mode 0: x fp16 [T][H]; mode 1: xd fp16 [n][I]
-    const int32_t* offsets;   // [E+2]
+    const uint16_t* xin;      // mode 0: x fp16 [T][H]; mode 1: xd fp16 [n][I] (flat route order)
+    const int64_t* ids;       // [n] route expert ids (in-kernel routing)
+    const int32_t* offsets;   // [E+2] or null (then in-kernel routing)
     const int32_t* order;     // [n]
     const int32_t* active;    // [E]
     const int32_t* nactive;   // [1]
-    float* part;              // [kparts][n][nmat][N]
-    int32_t* tickets;         // [max_active * ncb * maxchunk]
-    uint16_t* xd;             // mode 0 output: [n][I] fp16
-    float* Y;                 // mode 1 output: [n][H] fp32 at flat route index
+    uint16_t* xd;             // mode 0 output: [n][I] fp16, flat route order
+    float* Y;                 // mode 1 output: [n][H] fp32, flat route order
     int H, I, E, n, topk;
-    int K, N, ncb, kparts, maxchunk, max_active;
+    int K, N, ncb, max_active;
     float limit;
 };
 
-__device__ __forceinline__ uint32_t wbits(uint32_t v)
-{
-    // (1024 + bytesum(state * MUL1)) as fp16 bits: 1024 is 0x6400 and the byte sum (<= 1020) fills the
-    // mantissa exactly, so v_sad_u8 with 0x6400 as accumulator yields the fp16 operand of the hfma.
-    const uint32_t p = (v & 0xffffu) * MUL1;
-    return __builtin_amdgcn_sad_u8(p, 0u, 0x6400u);
-}
-
-// Decode one lane's 32 states of a tile from the 128-bit window d0:d1:d2:d3 (d0 most significant: tile
-// dwords 3c-1 .. 3c+2). State m has its LSB at bit 93 - 3m of the window. Returns 16 packed fp16 weight
-// pairs: w[4q + 0] rows (2q, 2q+1) col c; w[4q + 1] rows (2q+8, 2q+9) col c; w[4q + 2], w[4q + 3] the
-// same rows for col c + 8.
-__device__ __forceinline__ void decode_lane(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, half2_t* w)
+// One lane's share of a tile row: 32 trellis states -> 32 fp16 weights -> dot products with the transformed
+// inputs of nr routes.
+// Window d0:d1:d2:d3 = tile dwords 3c-1 .. 3c+2 (d0 most significant); state m (stream index 32c + m) has its
+// LSB at bit 93 - 3m. Every 16-bit field lies inside one of d1..d3 or one of the dwords straddling their
+// boundaries (bits 16..47, 48..79, 80..111 of the window), so each state is one v_bfe_u32.
+// The (1024 + bytesum) fp16 operands of a pair are produced packed by v_sad_u8 / v_sad_hi_u8 with 0x6400 in
+// both halves of the accumulator, then one v_pk_fma_f16 applies KINV, KBIAS with a single rounding.
+// States 8q+2j, 8q+2j+1 (j = 0..3) hold rows (2q, 2q+1) for j even and (2q+8, 2q+9) for j odd, of column c
+// (j < 2) or c + 8 (j >= 2) (PERM, ft_core.h:48-61); X[r][d] is the fp16 input pair of rows (2d, 2d+1) of
+// route r, so pair j meets X[r][q + 4 * (j & 1)] and accumulates into column j >> 1.
+template <int MT>
+__device__ __forceinline__ void decode_dot(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
+                                          const uint32_t (*X)[8], int nr, float (*acc)[MT])
 {
     const half2_t kinv = { __builtin_bit_cast(_Float16, KINV_BITS), __builtin_bit_cast(_Float16, KINV_BITS) };
     const half2_t kbias = { __builtin_bit_cast(_Float16, KBIAS_BITS), __builtin_bit_cast(_Float16, KBIAS_BITS) };
-    uint32_t h[32];
-#pragma unroll
-    for (int m = 0; m < 32; ++m)
-    {
-        const int s = 93 - 3 * m;
-        const int q = s >> 5, r = s & 31;
-        const uint32_t lo = q == 0 ? d3 : (q == 1 ? d2 : d1);
-        const uint32_t hi = q == 0 ? d2 : (q == 1 ? d1 : d0);
-        const uint32_t v = r == 0 ? lo : __builtin_amdgcn_alignbit(hi, lo, r);
-        h[m] = wbits(v);
-    }
+    const uint32_t mid[3] = { __builtin_amdgcn_alignbit(d2, d3, 16), __builtin_amdgcn_alignbit(d1, d2, 16),
+                              __builtin_amdgcn_alignbit(d0, d1, 16) };   // window bits 16.., 48.., 80..
+    const uint32_t dw[3] = { d3, d2, d1 };                              // window bits 0.., 32.., 64..
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
         {
-            const uint32_t pk = h[8 * q + 2 * j] | (h[8 * q + 2 * j + 1] << 16);
-            // j = 0: states 8q+0,1 (col c, rows 2q, 2q+1); j = 1: 8q+2,3 (col c, rows 2q+8, 2q+9);
-            // j = 2: 8q+4,5 (col c+8, rows 2q, 2q+1); j = 3: 8q+6,7 (col c+8, rows 2q+8, 2q+9)
-            w[4 * q + j] = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, pk), kinv, kbias);
+            uint32_t p[2];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+            {
+                const int m = 8 * q + 2 * j + h;
+                const int sft = 93 - 3 * m;
+                const uint32_t st = (sft & 31) <= 16 ? __builtin_amdgcn_ubfe(dw[sft >> 5], sft & 31, 16)
+                                                     : __builtin_amdgcn_ubfe(mid[(sft - 16) >> 5], (sft - 16) & 31, 16);
+                p[h] = st * MUL1;
+            }
+            const uint32_t lo = __builtin_amdgcn_sad_u8(p[0], 0u, 0x64006400u);
+            const uint32_t pk = __builtin_amdgcn_sad_hi_u8(p[1], 0u, lo);
+            const half2_t wv = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, pk), kinv, kbias);
+#pragma unroll
+            for (int r = 0; r < MT; ++r)
+            {
+                if (r >= nr) break;
+                acc[j >> 1][r] = __builtin_amdgcn_fdot2(wv, __builtin_bit_cast(half2_t, X[r][q + 4 * (j & 1)]), acc[j >> 1][r], false);
+            }
         }
 }
 
+__device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    int incl = v;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1)
+    {
+        const int o = __shfl_up(incl, d, 64);
+        if (lane >= d) incl += o;
+    }
+    __syncthreads();
+    if (lane == 63) tmp[wave] = incl;
+    __syncthreads();
+    int before = 0, all = 0;
+    for (int w = 0; w < nw; ++w)
+    {
+        const int s = tmp[w];
+        if (w < wave) before += s;
+        all += s;
+    }
+    *total = all;
+    return before + incl - v;
+}
+
 template <int MODE, int MT>
-__global__ __launch_bounds__(GV_THREADS) void k_expert_gemv(GemvArgs a)
+__global__ __launch_bounds__(GV_THREADS, MT >= 8 ? 2 : 4) void k_expert_gemv(GemvArgs a)
 {
     constexpr int NMAT = MODE == 0 ? 2 : 1;
-    // LDS: transformed inputs [NMAT][MT][KPART] fp16, reused as the cross-wave reduction buffer
-    // [GV_WAVES][NMAT][MT][GV_COLS] fp32 (same size: KPART * 2 B = GV_WAVES * GV_COLS * 4 B).
-    __shared__ __align__(16) uint32_t lds[NMAT * MT * GV_KPART / 2];
-    __shared__ int s_last;
-    static_assert(GV_KPART * 2 == GV_WAVES * GV_COLS * 4, "LDS reuse");
+    constexpr int WPM = GV_WAVES / NMAT;          // waves per matrix: gate on waves 0..3, up on 4..7
+    extern __shared__ __align__(16) uint32_t lds[];   // transformed inputs, then the cross-wave reduction
+    __shared__ uint32_t s_bm[32];
+    __shared__ int s_tmp[16];
+    __shared__ int s_e, s_cnt;
+    __shared__ int s_rows[GV_MAX_ROWS];
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int b = blockIdx.x;
-    const int xcd = b & 7, slot = b >> 3;
-    const int kq = slot % a.kparts;
-    const int g = (slot / a.kparts) * 8 + xcd;          // all K parts of a unit on one XCD
-    const int a_idx = g / a.ncb, cb = g % a.ncb;
-    if (a_idx >= a.max_active || a_idx >= a.nactive[0]) return;
-    const int e = a.active[a_idx];
-    const int row0 = a.offsets[e];
-    const int cnt = a.offsets[e + 1] - row0;
-    const int k0 = kq * GV_KPART;
-    const int klen = min(GV_KPART, a.K - k0);
-    const int ntr = klen / 16;                           // tile rows in this K part
-    const int NT = a.N / 16;                             // tiles per tile row
+    const int a_idx = blockIdx.x / a.ncb, cb = blockIdx.x % a.ncb;
+    if (a_idx >= a.max_active) return;
+
+    // ---- routing: this unit's expert and its routes (flat route indices, ascending)
+    if (a.offsets)
+    {
+        if (threadIdx.x == 0)
+        {
+            const int na = a.nactive[0];
+            s_e = a_idx < na ? a.active[a_idx] : -1;
+            s_cnt = s_e >= 0 ? min(GV_MAX_ROWS, a.offsets[s_e + 1] - a.offsets[s_e]) : 0;
+        }
+        __syncthreads();
+        if (s_e < 0) return;
+        for (int r = threadIdx.x; r < s_cnt; r += GV_THREADS) s_rows[r] = a.order[a.offsets[s_e] + r];
+    }
+    else
+    {
+        if (threadIdx.x < 32) s_bm[threadIdx.x] = 0;
+        __syncthreads();
+        for (int s = threadIdx.x; s < a.n; s += GV_THREADS)
+        {
+            const int64_t e = a.ids[s];
+            if (e >= 0 && e < a.E) atomicOr(&s_bm[e >> 5], 1u << (e & 31));
+        }
+        __syncthreads();
+        if (wave == 0)
+        {
+            const int c = lane < 32 ? __popc(s_bm[lane]) : 0;
+            int incl = c;
+#pragma unroll
+            for (int d = 1; d < 32; d <<= 1)
+            {
+                const int o = __shfl_up(incl, d, 64);
+                if (lane >= d) incl += o;
+            }
+            // the word holding the a_idx-th set bit (0-based)
+            const bool here = lane < 32 && a_idx >= incl - c && a_idx < incl;
+            if (lane == 0) s_e = -1;
+            if (here)
+            {
+                uint32_t bits = s_bm[lane];
+                for (int k = a_idx - (incl - c); k > 0; --k) bits &= bits - 1;
+                s_e = lane * 32 + __ffs(bits) - 1;
+            }
+        }
+        __syncthreads();
+        if (s_e < 0) return;
+        const int e = s_e;
+        int base = 0;
+        for (int s0 = 0; s0 < a.n; s0 += GV_THREADS)
+        {
+            const int s = s0 + threadIdx.x;
+            const bool f = s < a.n && a.ids[s] == e;
+            int tot;
+            const int pos = block_excl_scan(f ? 1 : 0, s_tmp, &tot);
+            if (f && base + pos < GV_MAX_ROWS) s_rows[base + pos] = s;
+            base += tot;
+        }
+        if (threadIdx.x == 0) s_cnt = min(base, GV_MAX_ROWS);
+    }
+    __syncthreads();
+    const int e = s_e, cnt = s_cnt;
+
+    const int K = a.K, KT = K / 16, NT = a.N / 16;
     const int tau = lane >> 3, cp = lane & 7;
     const int src_lane = cp == 0 ? lane + 7 : lane - 1;
+    const int mw = wave / WPM, kw = wave % WPM;   // this wave's matrix and its K slot
+    const int64_t* wtab = (NMAT == 2 && mw == 1) ? a.wptr1 : a.wptr0;
+    gu32* wbase = reinterpret_cast<gu32*>((uintptr_t)wtab[e]) + (size_t)(cb * 8 + tau) * 24 + 3 * cp;
+    const size_t row_stride = (size_t)NT * 24;   // dwords between tile rows
+    const int xrow = K / 2;                       // dwords per transformed input row in LDS
 
-    gu32* wbase[NMAT];
-    wbase[0] = reinterpret_cast<gu32*>((uintptr_t)a.wptr0[e]);
-    if constexpr (NMAT == 2) wbase[NMAT - 1] = reinterpret_cast<gu32*>((uintptr_t)a.wptr1[e]);
-
-    for (int chunk = 0; chunk * MT < cnt && chunk < a.maxchunk; ++chunk)
+    for (int r0 = 0; r0 < cnt; r0 += MT)
     {
-        const int r0 = chunk * MT, nr = min(MT, cnt - r0);
-        __syncthreads();   // LDS reuse across chunks
-        // ---- prologue: transformed inputs of this K part
+        const int nr = min(MT, cnt - r0);
+        __syncthreads();
+        // ---- prologue: transformed inputs (fp16) for all K, rows r0 .. r0+nr-1
         uint16_t* xt = reinterpret_cast<uint16_t*>(lds);
         if constexpr (MODE == 0)
         {
-            const int nblk = klen / 128;
-            for (int item = wave; item < NMAT * MT * nblk; item += GV_WAVES)
+            const int nblk = K / 128;
+            const int items = NMAT * nr * nblk;
+            for (int it0 = wave; it0 < items; it0 += 4 * GV_WAVES)
             {
-                const int m = item / (MT * nblk), r = (item / nblk) % MT, blk = item % nblk;
-                uint16_t* dst = xt + ((size_t)m * MT + r) * GV_KPART + blk * 128;
-                if (r < nr)
+                float va[4], vb[4], sa[4], sb[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
                 {
-                    const int p = row0 + r0 + r;
-                    const int tok = a.order[p] / a.topk;
-                    const int k = k0 + blk * 128;
-                    const uint16_t* xr = a.xin + (size_t)tok * a.H + k;
-                    const uint16_t* su = a.suh13 + ((size_t)e * 2 + m) * a.H + k;
-                    float va = h2f(xr[lane]), vb = h2f(xr[lane + 64]);
-                    prep_block_wave(va, vb, h2f(su[lane]), h2f(su[lane + 64]));
-                    dst[lane] = f2h(va);
-                    dst[lane + 64] = f2h(vb);
+                    const int it = it0 + u * GV_WAVES;
+                    if (it < items)
+                    {
+                        const int m = it / (nr * nblk), r = (it / nblk) % nr, blk = it % nblk;
+                        const int tok = s_rows[r0 + r] / a.topk;
+                        const uint16_t* xr = a.xin + (size_t)tok * a.H + blk * 128;
+                        const uint16_t* su = a.suh13 + ((size_t)e * 2 + m) * a.H + blk * 128;
+                        va[u] = h2f(xr[lane]); vb[u] = h2f(xr[lane + 64]);
+                        sa[u] = h2f(su[lane]); sb[u] = h2f(su[lane + 64]);
+                    }
                 }
-                else
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
                 {
-                    dst[lane] = 0;
-                    dst[lane + 64] = 0;
+                    const int it = it0 + u * GV_WAVES;
+                    if (it < items)
+                    {
+                        const int m = it / (nr * nblk), r = (it / nblk) % nr, blk = it % nblk;
+                        prep_block_wave(va[u], vb[u], sa[u], sb[u]);
+                        uint16_t* dst = xt + ((size_t)m * MT + r) * K + blk * 128;
+                        dst[lane] = f2h(va[u]);
+                        dst[lane + 64] = f2h(vb[u]);
+                    }
                 }
             }
         }
         else
         {
-            for (int i = threadIdx.x; i < MT * klen / 2; i += GV_THREADS)
+            for (int i = threadIdx.x; i < nr * xrow; i += GV_THREADS)
             {
-                const int r = i / (klen / 2), c = i % (klen / 2);
-                uint32_t v = 0;
-                if (r < nr)
-                {
-                    const int p = row0 + r0 + r;
-                    v = reinterpret_cast<const uint32_t*>(a.xin + (size_t)p * a.I + k0)[c];
-                }
-                lds[r * (GV_KPART / 2) + c] = v;
+                const int r = i / xrow, c = i % xrow;
+                lds[r * xrow + c] = reinterpret_cast<const uint32_t*>(a.xin + (size_t)s_rows[r0 + r] * a.I)[c];
             }
         }
         __syncthreads();
 
-        // ---- main loop: decode + dot2 over this wave's tile rows
-        float acc[NMAT][2][MT];
+        // ---- main loop: decode + dot2, GV_PF tile rows in flight per wave
+        float acc[2][MT];
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
+        for (int c = 0; c < 2; ++c)
 #pragma unroll
-            for (int c = 0; c < 2; ++c)
-#pragma unroll
-                for (int r = 0; r < MT; ++r) acc[m][c][r] = 0.0f;
+            for (int r = 0; r < MT; ++r) acc[c][r] = 0.0f;
 
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m)
+        const int nit = (KT - kw + WPM - 1) / WPM;   // tile rows of this wave
         {
-            gu32* wb = wbase[m] + ((size_t)(k0 / 16) * NT + cb * 8 + tau) * 24 + 3 * cp;
-            const uint32_t* xm = lds + (size_t)m * MT * (GV_KPART / 2);
-            // software pipeline: the next tile row's 12 bytes are in flight while the current one decodes
-            int tr = wave;
-            uint32_t n1 = 0, n2 = 0, n3 = 0;
-            if (tr < ntr)
-            {
-                gu32* src = wb + (size_t)tr * NT * 24;
-                n1 = __builtin_nontemporal_load(src);
-                n2 = __builtin_nontemporal_load(src + 1);
-                n3 = __builtin_nontemporal_load(src + 2);
-            }
-            for (; tr < ntr; tr += GV_WAVES)
-            {
-                const uint32_t d1 = n1, d2 = n2, d3 = n3;
-                const int nx = tr + GV_WAVES;
-                if (nx < ntr)
+            gu32* wb = wbase + (size_t)kw * row_stride;
+            const uint32_t* xm = lds + (size_t)mw * MT * xrow;
+            uint32_t buf[GV_PF][3];
+#pragma unroll
+            for (int j = 0; j < GV_PF; ++j)
+                if (j < nit)
                 {
-                    gu32* src = wb + (size_t)nx * NT * 24;
-                    n1 = __builtin_nontemporal_load(src);
-                    n2 = __builtin_nontemporal_load(src + 1);
-                    n3 = __builtin_nontemporal_load(src + 2);
+                    gu32* src = wb + (size_t)j * WPM * row_stride;
+                    buf[j][0] = __builtin_nontemporal_load(src);
+                    buf[j][1] = __builtin_nontemporal_load(src + 1);
+                    buf[j][2] = __builtin_nontemporal_load(src + 2);
                 }
-                const uint32_t d0 = __shfl(d3, src_lane, 64);
-                half2_t wv[16];
-                decode_lane(d0, d1, d2, d3, wv);
+            for (int g = 0; g < nit; g += GV_PF)
+            {
 #pragma unroll
-                for (int r = 0; r < MT; ++r)
+                for (int j = 0; j < GV_PF; ++j)
                 {
-                    const uint4 xa = *reinterpret_cast<const uint4*>(xm + (size_t)r * (GV_KPART / 2) + tr * 8);
-                    const uint4 xb = *reinterpret_cast<const uint4*>(xm + (size_t)r * (GV_KPART / 2) + tr * 8 + 4);
-                    const uint32_t X[8] = { xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w };
-                    float c0 = acc[m][0][r], c1 = acc[m][1][r];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q)
+                    if (g + j >= nit) break;
+                    const uint32_t d1 = buf[j][0], d2 = buf[j][1], d3 = buf[j][2];
+                    if (g + GV_PF + j < nit)      // refill this slot: GV_PF tile rows stay in flight
                     {
-                        c0 = __builtin_amdgcn_fdot2(wv[4 * q + 0], __builtin_bit_cast(half2_t, X[q]), c0, false);
-                        c0 = __builtin_amdgcn_fdot2(wv[4 * q + 1], __builtin_bit_cast(half2_t, X[4 + q]), c0, false);
-                        c1 = __builtin_amdgcn_fdot2(wv[4 * q + 2], __builtin_bit_cast(half2_t, X[q]), c1, false);
-                        c1 = __builtin_amdgcn_fdot2(wv[4 * q + 3], __builtin_bit_cast(half2_t, X[4 + q]), c1, false);
+                        gu32* src = wb + (size_t)(g + GV_PF + j) * WPM * row_stride;
+                        buf[j][0] = __builtin_nontemporal_load(src);
+                        buf[j][1] = __builtin_nontemporal_load(src + 1);
+                        buf[j][2] = __builtin_nontemporal_load(src + 2);
                     }
-                    acc[m][0][r] = c0;
-                    acc[m][1][r] = c1;
+                    const int tr = kw + (g + j) * WPM;
+                    const uint32_t d0 = __shfl(d3, src_lane, 64);
+                    uint32_t X[MT][8];
+#pragma unroll
+                    for (int r = 0; r < MT; ++r)
+                    {
+                        if (r >= nr) break;
+                        const uint4 xa = *reinterpret_cast<const uint4*>(xm + (size_t)r * xrow + tr * 8);
+                        const uint4 xb = *reinterpret_cast<const uint4*>(xm + (size_t)r * xrow + tr * 8 + 4);
+                        X[r][0] = xa.x; X[r][1] = xa.y; X[r][2] = xa.z; X[r][3] = xa.w;
+                        X[r][4] = xb.x; X[r][5] = xb.y; X[r][6] = xb.z; X[r][7] = xb.w;
+                    }
+                    decode_dot<MT>(d0, d1, d2, d3, X, nr, acc);
+                    // keep each tile row's decode within its step: bounds the live registers while the
+                    // GV_PF loads stay in flight
+                    __builtin_amdgcn_sched_barrier(0);
                 }
             }
         }
 
-        // ---- cross-wave reduction (fixed wave order) and partial store
+        // ---- cross-wave reduction in fixed wave order (waves of one matrix are consecutive)
         __syncthreads();
         float* red = reinterpret_cast<float*>(lds);
         const int col0 = tau * 16 + cp;
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-#pragma unroll
-            for (int r = 0; r < MT; ++r)
-            {
-                float* rr = red + (((size_t)wave * NMAT + m) * MT + r) * GV_COLS;
-                rr[col0] = acc[m][0][r];
-                rr[col0 + 8] = acc[m][1][r];
-            }
-        __syncthreads();
-        for (int i = threadIdx.x; i < NMAT * MT * GV_COLS; i += GV_THREADS)
+        for (int r = 0; r < MT; ++r)
         {
-            const int m = i / (MT * GV_COLS), r = (i / GV_COLS) % MT, c = i % GV_COLS;
-            if (r >= nr) continue;
+            if (r >= nr) break;
+            float* rr = red + ((size_t)wave * MT + r) * GV_COLS;
+            rr[col0] = acc[0][r];
+            rr[col0 + 8] = acc[1][r];
+        }
+        __syncthreads();
+        float* sum = red + (size_t)GV_WAVES * MT * GV_COLS;
+        for (int i = threadIdx.x; i < NMAT * nr * GV_COLS; i += GV_THREADS)
+        {
+            const int m = i / (nr * GV_COLS), r = (i / GV_COLS) % nr, c = i % GV_COLS;
             float s = 0.0f;
 #pragma unroll
-            for (int w = 0; w < GV_WAVES; ++w) s += red[(((size_t)w * NMAT + m) * MT + r) * GV_COLS + c];
-            const int p = row0 + r0 + r;
-            a.part[(((size_t)kq * a.n + p) * NMAT + m) * a.N + cb * GV_COLS + c] = s;
-        }
-
-        // ---- ticket: the last K part of this unit runs the epilogue
-        __threadfence();
-        __syncthreads();
-        if (threadIdx.x == 0)
-        {
-            int32_t* tk = a.tickets + ((size_t)g * a.maxchunk + chunk);
-            const int old = atomicAdd(tk, 1);
-            s_last = old == a.kparts - 1;
-            if (s_last) *tk = 0;
+            for (int w = 0; w < WPM; ++w) s += red[((size_t)(m * WPM + w) * MT + r) * GV_COLS + c];
+            sum[((size_t)m * MT + r) * GV_COLS + c] = s;
         }
         __syncthreads();
-        if (!s_last) continue;
-        __threadfence();
 
+        // ---- epilogue (one wave per route row)
         for (int r = wave; r < nr; r += GV_WAVES)
         {
-            const int p = row0 + r0 + r;
+            const int s = s_rows[r0 + r];
             const int c = cb * GV_COLS;
-            float v[NMAT][2];
-#pragma unroll
-            for (int m = 0; m < NMAT; ++m)
-            {
-                float sa = 0.0f, sb = 0.0f;
-                for (int q = 0; q < a.kparts; ++q)
-                {
-                    const float* pp = a.part + (((size_t)q * a.n + p) * NMAT + m) * a.N + c;
-                    sa += __builtin_nontemporal_load(pp + lane);
-                    sb += __builtin_nontemporal_load(pp + lane + 64);
-                }
-                v[m][0] = sa;
-                v[m][1] = sb;
-            }
             if constexpr (MODE == 0)
             {
+                float ga = sum[(0 * MT + r) * GV_COLS + lane], gb = sum[(0 * MT + r) * GV_COLS + lane + 64];
+                float ua = sum[(1 * MT + r) * GV_COLS + lane], ub = sum[(1 * MT + r) * GV_COLS + lane + 64];
                 const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c;
                 const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c;
-                out_block_wave(v[0][0], v[0][1], h2f(svg[lane]), h2f(svg[lane + 64]));
-                out_block_wave(v[1][0], v[1][1], h2f(svu[lane]), h2f(svu[lane + 64]));
-                float xa = r16(act_gu(v[0][0], v[1][0], a.limit));
-                float xb = r16(act_gu(v[0][1], v[1][1], a.limit));
+                out_block_wave(ga, gb, h2f(svg[lane]), h2f(svg[lane + 64]));
+                out_block_wave(ua, ub, h2f(svu[lane]), h2f(svu[lane + 64]));
+                float xa = r16(act_gu(ga, ua, a.limit));
+                float xb = r16(act_gu(gb, ub, a.limit));
                 const uint16_t* sd = a.suh2 + (size_t)e * a.I + c;
                 prep_block_wave(xa, xb, h2f(sd[lane]), h2f(sd[lane + 64]));
-                a.xd[(size_t)p * a.I + c + lane] = f2h(xa);
-                a.xd[(size_t)p * a.I + c + lane + 64] = f2h(xb);
+                a.xd[(size_t)s * a.I + c + lane] = f2h(xa);
+                a.xd[(size_t)s * a.I + c + lane + 64] = f2h(xb);
             }
             else
             {
+                float ya = sum[r * GV_COLS + lane], yb = sum[r * GV_COLS + lane + 64];
                 const uint16_t* sv = a.svh2 + (size_t)e * a.H + c;
-                out_block_wave(v[0][0], v[0][1], h2f(sv[lane]), h2f(sv[lane + 64]));
-                const int s = a.order[p];
-                a.Y[(size_t)s * a.H + c + lane] = v[0][0];
-                a.Y[(size_t)s * a.H + c + lane + 64] = v[0][1];
+                out_block_wave(ya, yb, h2f(sv[lane]), h2f(sv[lane + 64]));
+                a.Y[(size_t)s * a.H + c + lane] = ya;
+                a.Y[(size_t)s * a.H + c + lane + 64] = yb;
             }
         }
     }
 }
 
-struct GemvPlan
-{
-    int max_active, maxchunk, mt;
-    size_t part_gu, part_d, xd, tickets_gu, tickets_d;
-};
-
 static int pick_mt(int max_rows) { return max_rows <= 1 ? 1 : max_rows <= 2 ? 2 : max_rows <= 4 ? 4 : 8; }
 
-static GemvPlan plan(int n, int E, int H, int I, int max_rows)
+static size_t lds_bytes(int nmat, int mt, int K)
 {
-    GemvPlan p;
-    p.max_active = n < E ? n : E;
-    p.mt = pick_mt(max_rows);
-    p.maxchunk = (GV_MAX_ROWS + 1 - 1) / 1;   // tickets sized for the largest chunk count (MT = 1)
-    const int kp_gu = (H + GV_KPART - 1) / GV_KPART, kp_d = (I + GV_KPART - 1) / GV_KPART;
-    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    p.tickets_gu = al((size_t)p.max_active * (I / GV_COLS) * p.maxchunk * 4);
-    p.tickets_d = al((size_t)p.max_active * (H / GV_COLS) * p.maxchunk * 4);
-    p.part_gu = al((size_t)kp_gu * n * 2 * I * 4);
-    p.part_d = al((size_t)kp_d * n * H * 4);
-    p.xd = al((size_t)n * I * 2);
-    return p;
+    const size_t xt = (size_t)nmat * mt * K * 2;
+    const size_t red = ((size_t)GV_WAVES + nmat) * mt * GV_COLS * 4;
+    return xt > red ? xt : red;
 }
 
 template <int MODE>
 static void launch_gemv(const GemvArgs& a, int mt, int blocks, hipStream_t s)
 {
+    const int nmat = MODE == 0 ? 2 : 1;
+    const size_t sh = lds_bytes(nmat, mt, a.K);
     switch (mt)
     {
-        case 1: hipLaunchKernelGGL((k_expert_gemv<MODE, 1>), dim3(blocks), dim3(GV_THREADS), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((k_expert_gemv<MODE, 2>), dim3(blocks), dim3(GV_THREADS), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((k_expert_gemv<MODE, 4>), dim3(blocks), dim3(GV_THREADS), 0, s, a); break;
-        default: hipLaunchKernelGGL((k_expert_gemv<MODE, 8>), dim3(blocks), dim3(GV_THREADS), 0, s, a); break;
+        case 1: hipLaunchKernelGGL((k_expert_gemv<MODE, 1>), dim3(blocks), dim3(GV_THREADS), sh, s, a); break;
+        case 2: hipLaunchKernelGGL((k_expert_gemv<MODE, 2>), dim3(blocks), dim3(GV_THREADS), sh, s, a); break;
+        case 4: hipLaunchKernelGGL((k_expert_gemv<MODE, 4>), dim3(blocks), dim3(GV_THREADS), sh, s, a); break;
+        default: hipLaunchKernelGGL((k_expert_gemv<MODE, 8>), dim3(blocks), dim3(GV_THREADS), sh, s, a); break;
     }
+}
+
+static bool g_attr_done = false;
+static int g_max_dyn_lds = 64 * 1024;
+
+template <typename F>
+static void allow_dynamic_lds(F* kernel, int max_block)
+{
+    hipFuncAttributes fa{};
+    if (hipFuncGetAttributes(&fa, (const void*)kernel) != hipSuccess) return;
+    const int dyn = max_block - (int)fa.sharedSizeBytes;
+    if (dyn > 0) (void)hipFuncSetAttribute((const void*)kernel, hipFuncAttributeMaxDynamicSharedMemorySize, dyn);
+}
+
+// Lets the kernels use the whole LDS of a workgroup (160 KB on gfx950) for their dynamic part; clears any
+// error these queries leave behind so it is not reported by a later launch check.
+static int set_lds_limits()
+{
+    if (g_attr_done) return MM_OK;
+    int dev = 0, max_block = 0;
+    (void)hipGetDevice(&dev);
+    if (hipDeviceGetAttribute(&max_block, hipDeviceAttributeMaxSharedMemoryPerBlock, dev) != hipSuccess || max_block <= 0)
+        max_block = 64 * 1024;
+    allow_dynamic_lds(k_expert_gemv<0, 1>, max_block);
+    allow_dynamic_lds(k_expert_gemv<0, 2>, max_block);
+    allow_dynamic_lds(k_expert_gemv<0, 4>, max_block);
+    allow_dynamic_lds(k_expert_gemv<0, 8>, max_block);
+    allow_dynamic_lds(k_expert_gemv<1, 1>, max_block);
+    allow_dynamic_lds(k_expert_gemv<1, 2>, max_block);
+    allow_dynamic_lds(k_expert_gemv<1, 4>, max_block);
+    allow_dynamic_lds(k_expert_gemv<1, 8>, max_block);
+    (void)hipGetLastError();
+    g_max_dyn_lds = max_block - 2048;   // static LDS of the kernels is < 2 KB
+    g_attr_done = true;
+    return MM_OK;
 }
 
 }  // namespace mm
@@ -348,61 +431,52 @@ using namespace mm;
 
 extern "C" {
 
-size_t mm_gemv_counter_bytes(int n, int E, int H, int I)
-{
-    const GemvPlan p = plan(n, E, H, I, 1);
-    return p.tickets_gu + p.tickets_d;
-}
-
 size_t mm_gemv_workspace(int n, int E, int H, int I)
 {
-    const GemvPlan p = plan(n, E, H, I, 1);
-    return p.tickets_gu + p.tickets_d + p.part_gu + p.part_d + p.xd;
+    (void)E; (void)H;
+    return ((size_t)n * I * 2 + 255) & ~(size_t)255;   // xd: transformed down-projection inputs, fp16 [n][I]
 }
 
-int mm_expert_gemv(const mm_layer_t* L, const void* x_fp16, int T, int n, int topk, const int32_t* offsets,
-                   const int32_t* order, const int32_t* active, const int32_t* nactive, int max_rows, float* Y,
-                   void* workspace, size_t workspace_bytes, mm_stream_t stream)
+int mm_expert_gemv(const mm_layer_t* L, const void* x_fp16, int T, int n, int topk, const int64_t* ids,
+                   const int32_t* offsets, const int32_t* order, const int32_t* active, const int32_t* nactive,
+                   int max_rows, float* Y, void* workspace, size_t workspace_bytes, int phases, mm_stream_t stream)
 {
     MM_CHECK_ARG(L && L->gate_ptr && L->up_ptr && L->down_ptr && L->suh13 && L->svh13 && L->suh2 && L->svh2,
                  "mm_expert_gemv: incomplete layer");
-    MM_CHECK_ARG(L->E > 0 && L->H > 0 && L->I > 0 && L->H % 128 == 0 && L->I % 128 == 0,
-                 "mm_expert_gemv: H and I must be positive multiples of 128 (H=%d I=%d)", L->H, L->I);
-    MM_CHECK_ARG(x_fp16 && offsets && order && active && nactive && Y, "mm_expert_gemv: null pointer");
+    MM_CHECK_ARG(phases >= 1 && phases <= 3, "mm_expert_gemv: phases must be 1, 2 or 3");
+    MM_CHECK_ARG(L->E > 0 && L->E <= 1024 && L->H > 0 && L->I > 0 && L->H % 128 == 0 && L->I % 128 == 0,
+                 "mm_expert_gemv: need 0 < E <= 1024 and H, I positive multiples of 128 (E=%d H=%d I=%d)", L->E, L->H, L->I);
+    MM_CHECK_ARG(x_fp16 && Y, "mm_expert_gemv: null pointer");
     MM_CHECK_ARG(T > 0 && n > 0 && topk > 0 && n <= T * topk, "mm_expert_gemv: bad T/n/topk");
     MM_CHECK_ARG(max_rows > 0 && max_rows <= GV_MAX_ROWS, "mm_expert_gemv: max_rows must be in [1, %d]", GV_MAX_ROWS);
+    const bool perm = offsets != nullptr;
+    MM_CHECK_ARG(perm ? (order && active && nactive) : (ids != nullptr && n <= GV_ROUTE_MAX),
+                 "mm_expert_gemv: pass ids (n <= %d) or the permutation (offsets, order, active, nactive)", GV_ROUTE_MAX);
     const size_t need = mm_gemv_workspace(n, L->E, L->H, L->I);
     MM_CHECK_ARG(workspace && workspace_bytes >= need, "mm_expert_gemv: workspace too small (%zu < %zu)", workspace_bytes, need);
-    const GemvPlan p = plan(n, L->E, L->H, L->I, max_rows);
-    char* ws = static_cast<char*>(workspace);
-    int32_t* tk_gu = reinterpret_cast<int32_t*>(ws);
-    int32_t* tk_d = reinterpret_cast<int32_t*>(ws + p.tickets_gu);
-    float* part_gu = reinterpret_cast<float*>(ws + p.tickets_gu + p.tickets_d);
-    float* part_d = reinterpret_cast<float*>(ws + p.tickets_gu + p.tickets_d + p.part_gu);
-    uint16_t* xd = reinterpret_cast<uint16_t*>(ws + p.tickets_gu + p.tickets_d + p.part_gu + p.part_d);
-    const int maxchunk = (max_rows + p.mt - 1) / p.mt;
+    const int mt = pick_mt(max_rows);
+    set_lds_limits();
+    MM_CHECK_ARG(lds_bytes(2, mt, L->H) <= (size_t)g_max_dyn_lds && lds_bytes(1, mt, L->I) <= (size_t)g_max_dyn_lds,
+                 "mm_expert_gemv: H or I too large for the LDS budget at %d rows", mt);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
 
     GemvArgs a{};
     a.suh13 = L->suh13; a.svh13 = L->svh13; a.suh2 = L->suh2; a.svh2 = L->svh2;
-    a.offsets = offsets; a.order = order; a.active = active; a.nactive = nactive;
+    a.ids = ids; a.offsets = offsets; a.order = order; a.active = active; a.nactive = nactive;
     a.H = L->H; a.I = L->I; a.E = L->E; a.n = n; a.topk = topk; a.limit = L->limit;
-    a.max_active = p.max_active; a.maxchunk = maxchunk;
-    // gate + up
-    a.wptr0 = L->gate_ptr; a.wptr1 = L->up_ptr; a.xin = (const uint16_t*)x_fp16;
-    a.part = part_gu; a.tickets = tk_gu; a.xd = xd; a.Y = nullptr;
-    a.K = L->H; a.N = L->I; a.ncb = L->I / GV_COLS; a.kparts = (L->H + GV_KPART - 1) / GV_KPART;
+    a.max_active = n < L->E ? n : L->E;
+    uint16_t* xd = static_cast<uint16_t*>(workspace);
+    if (phases & 1)
     {
-        const int groups = (p.max_active * a.ncb + 7) / 8 * 8;
-        launch_gemv<0>(a, p.mt, groups * a.kparts, s);
+        a.wptr0 = L->gate_ptr; a.wptr1 = L->up_ptr; a.xin = (const uint16_t*)x_fp16; a.xd = xd; a.Y = nullptr;
+        a.K = L->H; a.N = L->I; a.ncb = L->I / GV_COLS;
+        launch_gemv<0>(a, mt, a.max_active * a.ncb, s);
     }
-    // down
-    a.wptr0 = L->down_ptr; a.wptr1 = nullptr; a.xin = xd;
-    a.part = part_d; a.tickets = tk_d; a.xd = nullptr; a.Y = Y;
-    a.K = L->I; a.N = L->H; a.ncb = L->H / GV_COLS; a.kparts = (L->I + GV_KPART - 1) / GV_KPART;
+    if (phases & 2)
     {
-        const int groups = (p.max_active * a.ncb + 7) / 8 * 8;
-        launch_gemv<1>(a, p.mt, groups * a.kparts, s);
+        a.wptr0 = L->down_ptr; a.wptr1 = nullptr; a.xin = xd; a.xd = nullptr; a.Y = Y;
+        a.K = L->I; a.N = L->H; a.ncb = L->H / GV_COLS;
+        launch_gemv<1>(a, mt, a.max_active * a.ncb, s);
     }
     return check_launch("mm_expert_gemv");
 }

@@ -40,15 +40,18 @@ def permute(ids, w, topk, E, stream=None):
     return o
 
 
-def expert_gemv(store, x16, routes, T, n, topk, max_rows, stream=None):
-    """Per-route expert outputs Y fp32 [n, H] (flat route order) on the decode path."""
+def expert_gemv(store, x16, ids, T, n, topk, max_rows, routes=None, stream=None):
+    """Per-route expert outputs Y fp32 [n, H] (flat route order) on the decode path. Routes are found in-kernel
+    from ids, or taken from a permutation (`routes`, from permute())."""
     dev = x16.device
     E, H, I = store.E, store.H, store.I
     wsb = _lib.load().mm_gemv_workspace(n, E, H, I)
     ws = torch.zeros(wsb, dtype=torch.uint8, device=dev)
     Y = torch.zeros((n, H), dtype=torch.float32, device=dev)
-    _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), T, n, topk, _i(routes["offsets"]), _i(routes["order"]),
-              _i(routes["active"]), _i(routes["nactive"]), int(max_rows), _i(Y), _i(ws), wsb, _lib.stream_ptr(stream))
+    ids = ids.reshape(-1).contiguous().long()
+    r = routes or {}
+    _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), T, n, topk, _i(ids), _i(r.get("offsets")), _i(r.get("order")),
+              _i(r.get("active")), _i(r.get("nactive")), int(max_rows), _i(Y), _i(ws), wsb, 3, _lib.stream_ptr(stream))
     return Y
 
 
@@ -74,11 +77,11 @@ def to_expert_input(x):
     return x.contiguous().to(torch.float16)
 
 
-def moe_forward(store, x, ids, w, shared_expert=None, stream=None):
+def moe_forward(store, x, ids, w, shared_expert=None, use_permutation=None, stream=None):
     """out fp32 [T, H] = sum_j w[t, j] * expert_{ids[t, j]}(x_t) (+ expert `shared_expert` with weight 1).
 
     Routes with ids outside [0, E) contribute nothing. The decode path serves up to GEMV_MAX_ROWS routes
-    per expert."""
+    per expert. Routing is found in-kernel for up to 1024 routes, else through permute()."""
     T = x.shape[0]
     ids = ids.reshape(T, -1).long()
     w = w.reshape(T, -1).float()
@@ -91,8 +94,10 @@ def moe_forward(store, x, ids, w, shared_expert=None, stream=None):
     max_rows = int(routes["counts"][: store.E].max().item()) if n else 0
     if max_rows > GEMV_MAX_ROWS:
         raise NotImplementedError(f"expert with {max_rows} routes: the fat-expert path is required (> {GEMV_MAX_ROWS})")
+    if use_permutation is None:
+        use_permutation = n > 1024
     x16 = to_expert_input(x)
-    Y = expert_gemv(store, x16, routes, T, n, k, max(1, max_rows), stream)
+    Y = expert_gemv(store, x16, ids, T, n, k, max(1, max_rows), routes if use_permutation else None, stream)
     return combine(Y, ids, w, T, k, store.H, store.E, stream=stream)
 
 
@@ -100,8 +105,10 @@ class DecodeRunner:
     """Fixed-shape decode MoE layer with every buffer preallocated: no allocation and no host sync per call,
     so a sequence of layers can be captured in one HIP graph."""
 
-    def __init__(self, E, H, I, T, k, device="cuda", shared=True):
+    def __init__(self, E, H, I, T, k, device="cuda", shared=True, max_rows=None):
         self.E, self.H, self.I, self.T, self.k0 = E, H, I, T, k
+        # routes per expert: one per token when every token picks distinct experts
+        self.max_rows = T if max_rows is None else max_rows
         self.shared = shared
         self.Eall = E + (1 if shared else 0)
         self.k = k + (1 if shared else 0)
@@ -130,16 +137,45 @@ class DecodeRunner:
         self.ids[:, : self.k0].copy_(ids)
         self.w[:, : self.k0].copy_(w)
 
-    def run(self, store, x16=None, ids=None, w=None, out=None, stream=None):
-        """One layer: permute -> fused decode expert MLP -> combine. ids/w default to the runner's buffers."""
-        s = _lib.stream_ptr(stream)
+    def route(self, ids=None, w=None, stream=None):
         ids = self.ids if ids is None else ids
         w = self.w if w is None else w
-        x16 = self.x16 if x16 is None else x16
-        out = self.out if out is None else out
         _lib.call("mm_permute", _i(ids), _i(w), self.n, self.k, self.Eall, _i(self.counts), _i(self.offsets),
-                  _i(self.order), None, None, None, _i(self.active), _i(self.nactive), _i(self.pws), self.pws_bytes, s)
-        _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), self.T, self.n, self.k, _i(self.offsets), _i(self.order),
-                  _i(self.active), _i(self.nactive), self.T, _i(self.Y), _i(self.gws), self.gws_bytes, s)
-        _lib.call("mm_combine", _i(out), _i(self.Y), _i(ids), _i(w), self.T, self.k, self.H, self.Eall, 0, s)
+                  _i(self.order), None, None, None, _i(self.active), _i(self.nactive), _i(self.pws), self.pws_bytes,
+                  _lib.stream_ptr(stream))
+
+    def experts(self, store, x16=None, ids=None, phases=3, use_permutation=False, stream=None):
+        """The fused expert kernels; routes found in-kernel from ids (or from route()'s permutation)."""
+        x16 = self.x16 if x16 is None else x16
+        ids = self.ids if ids is None else ids
+        p = use_permutation
+        _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), self.T, self.n, self.k, _i(ids),
+                  _i(self.offsets) if p else None, _i(self.order) if p else None, _i(self.active) if p else None,
+                  _i(self.nactive) if p else None, self.max_rows, _i(self.Y), _i(self.gws), self.gws_bytes, phases,
+                  _lib.stream_ptr(stream))
+
+    def combine(self, ids=None, w=None, out=None, stream=None):
+        ids = self.ids if ids is None else ids
+        w = self.w if w is None else w
+        out = self.out if out is None else out
+        _lib.call("mm_combine", _i(out), _i(self.Y), _i(ids), _i(w), self.T, self.k, self.H, self.Eall, 0,
+                  _lib.stream_ptr(stream))
         return out
+
+    def combine_prepare(self, ids=None, w=None, out=None, x16_next=None, rescale=True, stream=None):
+        """combine, then the next layer's fp16 input (bf16 rounding, optional unit-RMS rescale) in one launch."""
+        ids = self.ids if ids is None else ids
+        w = self.w if w is None else w
+        out = self.out if out is None else out
+        x16_next = self.x16 if x16_next is None else x16_next
+        _lib.call("mm_combine_prepare", _i(out), _i(self.Y), _i(ids), _i(w), self.T, self.k, self.H, self.Eall,
+                  1 if rescale else 0, _i(x16_next), _lib.stream_ptr(stream))
+        return out
+
+    def run(self, store, x16=None, ids=None, w=None, out=None, use_permutation=False, stream=None):
+        """One layer: fused decode expert MLP (in-kernel routing) -> combine. ids/w default to the runner's
+        buffers. With use_permutation the routes go through mm_permute first."""
+        if use_permutation:
+            self.route(ids, w, stream)
+        self.experts(store, x16, ids, 3, use_permutation, stream)
+        return self.combine(ids, w, out, stream)

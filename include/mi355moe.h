@@ -109,19 +109,19 @@ typedef struct mm_layer
     float limit;                /* SwiGLU clamp (0 = off); reference default 10 */
 } mm_layer_t;
 
-/* Bytes of device workspace mm_expert_gemv needs; the first mm_gemv_counter_bytes(...) bytes of it must be
- * zero before the first call (the kernels leave them zero again). */
+/* Bytes of device workspace mm_expert_gemv needs (the transformed down-projection inputs, fp16 [n][I]). */
 size_t mm_gemv_workspace(int n, int E, int H, int I);
-size_t mm_gemv_counter_bytes(int n, int E, int H, int I);
 
 /* Decode expert path (replaces exllamav3 exl3_moe on the decode split, patches/vllm-exl3-host-dma.patch:323-445):
- * routes come from mm_permute (offsets, order, active, nactive over the same n routes and E experts). For every
- * routed (token, expert) pair with 0 <= expert < E, computes the expert SwiGLU MLP on x fp16 [T][H] with fused
- * EXL3 trellis decode and writes Y fp32 [n][H] at the route's flat index (rows of sentinel routes are left
- * untouched). max_rows bounds the routes of any one expert (<= 256). */
-int mm_expert_gemv(const mm_layer_t* layer, const void* x_fp16, int T, int n, int topk, const int32_t* offsets,
-                   const int32_t* order, const int32_t* active, const int32_t* nactive, int max_rows, float* Y,
-                   void* workspace, size_t workspace_bytes, mm_stream_t stream);
+ * for every route s < n with 0 <= ids[s] < E (token s / topk), computes the expert SwiGLU MLP on x fp16 [T][H]
+ * with fused EXL3 trellis decode and writes Y fp32 [n][H] row s (rows of other routes are left untouched).
+ * Routes are found in-kernel from ids when offsets is NULL (n <= 1024); otherwise offsets/order/active/nactive
+ * from mm_permute over the same routes are used (ids may then be NULL). max_rows bounds the routes of any one
+ * expert (<= 256). phases: 1 = gate/up projection (+ SwiGLU and down-input transform into the workspace),
+ * 2 = down projection from that workspace, 3 = both. */
+int mm_expert_gemv(const mm_layer_t* layer, const void* x_fp16, int T, int n, int topk, const int64_t* ids,
+                   const int32_t* offsets, const int32_t* order, const int32_t* active, const int32_t* nactive,
+                   int max_rows, float* Y, void* workspace, size_t workspace_bytes, int phases, mm_stream_t stream);
 
 /* ----------------------------------------------------------------------------------------- utility */
 
@@ -138,6 +138,11 @@ uint64_t mm_expert_seed(uint64_t layer_seed, uint64_t expert);
  * row to unit RMS first (the decode-chain workload's between-layer step): x16 = fp16(bf16(x * s_t)),
  * s_t = 1/sqrt(mean(x_t^2)) if rescale else 1. Also writes bf16 [T][H] if x_bf16 != NULL. */
 int mm_prepare_input(const float* x, int T, int H, int rescale, void* x_bf16, void* x_fp16, mm_stream_t stream);
+
+/* mm_combine (accumulate = 0) followed by mm_prepare_input on its output, in one launch (one workgroup per
+ * token): out fp32 [T][H], and the next expert input x_fp16 [T][H] (bf16 rounding, optional unit-RMS rescale). */
+int mm_combine_prepare(float* out, const float* Y, const int64_t* ids, const float* w, int T, int k, int H, int E,
+                       int rescale, void* x_fp16, mm_stream_t stream);
 
 #ifdef __cplusplus
 }

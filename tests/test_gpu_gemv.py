@@ -68,14 +68,18 @@ def test_per_route_outputs_and_masked_routes(dev):
     w = np.full((T, k), 0.5, np.float32)
     x16 = np.random.default_rng(1).normal(0, 1, (T, H)).astype(np.float16)
     routes = moe.permute(_t(ids, dev), _t(w, dev), k, E)
-    Y = moe.expert_gemv(st, _t(x16, dev), routes, T, T * k, k, 4)
-    torch.cuda.synchronize()
     ref = OracleLayer(st, seed).per_route(x16.astype(np.float32), ids)
-    Yg = Y.cpu().numpy()
     valid = ~np.isnan(ref[:, 0])
-    assert np.all(Yg[~valid] == 0.0)                 # masked routes left untouched (zero-initialised)
-    ok, m = within_tolerance(Yg[valid], ref[valid])
-    assert ok, m
+    outs = []
+    for use_perm in (False, True):                   # in-kernel routing and the permutation give the same rows
+        Y = moe.expert_gemv(st, _t(x16, dev), _t(ids, dev), T, T * k, k, 4, routes if use_perm else None)
+        torch.cuda.synchronize()
+        Yg = Y.cpu().numpy()
+        assert np.all(Yg[~valid] == 0.0)             # masked routes left untouched (zero-initialised)
+        ok, m = within_tolerance(Yg[valid], ref[valid])
+        assert ok, m
+        outs.append(Yg)
+    assert np.array_equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("T", [1, 4])
@@ -113,6 +117,47 @@ def test_deterministic_and_runner_matches(dev):
     R.set_routes(_t(ids, dev), _t(w, dev))
     R.x16.copy_(x16)
     c = R.run(st).clone()
-    d = R.run(st).clone()
+    d = R.run(st, use_permutation=True).clone()
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(c, d)
+
+
+def test_many_routes_per_expert_chunks(dev):
+    """An expert with more routes than one chunk (rows > 8) and the permutation path (> 1024 routes)."""
+    import torch
+    from mi355moe import moe
+    H, I, E, T, k = 512, 256, 6, 200, 6
+    seed = 321
+    st = make_store(E, H, I, seed, device=dev)
+    rng = np.random.default_rng(9)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)    # each expert ~200 routes
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
+    out = moe.moe_forward(st, _t(x16, dev), _t(ids, dev), _t(w, dev))
+    torch.cuda.synchronize()
+    ref = OracleLayer(st, seed).forward(x16.astype(np.float32), ids, w)
+    ok, m = within_tolerance(out.cpu().numpy(), ref)
+    assert ok, m
+
+
+def test_combine_prepare_matches_parts(dev):
+    import torch
+    from mi355moe import _lib, moe
+    T, k, H, E = 4, 9, 4096, 385
+    rng = np.random.default_rng(2)
+    Y = _t(rng.normal(0, 1, (T * k, H)).astype(np.float32), dev)
+    ids = _t(rng.integers(0, E, (T, k)).astype(np.int64), dev)
+    w = _t(rng.uniform(0, 1, (T, k)).astype(np.float32), dev)
+    ref = moe.combine(Y, ids, w, T, k, H, E)
+    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    x16 = torch.empty((T, H), dtype=torch.float16, device=dev)
+    _lib.call("mm_combine_prepare", out.data_ptr(), Y.data_ptr(), ids.data_ptr(), w.data_ptr(), T, k, H, E, 1,
+              x16.data_ptr(), _lib.stream_ptr())
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)
+    o = ref.cpu().numpy().astype(np.float64)
+    scaled = (o / np.sqrt((o * o).mean(1, keepdims=True))).astype(np.float32)
+    bf = (scaled.view(np.uint32) + 0x7FFF + ((scaled.view(np.uint32) >> 16) & 1)) & 0xFFFF0000
+    expect = bf.view(np.float32).astype(np.float16)
+    got = x16.cpu().numpy()
+    assert np.mean(got != expect) < 1e-3 and np.allclose(got, expect, rtol=1e-2)
