@@ -51,7 +51,7 @@ def expert_gemv(store, x16, ids, T, n, topk, max_rows, routes=None, stream=None)
     ids = ids.reshape(-1).contiguous().long()
     r = routes or {}
     _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), T, n, topk, _i(ids), _i(r.get("offsets")), _i(r.get("order")),
-              _i(r.get("active")), _i(r.get("nactive")), int(max_rows), _i(Y), _i(ws), wsb, 3, _lib.stream_ptr(stream))
+              _i(r.get("active")), _i(r.get("nactive")), int(max_rows), _i(Y), _i(ws), wsb, 15, _lib.stream_ptr(stream))
     return Y
 
 
@@ -144,8 +144,9 @@ class DecodeRunner:
                   _i(self.order), None, None, None, _i(self.active), _i(self.nactive), _i(self.pws), self.pws_bytes,
                   _lib.stream_ptr(stream))
 
-    def experts(self, store, x16=None, ids=None, phases=3, use_permutation=False, stream=None):
-        """The fused expert kernels; routes found in-kernel from ids (or from route()'s permutation)."""
+    def experts(self, store, x16=None, ids=None, phases=15, use_permutation=False, stream=None):
+        """The expert kernels (phases: mask of 1 gate/up partial, 2 gate/up epilogue, 4 down partial, 8 down
+        epilogue); routes found in-kernel from ids (or from route()'s permutation)."""
         x16 = self.x16 if x16 is None else x16
         ids = self.ids if ids is None else ids
         p = use_permutation
@@ -172,10 +173,21 @@ class DecodeRunner:
                   1 if rescale else 0, _i(x16_next), _lib.stream_ptr(stream))
         return out
 
+    def layer(self, store, x16=None, ids=None, w=None, out=None, x16_next=None, rescale=True, stream=None):
+        """One decode MoE layer through mm_moe_decode (4 launches: gate/up partial + epilogue, down partial,
+        down epilogue fused with the combine and, if x16_next is given, the next layer's input)."""
+        x16 = self.x16 if x16 is None else x16
+        ids = self.ids if ids is None else ids
+        w = self.w if w is None else w
+        out = self.out if out is None else out
+        _lib.call("mm_moe_decode", store.mm_layer(), _i(x16), self.T, self.k, _i(ids), _i(w), self.max_rows, _i(out),
+                  _i(x16_next), 1 if rescale else 0, _i(self.gws), self.gws_bytes, _lib.stream_ptr(stream))
+        return out
+
     def run(self, store, x16=None, ids=None, w=None, out=None, use_permutation=False, stream=None):
-        """One layer: fused decode expert MLP (in-kernel routing) -> combine. ids/w default to the runner's
-        buffers. With use_permutation the routes go through mm_permute first."""
+        """One layer as separate steps: expert MLP (in-kernel routing, or the permutation with use_permutation)
+        -> Y -> combine. ids/w default to the runner's buffers."""
         if use_permutation:
             self.route(ids, w, stream)
-        self.experts(store, x16, ids, 3, use_permutation, stream)
+        self.experts(store, x16, ids, 15, use_permutation, stream)
         return self.combine(ids, w, out, stream)

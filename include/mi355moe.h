@@ -109,19 +109,30 @@ typedef struct mm_layer
     float limit;                /* SwiGLU clamp (0 = off); reference default 10 */
 } mm_layer_t;
 
-/* Bytes of device workspace mm_expert_gemv needs (the transformed down-projection inputs, fp16 [n][I]). */
+/* Bytes of device workspace mm_expert_gemv / mm_moe_decode need for n routes (K-part partial sums and the
+ * transformed down-projection inputs). */
 size_t mm_gemv_workspace(int n, int E, int H, int I);
 
 /* Decode expert path (replaces exllamav3 exl3_moe on the decode split, patches/vllm-exl3-host-dma.patch:323-445):
  * for every route s < n with 0 <= ids[s] < E (token s / topk), computes the expert SwiGLU MLP on x fp16 [T][H]
  * with fused EXL3 trellis decode and writes Y fp32 [n][H] row s (rows of other routes are left untouched).
  * Routes are found in-kernel from ids when offsets is NULL (n <= 1024); otherwise offsets/order/active/nactive
- * from mm_permute over the same routes are used (ids may then be NULL). max_rows bounds the routes of any one
- * expert (<= 256). phases: 1 = gate/up projection (+ SwiGLU and down-input transform into the workspace),
- * 2 = down projection from that workspace, 3 = both. */
+ * from mm_permute over the same routes are used. max_rows bounds the routes of any one expert (<= 256).
+ * phases is a mask of the four launches, run in this order on the same workspace: 1 = gate/up partial sums,
+ * 2 = gate/up epilogue (output transforms, SwiGLU, down-input transform), 4 = down partial sums, 8 = down
+ * epilogue (output transform into Y); 15 = the whole expert MLP. */
 int mm_expert_gemv(const mm_layer_t* layer, const void* x_fp16, int T, int n, int topk, const int64_t* ids,
                    const int32_t* offsets, const int32_t* order, const int32_t* active, const int32_t* nactive,
                    int max_rows, float* Y, void* workspace, size_t workspace_bytes, int phases, mm_stream_t stream);
+
+/* One decode MoE layer (the fused-MoE call of the decode split, patches/vllm-exl3-host-dma.patch:315-449, with the
+ * weighted combine of patches/vllm-exl3-host-dma.patch:327-342 made deterministic): routes ids int64 [T*topk]
+ * with weights w fp32 [T*topk] (T*topk <= 1024; ids outside [0, E) contribute nothing) ->
+ * out fp32 [T][H] = sum_j w[t,j] * expert_{ids[t,j]}(x_t). If x_next_fp16 != NULL it also receives the next
+ * layer's fp16 input fp16(bf16(out_t * s_t)), s_t = 1/RMS(out_t) if rescale else 1. */
+int mm_moe_decode(const mm_layer_t* layer, const void* x_fp16, int T, int topk, const int64_t* ids, const float* w,
+                  int max_rows, float* out, void* x_next_fp16, int rescale, void* workspace, size_t workspace_bytes,
+                  mm_stream_t stream);
 
 /* ----------------------------------------------------------------------------------------- utility */
 

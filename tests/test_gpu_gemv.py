@@ -118,8 +118,18 @@ def test_deterministic_and_runner_matches(dev):
     R.x16.copy_(x16)
     c = R.run(st).clone()
     d = R.run(st, use_permutation=True).clone()
+    xn = torch.empty_like(R.x16)
+    f = R.layer(st, x16_next=xn).clone()
     torch.cuda.synchronize()
-    assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(c, d)
+    assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(c, d) and torch.equal(a, f)
+    # the fused next-input matches mm_combine_prepare on the same output
+    from mi355moe import _lib
+    out2 = torch.empty_like(f)
+    x2 = torch.empty_like(xn)
+    _lib.call("mm_combine_prepare", out2.data_ptr(), R.Y.data_ptr(), R.ids.data_ptr(), R.w.data_ptr(), T, R.k, H, R.Eall, 1,
+              x2.data_ptr(), _lib.stream_ptr())
+    torch.cuda.synchronize()
+    assert torch.equal(out2, f) and torch.equal(x2, xn)
 
 
 def test_many_routes_per_expert_chunks(dev):
