@@ -124,21 +124,9 @@ def main():
     outs = [torch.empty((T, H), dtype=torch.float32, device=dev) for _ in range(2)]
     L_ = _lib.load()
 
-    def layer(l, phase_events=None):
+    def layer(l):
         # mm_moe_decode reads R.x16 and writes this layer's output and the next layer's input (R.x16)
-        if phase_events is None:
-            return R.layer(stores[l], x16=R.x16, ids=ids_d[l], w=w_d[l], out=outs[l % 2], x16_next=R.x16, rescale=True)
-        # the same computation as separate launches (bit-identical), with the dominant kernel bracketed by events
-        e0, e1, e2, e3 = phase_events
-        e0.record()
-        R.experts(stores[l], ids=ids_d[l], phases=1)       # gate/up partial sums (dominant kernel)
-        e1.record()
-        R.experts(stores[l], ids=ids_d[l], phases=2)       # gate/up epilogue
-        e2.record()
-        R.experts(stores[l], ids=ids_d[l], phases=4)       # down partial sums
-        e3.record()
-        R.experts(stores[l], ids=ids_d[l], phases=8)       # down epilogue -> Y
-        return R.combine_prepare(ids_d[l], w_d[l], out=outs[l % 2], x16_next=R.x16, rescale=True)
+        return R.layer(stores[l], x16=R.x16, ids=ids_d[l], w=w_d[l], out=outs[l % 2], x16_next=R.x16, rescale=True)
 
     def step():
         _lib.check(L_.mm_prepare_input(x0.data_ptr(), T, H, 1, None, R.x16.data_ptr(), _lib.stream_ptr()), "prepare")
@@ -176,23 +164,36 @@ def main():
     out_rms = float(final.float().pow(2).mean().sqrt())
     log(f"step {ms_step:.3f} ms (wall {ms_wall:.3f} ms), final output rms {out_rms:.4f}")
 
-    # live roofline of the dominant kernel (gate/up decode GEMV partial sums), HIP events on its stream
-    reps = 3
-    evs = [[tuple(torch.cuda.Event(enable_timing=True) for _ in range(4)) for _ in range(L)] for _ in range(reps)]
-    for r in range(reps):
-        _lib.check(L_.mm_prepare_input(x0.data_ptr(), T, H, 1, None, R.x16.data_ptr(), _lib.stream_ptr()), "prepare")
-        for l in range(L):
-            layer(l, evs[r][l])
-    torch.cuda.synchronize()
-    t_gu = np.array([[evs[r][l][0].elapsed_time(evs[r][l][1]) for l in range(L)] for r in range(reps)]).mean(0)
-    t_d = np.array([[evs[r][l][2].elapsed_time(evs[r][l][3]) for l in range(L)] for r in range(reps)]).mean(0)
+    # live roofline of the dominant kernel (gate/up decode GEMV partial sums) and of the down partial sums: each
+    # kernel's 40 per-layer launches are captured in a graph of their own and replayed between HIP events on the
+    # replay stream, so the average launch time carries no host launch gaps
+    def kernel_graph(phase):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for l in range(L):
+                R.experts(stores[l], ids=ids_d[l], phases=phase)
+        return g
+
+    def time_graph(g, reps=5):
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / (reps * L)     # ms per launch
+
+    g_gu, g_d = kernel_graph(1), kernel_graph(4)
+    t_gu, t_d = time_graph(g_gu), time_graph(g_d)
     bytes_gu = np.array([(u + 1) * BYTES_GU_PARTIAL for u in uniq], np.float64)
     bytes_d = np.array([(u + 1) * BYTES_TRELLIS for u in uniq], np.float64)
-    gu_gbs = bytes_gu.sum() / (t_gu.sum() * 1e-3) / 1e9
-    d_gbs = bytes_d.sum() / (t_d.sum() * 1e-3) / 1e9
+    gu_gbs = bytes_gu.mean() / (t_gu * 1e-3) / 1e9
+    d_gbs = bytes_d.mean() / (t_d * 1e-3) / 1e9
     step_bytes = float(sum((u + 1) * BYTES_EXPERT for u in uniq))
     step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"gate/up kernel: {t_gu.mean() * 1e3:.1f} us avg, {gu_gbs:.0f} GB/s; down kernel: {t_d.mean() * 1e3:.1f} us avg, "
+    log(f"gate/up kernel: {t_gu * 1e3:.1f} us avg, {gu_gbs:.0f} GB/s; down kernel: {t_d * 1e3:.1f} us avg, "
         f"{d_gbs:.0f} GB/s; step {step_gbs:.0f} GB/s")
 
     cpu = None
@@ -220,11 +221,11 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "k_expert_partial<0,*> (gate/up decode GEMV partial sums)",
-                     "avg_launch_us": round(float(t_gu.mean()) * 1e3, 2),
+                     "avg_launch_us": round(float(t_gu) * 1e3, 2),
                      "bytes_per_launch": round(float(bytes_gu.mean()), 1)},
         "step_hbm": {"bytes_per_step": step_bytes, "achieved_gbs": round(step_gbs, 1),
                      "frac_of_peak": round(step_gbs / HBM_PEAK_GBS, 4),
-                     "down_kernel_gbs": round(d_gbs, 1), "down_avg_launch_us": round(float(t_d.mean()) * 1e3, 2)},
+                     "down_kernel_gbs": round(d_gbs, 1), "down_avg_launch_us": round(float(t_d) * 1e3, 2)},
         "ms_per_step_wall": round(ms_wall, 4),
     }
     if cpu is not None:
