@@ -117,22 +117,21 @@ def main():
     ids_ext = [np.concatenate([r[0], np.full((T, 1), E, np.int64)], 1) for r in routes]
     w_ext = [np.concatenate([r[1], np.ones((T, 1), np.float32)], 1) for r in routes]
     uniq = [len(np.unique(r[0])) for r in routes]
-    ids_d = [torch.from_numpy(a).to(dev) for a in ids_ext]
-    w_d = [torch.from_numpy(a).to(dev) for a in w_ext]
-    R = DecodeRunner(E, H, I, T, K_TOP, device=dev)
+    # one runner (routes + workspace) per layer, so every kernel reads its own layer's routing state
+    runners = []
+    for l in range(L):
+        R = DecodeRunner(E, H, I, T, K_TOP, device=dev)
+        R.set_routes(torch.from_numpy(routes[l][0]).to(dev), torch.from_numpy(routes[l][1]).to(dev))
+        runners.append(R)
     x0 = torch.from_numpy(workload.activations(T, H, seed=7)).to(dev)
     outs = [torch.empty((T, H), dtype=torch.float32, device=dev) for _ in range(2)]
-    L_ = _lib.load()
-
-    def layer(l):
-        # mm_moe_decode reads R.x16 and writes this layer's output and the next layer's input (R.x16)
-        return R.layer(stores[l], x16=R.x16, ids=ids_d[l], w=w_d[l], out=outs[l % 2], x16_next=R.x16, rescale=True)
 
     def step():
-        _lib.check(L_.mm_prepare_input(x0.data_ptr(), T, H, 1, None, R.x16.data_ptr(), _lib.stream_ptr()), "prepare")
+        # layer l reads the previous output (fp32), rescales it to unit RMS, rounds it through bf16 to the fp16
+        # expert input, and writes its own output
         src = x0
         for l in range(L):
-            src = layer(l)
+            src = runners[l].layer(stores[l], x=src, out=outs[l % 2], rescale=True)
         return src
 
     # eager warm-up, then capture the 40-layer step as one graph
@@ -166,12 +165,13 @@ def main():
 
     # live roofline of the dominant kernel (gate/up decode GEMV partial sums) and of the down partial sums: each
     # kernel's 40 per-layer launches are captured in a graph of their own and replayed between HIP events on the
-    # replay stream, so the average launch time carries no host launch gaps
+    # replay stream, so the average launch time carries no host launch gaps. Every runner's workspace holds its
+    # layer's routing records from the step replays above.
     def kernel_graph(phase):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for l in range(L):
-                R.experts(stores[l], ids=ids_d[l], phases=phase)
+                runners[l].experts(stores[l], x=outs[0], phases=phase)
         return g
 
     def time_graph(g, reps=5):
@@ -185,7 +185,7 @@ def main():
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / (reps * L)     # ms per launch
 
-    g_gu, g_d = kernel_graph(1), kernel_graph(4)
+    g_gu, g_d = kernel_graph(2), kernel_graph(8)
     t_gu, t_d = time_graph(g_gu), time_graph(g_d)
     bytes_gu = np.array([(u + 1) * BYTES_GU_PARTIAL for u in uniq], np.float64)
     bytes_d = np.array([(u + 1) * BYTES_TRELLIS for u in uniq], np.float64)
@@ -220,7 +220,7 @@ def main():
                    "shared_experts": 1, "mean_distinct_experts_per_layer": round(float(np.mean(uniq)), 2)},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "k_expert_partial<0,*> (gate/up decode GEMV partial sums)",
+                     "kernel": "mm::k_partial<0> (gate/up decode GEMV partial sums)",
                      "avg_launch_us": round(float(t_gu) * 1e3, 2),
                      "bytes_per_launch": round(float(bytes_gu.mean()), 1)},
         "step_hbm": {"bytes_per_step": step_bytes, "achieved_gbs": round(step_gbs, 1),

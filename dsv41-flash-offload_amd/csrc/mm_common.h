@@ -21,6 +21,16 @@ __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_c
 __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }   // RNE
 __device__ __forceinline__ float r16(float f) { return (float)(_Float16)f; }
 
+// fp32 -> bf16 bits, round to nearest even; NaN stays a (quiet) NaN.
+__device__ __forceinline__ uint16_t f2bf(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__device__ __forceinline__ float bf16_value(float f) { return __uint_as_float((uint32_t)f2bf(f) << 16); }
+
 // 128-point fast Walsh-Hadamard transform held by one wave64: lane L owns elements L (a) and L + 64 (b).
 // Stages run with strides 1, 2, ..., 64 and write (lo + hi, lo - hi), exactly the reference butterfly
 // (ft_core.h:89-94), so the fp32 results are bit-identical.

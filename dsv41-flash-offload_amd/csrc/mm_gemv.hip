@@ -1,474 +1,500 @@
-// Decode expert path: EXL3 3-bpw trellis decode fused into a multi-token GEMV on gfx950.
+// Decode expert path: EXL3 3-bpw trellis decode fused into a multi-token GEMV on gfx950, multiply-accumulate
+// on MFMA.
 //
-// Each projection runs as two launches. The partial kernel's work unit is (active expert, 128-column output
-// block, 1024-row K part): a 4-wave workgroup streams the unit's tiles straight from HBM -- a wave covers one
-// tile row of the block per step (8 tiles x 96 B = 768 B contiguous, one 12-byte load per lane, two register
-// sets of 4 tile rows in flight), 8 lanes per tile, each lane decoding 32 consecutive trellis states = 16 input
-// rows x 2 output columns -- and writes the unit's partial sums. The epilogue kernel adds the K parts in fixed
-// order and applies the output Hadamard transform, SwiGLU and the down-input transform (gate/up) or the down
-// output transform. Stream order alone makes the partials visible to the epilogue: the kernels never fence or
-// wait on each other, and every result is deterministic. Splitting K gives ~1600 units per projection at the
-// decode shapes, which keeps all 256 CUs evenly busy.
+// A layer runs as five launches on the caller's stream. Stream order is the only synchronisation (no fences,
+// no atomics between workgroups), so every result is deterministic:
+//   1. k_route_prep    one workgroup per (route, gate|up, 512 input rows): the route's sorted position (stable
+//                      by expert, then route index), one record per active expert, and the route's transformed
+//                      input xt = r16(FWHT128(x * suh) * HAD) in MFMA operand order, with its sums (the input
+//                      conversion and the optional unit-RMS rescale happen here too).
+//   2. k_partial<0>    gate/up partial sums, one launch that fills the GPU once: the work -- every
+//                      (active expert, matrix, 128 output columns) segment of 256 tile rows -- is cut into
+//                      equal row ranges, one per wave, from the active-expert count on the device. A wave
+//                      streams its rows (8 tiles = 768 contiguous bytes each) from HBM into an 8-deep
+//                      wave-private LDS ring with buffer-to-LDS loads, decodes each tile in registers and
+//                      multiplies two tile rows at a time on v_mfma_f32_16x16x32_f16 against the inputs of up
+//                      to 16 routes (L2 reads, prefetched with the same depth).
+//   3. k_gu_epilogue   per (route, 128 columns of I): row ranges added in order, output transforms, SwiGLU, the
+//                      down-input transform (MFMA operand order) and its sums.
+//   4. k_partial<1>    down partial sums, as 2.
+//   5. k_down_combine  per (token, 128 columns of H): row ranges, output transform, weighted sum of the token's
+//                      routes in ascending order; or k_down_y: per-route rows.
 //
-// Routing: for decode-sized calls (n <= 1024 routes) a workgroup finds its expert and that expert's routes from
-// the route ids -- the a-th active expert in ascending id, its routes in ascending route index, the same stable
-// order as the permutation. Larger calls pass the permutation (offsets/order/active).
-//
-// Numerics follow the reference's EXACT expert (kernels/cpu_avx2/ft_core.h:977-1011): fp16 weights
-// fp16(fma(1024 + bytesum, KINV, KBIAS)) (one rounding, v_pk_fma_f16), fp16 transformed activations,
-// fp32 accumulation (v_dot2_f32_f16), fp16 rounding at the same points.
+// Codebook (kernels/cpu_avx2/ft_core.h:75-83): w = fp16(fma(1024 + bytesum, KINV, KBIAS)). By default the
+// weights are evaluated as the reference's AFFINE expert does (ft_core.h:267-293): MFMA accumulates
+// S = sum x (1024 + bytesum) on the exact fp16 codes and the epilogue forms KINV * S + KBIAS * sum x, so no
+// per-weight rounding is spent. With MM_LAYER_EXACT every weight is rounded to fp16 first (v_pk_fma_f16), the
+// reference's EXACT expert (ft_core.h:977-1011). fp16 activations, fp32 accumulation, fp16 rounding at the
+// reference's points in both.
 #include "mm_common.h"
 
 namespace mm {
 
 constexpr int GV_WAVES = 4;
 constexpr int GV_THREADS = 64 * GV_WAVES;
-constexpr int GV_COLS = 128;         // output columns per unit (8 tiles)
-constexpr int GV_KPART = 1024;       // input rows per unit
-constexpr int GV_MAX_ROWS = 256;     // routes per expert on this path
-constexpr int GV_ROUTE_MAX = 1024;   // in-kernel routing limit (routes per call)
-constexpr int GV_PF = 4;             // tile rows per register set (two sets in flight)
+constexpr int GV_COLS = 128;          // output columns per segment (8 tiles)
+constexpr int GV_MAX_ROWS = 256;      // routes per expert on this path
+constexpr int GV_ROUTE_MAX = 1024;    // in-kernel routing limit (routes per call)
+constexpr int GV_RING = 8;            // tile rows in flight per wave (even: rows go through MFMA in pairs)
+static_assert(GV_RING % 2 == 0, "row pairs");
+constexpr int ROW_BYTES = 8 * 96;     // one tile row of a segment
+constexpr int WAVES_PER_CU = 16;      // partial kernels: 4 workgroups of 4 waves per CU (<= 128 VGPRs)
+constexpr int PREP_ROWS = 512;        // input rows per route-prep workgroup
+constexpr int MAX_TOPK = 16;
 
-typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
 
-// Trellis rows are read with raw buffer loads: a per-matrix resource descriptor in SGPRs (bounds-checked to the
-// matrix), one per-lane 32-bit byte offset and a wave-uniform row offset, so the in-flight loads cost no VGPRs
-// for addresses. aux = 2 marks the loads non-temporal (each byte is read once per call).
-constexpr int BUF_DWORD3 = 0x00020000;
-__device__ __forceinline__ u32x3 load_row(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff)
+// One active expert of a call: its id, route count, first sorted position and matrix addresses.
+struct ExpertRec
 {
-    return __builtin_amdgcn_raw_buffer_load_b96(r, voff, soff, 2);
-}
-
-struct GemvArgs
-{
-    const int64_t* wptr0;     // gate (mode 0) or down (mode 1) pointer table
-    const int64_t* wptr1;     // up (mode 0)
-    const uint16_t* suh13;    // [E][2][H]
-    const uint16_t* xin;      // mode 0: x fp16 [T][H]; mode 1: xd fp16 [n][I] (flat route order)
-    const int64_t* ids;       // [n] route expert ids
-    const int32_t* offsets;   // [E+2] or null (then in-kernel routing)
-    const int32_t* order;     // [n]
-    const int32_t* active;    // [E]
-    const int32_t* nactive;   // [1]
-    float* part;              // [kparts][n][nmat][N] partial sums
-    int H, I, E, n, topk;
-    int K, N, ncb, kparts, max_active;
+    int32_t e, cnt, first, pad;
+    int64_t w[3];             // gate, up, down trellis
+    int64_t pad2;
 };
 
-// One lane's share of a tile row: 32 trellis states -> 32 fp16 weights -> dot products with the transformed
-// inputs of nr routes.
-// Window d0:d1:d2:d3 = tile dwords 3c-1 .. 3c+2 (d0 most significant); state m (stream index 32c + m) has its
-// LSB at bit 93 - 3m. Every 16-bit field lies inside one of d1..d3 or one of the dwords straddling their
-// boundaries (bits 16..47, 48..79, 80..111 of the window), so each state is one v_bfe_u32.
-// The (1024 + bytesum) fp16 operands of a pair are produced packed by v_sad_u8 / v_sad_hi_u8 with 0x6400 in
-// both halves of the accumulator, then one v_pk_fma_f16 applies KINV, KBIAS with a single rounding.
-// States 8q+2j, 8q+2j+1 (j = 0..3) hold rows (2q, 2q+1) for j even and (2q+8, 2q+9) for j odd, of column c
-// (j < 2) or c + 8 (j >= 2) (PERM, ft_core.h:48-61); X[r][d] is the fp16 input pair of rows (2d, 2d+1) of
-// route r, so pair j meets X[r][q + 4 * (j & 1)] and accumulates into column j >> 1.
-template <int MT>
-__device__ __forceinline__ void decode_dot(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3,
-                                          const uint32_t (*X)[8], int nr, float (*acc)[MT])
+__device__ __forceinline__ float kinv_f() { return h2f(KINV_BITS); }
+__device__ __forceinline__ float kbias_f() { return h2f(KBIAS_BITS); }
+
+// Row ranges per segment of a partial launch: as many equal pieces as fit one wave each (at least 1, at most
+// cap). Kernels 2-5 derive it from the same inputs, so they agree on the layout of the partial sums.
+__device__ __forceinline__ int pieces_per_segment(int nwaves, int nseg, int cap)
 {
-    const half2_t kinv = { __builtin_bit_cast(_Float16, KINV_BITS), __builtin_bit_cast(_Float16, KINV_BITS) };
-    const half2_t kbias = { __builtin_bit_cast(_Float16, KBIAS_BITS), __builtin_bit_cast(_Float16, KBIAS_BITS) };
-    const uint32_t mid[3] = { __builtin_amdgcn_alignbit(d2, d3, 16), __builtin_amdgcn_alignbit(d1, d2, 16),
-                              __builtin_amdgcn_alignbit(d0, d1, 16) };   // window bits 16.., 48.., 80..
-    const uint32_t dw[3] = { d3, d2, d1 };                              // window bits 0.., 32.., 64..
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-        {
-            uint32_t p[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-            {
-                const int m = 8 * q + 2 * j + h;
-                const int sft = 93 - 3 * m;
-                const uint32_t st = (sft & 31) <= 16 ? __builtin_amdgcn_ubfe(dw[sft >> 5], sft & 31, 16)
-                                                     : __builtin_amdgcn_ubfe(mid[(sft - 16) >> 5], (sft - 16) & 31, 16);
-                p[h] = st * MUL1;
-            }
-            const uint32_t lo = __builtin_amdgcn_sad_u8(p[0], 0u, 0x64006400u);
-            const uint32_t pk = __builtin_amdgcn_sad_hi_u8(p[1], 0u, lo);
-            const half2_t wv = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, pk), kinv, kbias);
-#pragma unroll
-            for (int r = 0; r < MT; ++r)
-            {
-                if (r >= nr) break;
-                acc[j >> 1][r] = __builtin_amdgcn_fdot2(wv, __builtin_bit_cast(half2_t, X[r][q + 4 * (j & 1)]), acc[j >> 1][r], false);
-            }
-        }
+    const int p = nseg > 0 ? nwaves / nseg : 1;
+    return p < 1 ? 1 : (p > cap ? cap : p);
 }
 
-// The same decode without the dot products: 16 packed fp16 weight pairs in the order of decode_dot's pairs
-// (pair 4q + j = states 8q + 2j, 8q + 2j + 1).
-__device__ __forceinline__ void decode_pairs(uint32_t d0, uint32_t d1, uint32_t d2, uint32_t d3, half2_t* wv)
-{
-    const half2_t kinv = { __builtin_bit_cast(_Float16, KINV_BITS), __builtin_bit_cast(_Float16, KINV_BITS) };
-    const half2_t kbias = { __builtin_bit_cast(_Float16, KBIAS_BITS), __builtin_bit_cast(_Float16, KBIAS_BITS) };
-    const uint32_t mid[3] = { __builtin_amdgcn_alignbit(d2, d3, 16), __builtin_amdgcn_alignbit(d1, d2, 16),
-                              __builtin_amdgcn_alignbit(d0, d1, 16) };
-    const uint32_t dw[3] = { d3, d2, d1 };
-#pragma unroll
-    for (int q = 0; q < 4; ++q)
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-        {
-            uint32_t p[2];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-            {
-                const int m = 8 * q + 2 * j + h;
-                const int sft = 93 - 3 * m;
-                const uint32_t st = (sft & 31) <= 16 ? __builtin_amdgcn_ubfe(dw[sft >> 5], sft & 31, 16)
-                                                     : __builtin_amdgcn_ubfe(mid[(sft - 16) >> 5], (sft - 16) & 31, 16);
-                p[h] = st * MUL1;
-            }
-            const uint32_t lo = __builtin_amdgcn_sad_u8(p[0], 0u, 0x64006400u);
-            const uint32_t pk = __builtin_amdgcn_sad_hi_u8(p[1], 0u, lo);
-            wv[4 * q + j] = __builtin_elementwise_fma(__builtin_bit_cast(half2_t, pk), kinv, kbias);
-        }
-}
+// ------------------------------------------------------------------------------------------------ decode
 
-__device__ __forceinline__ int block_excl_scan(int v, int* tmp, int* total)
+// The multiply-accumulate runs on v_mfma_f32_16x16x32_f16 over two tile rows at a time: A = transformed inputs
+// [16 routes][32 rows], B = two decoded 16x16 tiles stacked along k, D = [16 routes][16 columns]. Lane l of B
+// holds column n = l & 15 and MFMA k-group g = l >> 4 (8 values). A dot product does not depend on the order of
+// its terms, so the k-group need not be adjacent rows: k-group g is rows (2g, 2g+1, 2g+8, 2g+9) of the first tile
+// and the same rows of the second, which in column n are the 4 consecutive trellis states i0 .. i0+3 of each
+// tile with i0 = 32 (n & 7) + 8 g + 4 (n >> 3) (PERM, ft_core.h:48-61). A carries the same rows of the inputs,
+// so each lane decodes 4 adjacent states per tile and nothing moves between lanes.
+//
+// The 4 states span 25 stream bits ending at e = 3 i0 + 11, which lie in tile dwords b - 1 and b (b = e >> 5;
+// dword -1 is dword 23: the stream wraps). One v_alignbit puts state i0 + 3 - j at bits 3j .. 3j + 15.
+// The (1024 + bytesum) fp16 codes of a state pair come out packed from v_sad_u8 / v_sad_hi_u8 with 0x6400 in
+// both accumulator halves; EXACT applies KINV, KBIAS with one v_pk_fma_f16 (a single rounding).
+template <bool EXACT>
+__device__ __forceinline__ half4_t decode4(uint32_t hi, uint32_t lo, uint32_t sh)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    int incl = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1)
+    const uint32_t X = __builtin_amdgcn_alignbit(hi, lo, sh);
+    const uint32_t p0 = __builtin_amdgcn_ubfe(X, 9, 16) * MUL1;
+    const uint32_t p1 = __builtin_amdgcn_ubfe(X, 6, 16) * MUL1;
+    const uint32_t p2 = __builtin_amdgcn_ubfe(X, 3, 16) * MUL1;
+    const uint32_t p3 = (X & 0xffffu) * MUL1;
+    const uint32_t v01 = __builtin_amdgcn_sad_hi_u8(p1, 0u, __builtin_amdgcn_sad_u8(p0, 0u, 0x64006400u));
+    const uint32_t v23 = __builtin_amdgcn_sad_hi_u8(p3, 0u, __builtin_amdgcn_sad_u8(p2, 0u, 0x64006400u));
+    half2_t w01 = __builtin_bit_cast(half2_t, v01), w23 = __builtin_bit_cast(half2_t, v23);
+    if constexpr (EXACT)
     {
-        const int o = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += o;
+        const half2_t kinv = { __builtin_bit_cast(_Float16, KINV_BITS), __builtin_bit_cast(_Float16, KINV_BITS) };
+        const half2_t kbias = { __builtin_bit_cast(_Float16, KBIAS_BITS), __builtin_bit_cast(_Float16, KBIAS_BITS) };
+        w01 = __builtin_elementwise_fma(w01, kinv, kbias);
+        w23 = __builtin_elementwise_fma(w23, kinv, kbias);
     }
+    return half4_t{ w01[0], w01[1], w23[0], w23[1] };
+}
+
+// MFMA operand order of each 16-row group of an input row: dword 2g + h holds rows (2g + 8h, 2g + 8h + 1), so
+// the lane of k-group g reads its four rows (2g, 2g+1, 2g+8, 2g+9) with one 8-byte load.
+__device__ __forceinline__ int operand_index(int k)
+{
+    const int d = (k & 15) >> 1;
+    return (k & ~15) + 2 * (2 * (d & 3) + (d >> 2)) + (k & 1);
+}
+
+// Waits written as inline asm with a memory clobber, so the compiler neither moves LDS accesses across them
+// nor drops them: buffer-to-LDS loads are counted by vmcnt but their LDS writes are invisible to the compiler.
+template <int N>
+__device__ __forceinline__ void wait_vmcnt()
+{
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+// ------------------------------------------------------------------------------------------ 1. route prep
+
+struct PrepArgs
+{
+    const void* x;            // [T][H], element type x_dtype
+    const int64_t* ids;       // [n]
+    const int32_t* offsets;   // permutation (null: routing found here from ids)
+    const int32_t* order;
+    const int32_t* active;
+    const int32_t* nactive_in;
+    const int64_t* wtab0;     // gate, up, down pointer tables
+    const int64_t* wtab1;
+    const int64_t* wtab2;
+    const uint16_t* suh13;    // [E][2][H]
+    ExpertRec* rec;           // [max_active]
+    int32_t* counts;          // [2]: active experts, routed (valid) routes
+    int32_t* pos_of;          // [n] sorted position of each route, -1 if its id is outside [0, E)
+    int32_t* route_at;        // [n] route at each sorted position
+    uint16_t* xa;             // [n][2][H] fp16 in operand order
+    float* xsum;              // [n][2][nb] sums of xa over each workgroup's rows
+    int n, topk, E, H, nb, x_dtype, rescale;
+};
+
+__device__ __forceinline__ float load_x(const void* x, int dtype, size_t i)
+{
+    if (dtype == MM_DTYPE_F16) return h2f(static_cast<const uint16_t*>(x)[i]);
+    if (dtype == MM_DTYPE_BF16) return __uint_as_float((uint32_t) static_cast<const uint16_t*>(x)[i] << 16);
+    return static_cast<const float*>(x)[i];
+}
+
+__device__ __forceinline__ int block_sum_int(int v, int (*tmp)[4], int slot)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    if (lane == 0) tmp[wave][slot] = v;
     __syncthreads();
-    if (lane == 63) tmp[wave] = incl;
-    __syncthreads();
-    int before = 0, all = 0;
-    for (int w = 0; w < nw; ++w)
-    {
-        const int s = tmp[w];
-        if (w < wave) before += s;
-        all += s;
-    }
-    *total = all;
-    return before + incl - v;
+    return tmp[0][slot] + tmp[1][slot] + tmp[2][slot] + tmp[3][slot];
 }
 
-// Main loop for exactly NR routes (a compile-time count: no per-route branches inside the unrolled loop, which
-// keeps the register allocation tight). Decodes this wave's tile rows of the K part and leaves the wave's partial
-// sums for its 128 columns in red[wave][r][col].
-template <int NR>
-__device__ __forceinline__ void gemv_rows(__amdgpu_buffer_rsrc_t wres, uint32_t voff, uint32_t row0, uint32_t row_bytes,
-                                          int nit, int wpm, int kw, int src_lane, const uint32_t* xm, int xrow,
-                                          float* red, int wave, int col0, int mt)
+__global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
 {
-    float acc[2][NR];
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int r = 0; r < NR; ++r) acc[c][r] = 0.0f;
-    auto step = [&](uint32_t d1, uint32_t d2, uint32_t d3, int t) {
-        const int tr = kw + t * wpm;
-        const uint32_t d0 = __shfl(d3, src_lane, 64);
-        if constexpr (NR == 1)
-        {
-            // one route: the pairs feed the dot products as they are decoded
-            uint32_t X[1][8];
-            const uint4 xa = *reinterpret_cast<const uint4*>(xm + tr * 8);
-            const uint4 xb = *reinterpret_cast<const uint4*>(xm + tr * 8 + 4);
-            X[0][0] = xa.x; X[0][1] = xa.y; X[0][2] = xa.z; X[0][3] = xa.w;
-            X[0][4] = xb.x; X[0][5] = xb.y; X[0][6] = xb.z; X[0][7] = xb.w;
-            decode_dot<1>(d0, d1, d2, d3, X, 1, acc);
-        }
-        else
-        {
-            // several routes: decode once, then one route at a time (its inputs loaded just in time)
-            half2_t wv[16];
-            decode_pairs(d0, d1, d2, d3, wv);
-#pragma unroll
-            for (int r = 0; r < NR; ++r)
-            {
-                const uint4 xa = *reinterpret_cast<const uint4*>(xm + (size_t)r * xrow + tr * 8);
-                const uint4 xb = *reinterpret_cast<const uint4*>(xm + (size_t)r * xrow + tr * 8 + 4);
-                const uint32_t X[8] = { xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w };
-                float c0 = acc[0][r], c1 = acc[1][r];
-#pragma unroll
-                for (int q = 0; q < 4; ++q)
-                {
-                    c0 = __builtin_amdgcn_fdot2(wv[4 * q + 0], __builtin_bit_cast(half2_t, X[q]), c0, false);
-                    c0 = __builtin_amdgcn_fdot2(wv[4 * q + 1], __builtin_bit_cast(half2_t, X[q + 4]), c0, false);
-                    c1 = __builtin_amdgcn_fdot2(wv[4 * q + 2], __builtin_bit_cast(half2_t, X[q]), c1, false);
-                    c1 = __builtin_amdgcn_fdot2(wv[4 * q + 3], __builtin_bit_cast(half2_t, X[q + 4]), c1, false);
-                }
-                acc[0][r] = c0;
-                acc[1][r] = c1;
-            }
-        }
-    };
-    // Two register sets of GV_PF rows alternate: while one set is decoded the other set's loads are in flight, and
-    // a set is refilled only after it has been consumed, so no register copy (and no drain of the load queue) is
-    // needed at the loop back-edge. The refill past this wave's last row re-reads an in-range row; the remaining
-    // nit % (2 GV_PF) rows run unpipelined.
-    const int ngroups = (nit / (2 * GV_PF)) * 2;
-    u32x3 ra[GV_PF], rb[GV_PF];
-    auto load_set = [&](u32x3* rg, int g) {
-#pragma unroll
-        for (int j = 0; j < GV_PF; ++j)
-            rg[j] = load_row(wres, voff, (row0 + (uint32_t)(min(g * GV_PF + j, nit - 1) * wpm)) * row_bytes);
-    };
-    auto run_set = [&](u32x3* rg, int g) {
-#pragma unroll
-        for (int j = 0; j < GV_PF; ++j)
-        {
-            step(rg[j].x, rg[j].y, rg[j].z, g * GV_PF + j);
-            // keep each tile row's decode within its step: bounds the live registers
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    };
-    if (ngroups > 0) load_set(ra, 0);
-    for (int g = 0; g < ngroups; g += 2)
-    {
-        load_set(rb, g + 1);
-        run_set(ra, g);
-        load_set(ra, g + 2);
-        run_set(rb, g + 1);
-    }
-    for (int t = ngroups * GV_PF; t < nit; ++t)
-    {
-        const u32x3 v = load_row(wres, voff, (row0 + (uint32_t)(t * wpm)) * row_bytes);
-        step(v.x, v.y, v.z, t);
-    }
-    __syncthreads();      // every wave is done reading the LDS inputs before they are overwritten
-#pragma unroll
-    for (int r = 0; r < NR; ++r)
-    {
-        float* rr = red + ((size_t)wave * mt + r) * GV_COLS;
-        rr[col0] = acc[0][r];
-        rr[col0 + 8] = acc[1][r];
-    }
-}
-
-template <int MODE, int MT>
-__global__ __launch_bounds__(GV_THREADS, MT == 1 ? 8 : 4) void k_expert_partial(GemvArgs a)
-{
-    constexpr int NMAT = MODE == 0 ? 2 : 1;
-    constexpr int WPM = GV_WAVES / NMAT;          // waves per matrix (gate on the first half, up on the second)
-    __shared__ __align__(16) uint32_t lds[NMAT * MT * GV_KPART / 2];   // transformed inputs, then the reduction
     __shared__ uint32_t s_bm[32];
-    __shared__ int s_tmp[16];
-    __shared__ int s_e, s_cnt;
-    __shared__ int s_rows[GV_MAX_ROWS];
-    static_assert(NMAT * MT * GV_KPART * 2 >= GV_WAVES * MT * GV_COLS * 4, "LDS reuse");
-
-    // the wave index is uniform across the wave: readfirstlane keeps the loop bounds in SGPRs, so the K loop
-    // branches on scalars and the in-flight loads are not drained at every step
-    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int kq = blockIdx.x % a.kparts;
-    const int unit = blockIdx.x / a.kparts;
-    const int a_idx = unit / a.ncb, cb = unit % a.ncb;
-    if (a_idx >= a.max_active) return;
-
-    // ---- routing: this unit's expert and its routes (flat route indices, ascending)
-    if (a.offsets)
+    __shared__ int s_red[4][4];
+    __shared__ float s_ss[4];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int blk = blockIdx.x % a.nb, m = (blockIdx.x / a.nb) & 1, idx = blockIdx.x / (2 * a.nb);
+    const bool writer = m == 0 && blk == 0;      // the one workgroup of a route that writes its routing data
+    int s, pos, e;
+    if (!a.offsets)
     {
-        if (threadIdx.x == 0)
-        {
-            const int na = a.nactive[0];
-            s_e = a_idx < na ? a.active[a_idx] : -1;
-            s_cnt = s_e >= 0 ? min(GV_MAX_ROWS, a.offsets[s_e + 1] - a.offsets[s_e]) : 0;
-        }
+        // routing from the ids: position = routes of lower experts + earlier routes of the same expert
+        if (tid < 32) s_bm[tid] = 0;
         __syncthreads();
-        if (s_e < 0) return;
-        for (int r = threadIdx.x; r < s_cnt; r += GV_THREADS) s_rows[r] = a.order[a.offsets[s_e] + r];
+        s = idx;
+        const int64_t e64 = a.ids[s];
+        const bool valid = e64 >= 0 && e64 < a.E;
+        e = valid ? (int)e64 : -1;
+        int less = 0, same = 0, rank = 0, nv = 0;
+        for (int i = tid; i < a.n; i += 256)
+        {
+            const int64_t v = a.ids[i];
+            if (v < 0 || v >= a.E) continue;
+            atomicOr(&s_bm[v >> 5], 1u << (v & 31));
+            nv += 1;
+            less += v < e;
+            same += v == e;
+            rank += (v == e) && (i < s);
+        }
+        less = block_sum_int(less, s_red, 0);
+        same = block_sum_int(same, s_red, 1);
+        rank = block_sum_int(rank, s_red, 2);
+        nv = block_sum_int(nv, s_red, 3);
+        if (tid == 0 && (writer || blockIdx.x == 0))
+        {
+            int nact = 0, below = 0;
+            for (int wd = 0; wd < 32; ++wd)
+            {
+                const uint32_t bits = s_bm[wd];
+                nact += __popc(bits);
+                if (valid && wd < (e >> 5)) below += __popc(bits);
+            }
+            if (blockIdx.x == 0)
+            {
+                a.counts[0] = nact;
+                a.counts[1] = nv;
+            }
+            if (writer)
+            {
+                if (!valid)
+                    a.pos_of[s] = -1;
+                else
+                {
+                    a.pos_of[s] = less + rank;
+                    a.route_at[less + rank] = s;
+                    if (rank == 0)
+                    {
+                        below += __popc(s_bm[e >> 5] & ((1u << (e & 31)) - 1u));
+                        ExpertRec r{ e, same, less, 0, { a.wtab0[e], a.wtab1[e], a.wtab2[e] }, 0 };
+                        a.rec[below] = r;
+                    }
+                }
+            }
+        }
+        if (!valid) return;
+        pos = less + rank;
     }
     else
     {
-        if (threadIdx.x < 32) s_bm[threadIdx.x] = 0;
-        __syncthreads();
-        for (int s = threadIdx.x; s < a.n; s += GV_THREADS)
+        // routing from the permutation: the workgroups of index idx own sorted position idx
+        pos = idx;
+        const int nvalid = a.offsets[a.E];
+        s = a.order[pos];
+        if (tid == 0)
         {
-            const int64_t e = a.ids[s];
-            if (e >= 0 && e < a.E) atomicOr(&s_bm[e >> 5], 1u << (e & 31));
-        }
-        __syncthreads();
-        if (wave == 0)
-        {
-            const int c = lane < 32 ? __popc(s_bm[lane]) : 0;
-            int incl = c;
-#pragma unroll
-            for (int d = 1; d < 32; d <<= 1)
+            if (blockIdx.x == 0)
             {
-                const int o = __shfl_up(incl, d, 64);
-                if (lane >= d) incl += o;
+                a.counts[0] = a.nactive_in[0];
+                a.counts[1] = nvalid;
             }
-            // the word holding the a_idx-th set bit (0-based)
-            const bool here = lane < 32 && a_idx >= incl - c && a_idx < incl;
-            if (lane == 0) s_e = -1;
-            if (here)
+            if (writer)
             {
-                uint32_t bits = s_bm[lane];
-                for (int k = a_idx - (incl - c); k > 0; --k) bits &= bits - 1;
-                s_e = lane * 32 + __ffs(bits) - 1;
+                a.pos_of[s] = pos < nvalid ? pos : -1;
+                if (pos < nvalid) a.route_at[pos] = s;
             }
         }
-        __syncthreads();
-        if (s_e < 0) return;
-        const int e = s_e;
-        int base = 0;
-        for (int s0 = 0; s0 < a.n; s0 += GV_THREADS)
+        if (pos >= nvalid) return;
+        e = (int)a.ids[s];
+        if (tid == 0 && writer && pos == a.offsets[e])
         {
-            const int s = s0 + threadIdx.x;
-            const bool f = s < a.n && a.ids[s] == e;
-            int tot;
-            const int pos = block_excl_scan(f ? 1 : 0, s_tmp, &tot);
-            if (f && base + pos < GV_MAX_ROWS) s_rows[base + pos] = s;
-            base += tot;
+            const int na = a.nactive_in[0];
+            int ai = 0;
+            while (ai < na && a.active[ai] != e) ++ai;
+            if (ai < na)
+            {
+                ExpertRec r{ e, a.offsets[e + 1] - pos, pos, 0, { a.wtab0[e], a.wtab1[e], a.wtab2[e] }, 0 };
+                a.rec[ai] = r;
+            }
         }
-        if (threadIdx.x == 0) s_cnt = min(base, GV_MAX_ROWS);
     }
-    __syncthreads();
-    const int e = __builtin_amdgcn_readfirstlane(s_e), cnt = __builtin_amdgcn_readfirstlane(s_cnt);
 
-    const int k0 = kq * GV_KPART, klen = min(GV_KPART, a.K - k0);
-    const int KTp = klen / 16, NT = a.N / 16;
-    const int tau = lane >> 3, cp = lane & 7;
-    const int src_lane = cp == 0 ? lane + 7 : lane - 1;
-    const int mw = wave / WPM, kw = wave % WPM;   // this wave's matrix and its K slot
-    const int64_t* wtab = (NMAT == 2 && mw == 1) ? a.wptr1 : a.wptr0;
-    const size_t row_stride = (size_t)NT * 24;   // dwords between tile rows
-    // the matrix base is wave-uniform; readfirstlane puts it (and so the descriptor) in SGPRs. readfirstlane
-    // returns int: each half goes through uint32_t before widening, or a low word >= 2^31 would sign-extend
-    // into the high word and the descriptor would point at a wild address.
-    const uint64_t wp = (uint64_t)wtab[e];
-    const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)wp);
-    const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(wp >> 32));
-    const uint64_t wpu = (uint64_t)wlo | ((uint64_t)whi << 32);
-    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-        reinterpret_cast<void*>((uintptr_t)wpu), (short)0, (int)((size_t)(a.K / 16) * row_stride * 4), BUF_DWORD3);
-    const uint32_t voff = (uint32_t)(((cb * 8 + tau) * 24 + 3 * cp) * 4);      // bytes within a tile row
-    const uint32_t row_bytes = (uint32_t)(row_stride * 4);
-    constexpr int xrow = GV_KPART / 2;            // dwords per transformed input row in LDS
-
-    for (int r0 = 0; r0 < cnt; r0 += MT)
+    // the route's expert input: x16 = fp16(bf16(x_t * s_t)) (fp16 input without rescale is taken as is);
+    // s_t = 1 / RMS(x_t) in the reduction order of mm_prepare_input
+    const int t = s / a.topk;
+    const size_t row = (size_t)t * a.H;
+    float scale = 1.0f;
+    if (a.rescale)
     {
-        const int nr = min(MT, cnt - r0);
-        __syncthreads();
-        // ---- prologue: transformed inputs (fp16) of this K part, rows r0 .. r0+nr-1
-        uint16_t* xt = reinterpret_cast<uint16_t*>(lds);
-        if constexpr (MODE == 0)
+        float ss = 0.0f;
+        for (int h = tid; h < a.H; h += 256)
         {
-            const int nblk = klen / 128;
-            const int items = NMAT * nr * nblk;
-            for (int it0 = wave; it0 < items; it0 += 4 * GV_WAVES)
-            {
-                float va[4], vb[4], sa[4], sb[4];
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                {
-                    const int it = it0 + u * GV_WAVES;
-                    if (it < items)
-                    {
-                        const int m = it / (nr * nblk), r = (it / nblk) % nr, blk = it % nblk;
-                        const int tok = s_rows[r0 + r] / a.topk;
-                        const uint16_t* xr = a.xin + (size_t)tok * a.H + k0 + blk * 128;
-                        const uint16_t* su = a.suh13 + ((size_t)e * 2 + m) * a.H + k0 + blk * 128;
-                        va[u] = h2f(xr[lane]); vb[u] = h2f(xr[lane + 64]);
-                        sa[u] = h2f(su[lane]); sb[u] = h2f(su[lane + 64]);
-                    }
-                }
-#pragma unroll
-                for (int u = 0; u < 4; ++u)
-                {
-                    const int it = it0 + u * GV_WAVES;
-                    if (it < items)
-                    {
-                        const int m = it / (nr * nblk), r = (it / nblk) % nr, blk = it % nblk;
-                        prep_block_wave(va[u], vb[u], sa[u], sb[u]);
-                        uint16_t* dst = xt + ((size_t)m * MT + r) * GV_KPART + blk * 128;
-                        dst[lane] = f2h(va[u]);
-                        dst[lane + 64] = f2h(vb[u]);
-                    }
-                }
-            }
+            const float v = load_x(a.x, a.x_dtype, row + h);
+            ss = fmaf(v, v, ss);
         }
-        else
-        {
-            const int nd = klen / 2;
-            for (int i = threadIdx.x; i < nr * nd; i += GV_THREADS)
-            {
-                const int r = i / nd, c = i % nd;
-                lds[r * xrow + c] = reinterpret_cast<const uint32_t*>(a.xin + (size_t)s_rows[r0 + r] * a.I + k0)[c];
-            }
-        }
+        for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
+        if (lane == 0) s_ss[wave] = ss;
         __syncthreads();
+        const float tot = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
+        scale = tot > 0.0f ? 1.0f / sqrtf(tot / (float)a.H) : 1.0f;
+        __syncthreads();      // s_ss is reused below
+    }
+    const bool as_is = a.x_dtype == MM_DTYPE_F16 && !a.rescale;
+    const uint16_t* su = a.suh13 + ((size_t)e * 2 + m) * a.H;
+    uint16_t* dst = a.xa + ((size_t)pos * 2 + m) * a.H;
+    const int h0 = blk * PREP_ROWS + wave * 128;
+    float bsum = 0.0f;
+    if (h0 < a.H)
+    {
+        float va = load_x(a.x, a.x_dtype, row + h0 + lane);
+        float vb = load_x(a.x, a.x_dtype, row + h0 + lane + 64);
+        if (!as_is)
+        {
+            va = r16(bf16_value(va * scale));
+            vb = r16(bf16_value(vb * scale));
+        }
+        prep_block_wave(va, vb, h2f(su[h0 + lane]), h2f(su[h0 + lane + 64]));
+        dst[operand_index(h0 + lane)] = f2h(va);
+        dst[operand_index(h0 + lane + 64)] = f2h(vb);
+        bsum = wave_sum(va + vb);
+    }
+    if (lane == 0) s_ss[wave] = bsum;
+    __syncthreads();
+    if (tid == 0) a.xsum[((size_t)pos * 2 + m) * a.nb + blk] = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
+}
 
-        // ---- main loop (specialised for the route count) and the waves' partial sums into LDS
+// ------------------------------------------------------------------------------------ 2/4. partial sums
+
+struct PartArgs
+{
+    const ExpertRec* rec;
+    const int32_t* counts;
+    const uint16_t* xa;       // mode 0: [n][2][K]; mode 1: [n][K] (operand order)
+    float* part;              // [pieces][n][nmat][N]
+    int n, K, N, ncb, cap;
+};
+
+template <int MODE, bool EXACT>
+__global__ __launch_bounds__(GV_THREADS, 4) void k_partial(PartArgs a)
+{
+    constexpr int NMAT = MODE == 0 ? 2 : 1;
+    // A 12-byte buffer-to-LDS load writes lane i's bytes at slot + 16 i (the fourth dword of each lane's 16 is
+    // left untouched), so a tile row occupies 1024 bytes: tile c's dword w sits at dword 32 c + 4 (w / 3) + w % 3.
+    constexpr int SLOT = 256;                     // dwords per ring slot
+    __shared__ __align__(16) uint32_t ring[GV_WAVES * GV_RING * SLOT];
+
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // consecutive pieces (the row ranges of one segment, then adjacent 768-byte column chunks: the same
+    // inputs) go to one XCD; workgroups are dealt to the 8 XCDs round-robin
+    const int nb = gridDim.x;
+    const int b = (nb & 7) == 0 ? (int)(blockIdx.x & 7) * (nb >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
+    const int nwaves = nb * GV_WAVES;
+    const int nseg = a.counts[0] * NMAT * a.ncb;
+    const int pps = pieces_per_segment(nwaves, nseg, a.cap);
+    const int KT = a.K / 16, NT = a.N / 16;
+    const uint32_t row_bytes = (uint32_t)NT * 96;
+    const uint32_t wbytes = (uint32_t)KT * row_bytes;                   // one matrix
+    const uint32_t xbytes = (uint32_t)((size_t)a.n * NMAT * a.K * 2);   // the input array
+    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xa), (short)0,
+                                                                          (int)xbytes, 0x00020000);
+    // lane constants of the decode
+    const int col = lane & 15, g = lane >> 4;
+    const int i0 = 32 * (col & 7) + 8 * g + 4 * (col >> 3);
+    const int eb = 3 * i0 + 11;
+    const int blo = eb >> 5, bhi = (blo + 23) % 24;
+    const int llo = 4 * (blo / 3) + blo % 3, lhi = 4 * (bhi / 3) + bhi % 3;     // their places in a staged tile
+    const uint32_t sh = 31u - (uint32_t)(eb & 31);
+
+    for (int p = b * GV_WAVES + wave; p < nseg * pps; p += nwaves)
+    {
+        const int seg = p / pps, piece = p % pps;
+        const int cb = seg % a.ncb, r = seg / a.ncb;
+        const int m = r % NMAT, ai = r / NMAT;
+        const int tr0 = piece * KT / pps, nrow = (piece + 1) * KT / pps - tr0;
+        const ExpertRec rc = a.rec[ai];
+        const int cnt = min(rc.cnt, GV_MAX_ROWS);
+        // per-matrix buffer descriptor in SGPRs. readfirstlane returns int: each half goes through uint32_t
+        // before widening, or a low word >= 2^31 would sign-extend into the high word.
+        const uint64_t wp = (uint64_t)rc.w[MODE == 0 ? m : 2];
+        const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)wp);
+        const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(wp >> 32));
+        const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
+            reinterpret_cast<void*>((uintptr_t)((uint64_t)wlo | ((uint64_t)whi << 32))), (short)0, (int)wbytes,
+            0x00020000);
+        const uint32_t wcol = (uint32_t)cb * ROW_BYTES;
+
+        for (int r0 = 0; r0 < cnt; r0 += 16)
         {
-            const int nit = (KTp - kw + WPM - 1) / WPM;   // tile rows of this wave
-            const uint32_t row0 = (uint32_t)(k0 / 16 + kw);
-            const uint32_t* xm = lds + (size_t)mw * MT * xrow;
-            float* red = reinterpret_cast<float*>(lds);
-            const int col0 = tau * 16 + cp;
-#define MM_ROWS_CASE(R) case R: if constexpr (R <= MT) gemv_rows<R>(wres, voff, row0, row_bytes, nit, WPM, kw, src_lane, xm, xrow, red, wave, col0, MT); break;
-            switch (nr)
-            {
-                MM_ROWS_CASE(1)
-                MM_ROWS_CASE(2)
-                MM_ROWS_CASE(3)
-                MM_ROWS_CASE(4)
-                MM_ROWS_CASE(5)
-                MM_ROWS_CASE(6)
-                MM_ROWS_CASE(7)
-                default: gemv_rows<MT>(wres, voff, row0, row_bytes, nit, WPM, kw, src_lane, xm, xrow, red, wave, col0, MT); break;
-            }
-#undef MM_ROWS_CASE
-        }
-        __syncthreads();
-        const float* red = reinterpret_cast<const float*>(lds);
-        for (int i = threadIdx.x; i < NMAT * nr * GV_COLS; i += GV_THREADS)
-        {
-            const int m = i / (nr * GV_COLS), r = (i / GV_COLS) % nr, c = i % GV_COLS;
-            float sum = 0.0f;
+            const int nr = min(16, cnt - r0);
+            // this lane's A row: routes past nr repeat a valid one and their outputs are never stored
+            const int pos = rc.first + r0 + min(col, nr - 1);
+            const uint32_t xoff = (uint32_t)(((size_t)pos * NMAT + m) * a.K * 2) + (uint32_t)g * 8;
+            float4_t acc[8];
 #pragma unroll
-            for (int w = 0; w < WPM; ++w) sum += red[((size_t)(m * WPM + w) * MT + r) * GV_COLS + c];
-            const int s = s_rows[r0 + r];
-            a.part[(((size_t)kq * a.n + s) * NMAT + m) * a.N + cb * GV_COLS + c] = sum;
+            for (int c = 0; c < 8; ++c) acc[c] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+            uint2 areg[GV_RING];
+            // row t of the range: one 768-byte trellis load into ring slot j and the lane's 8 input bytes.
+            // Rows past the range are issued with offsets beyond the buffers, which the buffer unit answers with
+            // zeros and no memory access, so every row keeps the same two loads and the waits stay uniform.
+            auto issue = [&](int j, int t) {
+                const bool in = t < nrow;
+                const uint32_t tr = (uint32_t)(tr0 + t);
+                __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, &ring[(wave * GV_RING + j) * SLOT], 12,
+                                                         (uint32_t)lane * 12, in ? tr * row_bytes + wcol : wbytes, 0, 0);
+                areg[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xres, xoff, in ? tr * 32 : xbytes, 0));
+            };
+            // rows j and j + 1 (ring slots) through one MFMA per tile; a row past the range has zero inputs
+            auto pair_mma = [&](int j) {
+                const uint32_t* s0 = &ring[(wave * GV_RING + j) * SLOT];
+                const uint32_t* s1 = s0 + SLOT;
+                const half4_t a0 = __builtin_bit_cast(half4_t, areg[j]), a1 = __builtin_bit_cast(half4_t, areg[j + 1]);
+                const half8_t A = { a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3] };
+#pragma unroll
+                for (int c = 0; c < 8; ++c)
+                {
+                    const half4_t b0 = decode4<EXACT>(s0[c * 32 + lhi], s0[c * 32 + llo], sh);
+                    const half4_t b1 = decode4<EXACT>(s1[c * 32 + lhi], s1[c * 32 + llo], sh);
+                    const half8_t B = { b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3] };
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[c], 0, 0, 0);
+                }
+            };
+#pragma unroll
+            for (int j = 0; j < GV_RING; ++j) issue(j, j);
+            // rows t and t + 1 hold the oldest 4 of the 2 GV_RING loads in flight; their slots are refilled with
+            // rows t + GV_RING and t + GV_RING + 1 once the slots' LDS reads have returned
+            for (int t0 = 0; t0 < nrow; t0 += GV_RING)
+            {
+#pragma unroll
+                for (int j = 0; j < GV_RING; j += 2)
+                {
+                    if (t0 + j < nrow)
+                    {
+                        wait_vmcnt<2 * (GV_RING - 2)>();
+                        pair_mma(j);
+                        wait_lgkm0();
+                    }
+                    issue(j, t0 + j + GV_RING);
+                    issue(j + 1, t0 + j + 1 + GV_RING);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+            wait_vmcnt<0>();      // the trailing (empty) loads, so the ring is quiet when it is reused or left
+
+            // D layout: lane (column col, group g) holds routes 4g .. 4g+3 of column col of each tile
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+            {
+                const int rr = 4 * g + v;
+                if (rr < nr)
+                {
+                    float* dst = a.part + ((size_t)(piece * a.n + rc.first + r0 + rr) * NMAT + m) * a.N + cb * GV_COLS + col;
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) dst[c * 16] = acc[c][v];
+                }
+            }
         }
     }
 }
 
-// Gate/up epilogue, one wave per (route, 128-column block of I): K parts added in order, output transforms,
-// SwiGLU, down-input transform -> xd fp16 [n][I].
+// ------------------------------------------------------------------------------------ 3. gate/up epilogue
+
 struct GuEpiArgs
 {
-    const float* part;        // [kparts][n][2][I]
+    const float* part;        // [pieces][n][2][I]
+    const float* xsum;        // [n][2][nb]
+    const int32_t* counts;
+    const int32_t* route_at;
     const int64_t* ids;
     const uint16_t* svh13;    // [E][2][I]
     const uint16_t* suh2;     // [E][I]
-    uint16_t* xd;
-    int n, E, I, kparts;
+    uint16_t* xd;             // [n][I] fp16 in operand order
+    float* xdsum;             // [n][I / 128] sums of xd over each 128-column block
+    int n, I, nb, nwaves, cap, affine;
     float limit;
 };
 
+// One wave per (sorted position, 128-column block of I): row ranges added in order (then the AFFINE fixup),
+// output transforms, SwiGLU, the down-input transform.
 __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
 {
     const int lane = threadIdx.x & 63;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int ncb = a.I / GV_COLS;
-    const int s = item / ncb, cb = item % ncb;
-    if (s >= a.n) return;
-    const int64_t e = a.ids[s];
-    if (e < 0 || e >= a.E) return;
+    const int pos = item / ncb, cb = item % ncb;
+    if (pos >= a.counts[1]) return;
+    const int pps = pieces_per_segment(a.nwaves, a.counts[0] * 2 * ncb, a.cap);
+    const int64_t e = a.ids[a.route_at[pos]];
     const int c = cb * GV_COLS;
     float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
-    for (int q = 0; q < a.kparts; ++q)
+    for (int q = 0; q < pps; ++q)
     {
-        const float* pg = a.part + (((size_t)q * a.n + s) * 2 + 0) * a.I + c;
-        const float* pu = a.part + (((size_t)q * a.n + s) * 2 + 1) * a.I + c;
-        ga += pg[lane]; gb += pg[lane + 64];
-        ua += pu[lane]; ub += pu[lane + 64];
+        const float* pg = a.part + (((size_t)q * a.n + pos) * 2 + 0) * a.I + c;
+        const float* pu = a.part + (((size_t)q * a.n + pos) * 2 + 1) * a.I + c;
+        ga += pg[lane];
+        gb += pg[lane + 64];
+        ua += pu[lane];
+        ub += pu[lane + 64];
+    }
+    if (a.affine)
+    {
+        float sg = 0.f, su = 0.f;
+        for (int q = 0; q < a.nb; ++q)
+        {
+            sg += a.xsum[((size_t)pos * 2 + 0) * a.nb + q];
+            su += a.xsum[((size_t)pos * 2 + 1) * a.nb + q];
+        }
+        const float ki = kinv_f(), kb = kbias_f();
+        ga = fmaf(ki, ga, kb * sg);
+        gb = fmaf(ki, gb, kb * sg);
+        ua = fmaf(ki, ua, kb * su);
+        ub = fmaf(ki, ub, kb * su);
     }
     const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c;
     const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c;
@@ -478,140 +504,169 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     float xb = r16(act_gu(gb, ub, a.limit));
     const uint16_t* sd = a.suh2 + (size_t)e * a.I + c;
     prep_block_wave(xa, xb, h2f(sd[lane]), h2f(sd[lane + 64]));
-    a.xd[(size_t)s * a.I + c + lane] = f2h(xa);
-    a.xd[(size_t)s * a.I + c + lane + 64] = f2h(xb);
+    uint16_t* dst = a.xd + (size_t)pos * a.I;
+    dst[operand_index(c + lane)] = f2h(xa);
+    dst[operand_index(c + lane + 64)] = f2h(xb);
+    const float bs = wave_sum(xa + xb);
+    if (lane == 0) a.xdsum[(size_t)pos * ncb + cb] = bs;
 }
 
-// Down epilogue of one (route, 128-column block of H): K parts added in order, then the output transform.
-__device__ __forceinline__ void down_block(const float* part, int kparts, int n, int H, int s, int c, const uint16_t* sv,
-                                           int lane, float& ya, float& yb)
-{
-    ya = 0.f;
-    yb = 0.f;
-    for (int q = 0; q < kparts; ++q)
-    {
-        const float* pd = part + ((size_t)q * n + s) * H + c;
-        ya += pd[lane];
-        yb += pd[lane + 64];
-    }
-    out_block_wave(ya, yb, h2f(sv[lane]), h2f(sv[lane + 64]));
-}
+// ------------------------------------------------------------------------------------ 5. down epilogues
 
 struct DEpiArgs
 {
-    const float* part;        // [kparts][n][H]
+    const float* part;        // [pieces][n][H]
+    const float* xdsum;       // [n][I / 128]
+    const int32_t* counts;
+    const int32_t* pos_of;
+    const int32_t* route_at;
     const int64_t* ids;
-    const float* w;           // route weights (combine kernel)
+    const float* w;           // route weights (combine)
     const uint16_t* svh2;     // [E][H]
-    float* Y;                 // [n][H]
-    float* out;               // [T][H] (combine kernel)
-    uint16_t* xnext;          // [T][H] fp16 or null (combine kernel)
-    int n, E, H, kparts, topk, rescale;
+    float* Y;                 // [n][H] (per-route rows)
+    float* out;               // [T][H] (combine)
+    int n, H, I, topk, nwaves, cap, affine;
 };
 
-__global__ __launch_bounds__(256) void k_d_epilogue(DEpiArgs a)
+// Down output of one (sorted position, 128-column block of H): row ranges added in order (then the AFFINE
+// fixup), output transform.
+__device__ __forceinline__ void down_block(const DEpiArgs& a, int pos, int c, int64_t e, int lane, float& ya, float& yb)
+{
+    const int pps = pieces_per_segment(a.nwaves, a.counts[0] * (a.H / GV_COLS), a.cap);
+    ya = 0.f;
+    yb = 0.f;
+    for (int q = 0; q < pps; ++q)
+    {
+        const float* pd = a.part + ((size_t)q * a.n + pos) * a.H + c;
+        ya += pd[lane];
+        yb += pd[lane + 64];
+    }
+    if (a.affine)
+    {
+        float sx = 0.f;
+        for (int q = 0; q < a.I / GV_COLS; ++q) sx += a.xdsum[(size_t)pos * (a.I / GV_COLS) + q];
+        const float ki = kinv_f(), kb = kbias_f();
+        ya = fmaf(ki, ya, kb * sx);
+        yb = fmaf(ki, yb, kb * sx);
+    }
+    const uint16_t* sv = a.svh2 + (size_t)e * a.H + c;
+    out_block_wave(ya, yb, h2f(sv[lane]), h2f(sv[lane + 64]));
+}
+
+// Per-route rows: Y[s] for every routed s.
+__global__ __launch_bounds__(256) void k_down_y(DEpiArgs a)
 {
     const int lane = threadIdx.x & 63;
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int ncb = a.H / GV_COLS;
-    const int s = item / ncb, cb = item % ncb;
-    if (s >= a.n) return;
-    const int64_t e = a.ids[s];
-    if (e < 0 || e >= a.E) return;
+    const int pos = item / ncb, cb = item % ncb;
+    if (pos >= a.counts[1]) return;
+    const int s = a.route_at[pos];
     const int c = cb * GV_COLS;
     float ya, yb;
-    down_block(a.part, a.kparts, a.n, a.H, s, c, a.svh2 + (size_t)e * a.H + c, lane, ya, yb);
+    down_block(a, pos, c, a.ids[s], lane, ya, yb);
     a.Y[(size_t)s * a.H + c + lane] = ya;
     a.Y[(size_t)s * a.H + c + lane + 64] = yb;
 }
 
-// Down epilogue fused with the weighted combine and the next layer's input: one workgroup per token; a wave owns
-// a 128-column block and adds the routes in ascending j with fp32 fma (the order of k_combine), so out equals
-// the unfused path bit for bit.
-__global__ __launch_bounds__(1024) void k_d_epilogue_combine(DEpiArgs a)
+// Weighted combine: one workgroup per (token, 128-column block of H), wave j computes route j's output block,
+// then out = sum_j w_j y_j with fp32 fma in ascending j over the routed j (the order of mm_combine, so the
+// result equals mm_combine over the per-route rows bit for bit).
+__global__ __launch_bounds__(1024) void k_down_combine(DEpiArgs a)
 {
-    __shared__ float red[16];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    const int t = blockIdx.x;
+    __shared__ float ys[MAX_TOPK][GV_COLS];
+    __shared__ int ok[MAX_TOPK];
+    const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
     const int ncb = a.H / GV_COLS;
-    float ss = 0.0f;
-    for (int cb = wave; cb < ncb; cb += nw)
+    const int t = blockIdx.x / ncb, c = (blockIdx.x % ncb) * GV_COLS;
+    if (j < a.topk)
     {
-        const int c = cb * GV_COLS;
-        float oa = 0.f, ob = 0.f;
-        for (int j = 0; j < a.topk; ++j)
+        const int s = t * a.topk + j;
+        const int pos = a.pos_of[s];
+        if (pos >= 0)
         {
-            const int s = t * a.topk + j;
-            const int64_t e = a.ids[s];
-            if (e < 0 || e >= a.E) continue;
             float ya, yb;
-            down_block(a.part, a.kparts, a.n, a.H, s, c, a.svh2 + (size_t)e * a.H + c, lane, ya, yb);
-            const float wj = a.w[s];
-            oa = fmaf(wj, ya, oa);
-            ob = fmaf(wj, yb, ob);
+            down_block(a, pos, c, a.ids[s], lane, ya, yb);
+            ys[j][lane] = ya;
+            ys[j][lane + 64] = yb;
         }
-        a.out[(size_t)t * a.H + c + lane] = oa;
-        a.out[(size_t)t * a.H + c + lane + 64] = ob;
-        ss = fmaf(oa, oa, ss);
-        ss = fmaf(ob, ob, ss);
+        if (lane == 0) ok[j] = pos >= 0;
     }
-    if (!a.xnext) return;
-    float scale = 1.0f;
-    if (a.rescale)
+    __syncthreads();
+    for (int h = threadIdx.x; h < GV_COLS; h += blockDim.x)
     {
-        for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-        for (int i = 0; i < nw; ++i) tot += red[i];
-        scale = tot > 0.0f ? 1.0f / sqrtf(tot / (float)a.H) : 1.0f;
-    }
-    else
-        __syncthreads();
-    __syncthreads();   // every wave's out columns are written before they are re-read below
-    for (int h = threadIdx.x; h < a.H; h += blockDim.x)
-    {
-        uint32_t u = __float_as_uint(a.out[(size_t)t * a.H + h] * scale);
-        if ((u & 0x7fffffffu) > 0x7f800000u) u |= 0x400000u;
-        else u += 0x7fffu + ((u >> 16) & 1u);
-        a.xnext[(size_t)t * a.H + h] = f2h(__uint_as_float(u & 0xffff0000u));
+        float o = 0.0f;
+        for (int jj = 0; jj < a.topk; ++jj)
+            if (ok[jj]) o = fmaf(a.w[t * a.topk + jj], ys[jj][h], o);
+        a.out[(size_t)t * a.H + c + h] = o;
     }
 }
 
-static int pick_mt(int max_rows) { return max_rows <= 1 ? 1 : max_rows <= 2 ? 2 : max_rows <= 4 ? 4 : 8; }
-
-template <int MODE>
-static void launch_partial(const GemvArgs& a, int mt, hipStream_t s)
-{
-    const int blocks = a.max_active * a.ncb * a.kparts;
-    switch (mt)
-    {
-        case 1: hipLaunchKernelGGL((k_expert_partial<MODE, 1>), dim3(blocks), dim3(GV_THREADS), 0, s, a); break;
-        case 2: hipLaunchKernelGGL((k_expert_partial<MODE, 2>), dim3(blocks), dim3(GV_THREADS), 0, s, a); break;
-        case 4: hipLaunchKernelGGL((k_expert_partial<MODE, 4>), dim3(blocks), dim3(GV_THREADS), 0, s, a); break;
-        default: hipLaunchKernelGGL((k_expert_partial<MODE, 8>), dim3(blocks), dim3(GV_THREADS), 0, s, a); break;
-    }
-}
+// ------------------------------------------------------------------------------------------------- host
 
 struct Ws
 {
+    ExpertRec* rec;
+    int32_t* counts;
+    int32_t* pos_of;
+    int32_t* route_at;
+    uint16_t* xa;
+    float* xsum;
     float* part_gu;
-    float* part_d;
     uint16_t* xd;
+    float* xdsum;
+    float* part_d;
     size_t bytes;
 };
 
-static Ws carve(void* base, int n, int H, int I)
+static int prep_blocks(int H) { return (H + PREP_ROWS - 1) / PREP_ROWS; }
+
+// Most row ranges per segment a partial launch may use: bounded so the partial sums stay a few MB.
+static int piece_cap(int n)
 {
-    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    const size_t kq = (H + GV_KPART - 1) / GV_KPART, kh = (I + GV_KPART - 1) / GV_KPART;
-    const size_t b_gu = al(kq * n * 2 * I * 4), b_d = al(kh * n * H * 4), b_xd = al((size_t)n * I * 2);
-    char* p = static_cast<char*>(base);
-    return { reinterpret_cast<float*>(p), reinterpret_cast<float*>(p + b_gu), reinterpret_cast<uint16_t*>(p + b_gu + b_d),
-             b_gu + b_d + b_xd };
+    const int c = n > 0 ? 8192 / n : 32;
+    return c > 32 ? 32 : (c < 4 ? 4 : c);
 }
 
-static int check_common(const mm_layer_t* L, const void* x, int T, int n, int topk, const int64_t* ids,
+static Ws carve(void* base, int n, int E, int H, int I)
+{
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const size_t na = (size_t)(n < E ? n : E), cap = (size_t)piece_cap(n);
+    const size_t sizes[10] = { al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al((size_t)n * 4),
+                               al((size_t)n * 2 * H * 2), al((size_t)n * 2 * prep_blocks(H) * 4),
+                               al(cap * n * 2 * I * 4), al((size_t)n * I * 2), al((size_t)n * (I / GV_COLS) * 4),
+                               al(cap * n * H * 4) };
+    char* p = static_cast<char*>(base);
+    char* at[10];
+    size_t off = 0;
+    for (int i = 0; i < 10; ++i)
+    {
+        at[i] = p ? p + off : nullptr;
+        off += sizes[i];
+    }
+    return { reinterpret_cast<ExpertRec*>(at[0]), reinterpret_cast<int32_t*>(at[1]), reinterpret_cast<int32_t*>(at[2]),
+             reinterpret_cast<int32_t*>(at[3]), reinterpret_cast<uint16_t*>(at[4]), reinterpret_cast<float*>(at[5]),
+             reinterpret_cast<float*>(at[6]), reinterpret_cast<uint16_t*>(at[7]), reinterpret_cast<float*>(at[8]),
+             reinterpret_cast<float*>(at[9]), off };
+}
+
+// Waves of one partial launch: the whole GPU once (WAVES_PER_CU per CU), a multiple of 8 workgroups.
+static int partial_waves()
+{
+    static int waves = 0;
+    if (!waves)
+    {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        const int blocks = ((cus * WAVES_PER_CU / GV_WAVES) + 7) & ~7;
+        waves = blocks * GV_WAVES;
+    }
+    return waves;
+}
+
+static int check_common(const mm_layer_t* L, const void* x, int x_dtype, int T, int n, int topk, const int64_t* ids,
                         const int32_t* offsets, const int32_t* order, const int32_t* active, const int32_t* nactive,
                         int max_rows, void* ws, size_t ws_bytes, const char* who)
 {
@@ -619,43 +674,56 @@ static int check_common(const mm_layer_t* L, const void* x, int T, int n, int to
                  "%s: incomplete layer", who);
     MM_CHECK_ARG(L->E > 0 && L->E <= 1024 && L->H > 0 && L->I > 0 && L->H % 128 == 0 && L->I % 128 == 0,
                  "%s: need 0 < E <= 1024 and H, I positive multiples of 128 (E=%d H=%d I=%d)", who, L->E, L->H, L->I);
+    MM_CHECK_ARG((size_t)(L->H / 16) * (L->I / 16) * 96 < ((size_t)1 << 31), "%s: matrix larger than 2 GiB", who);
     MM_CHECK_ARG(x && ids, "%s: null pointer", who);
+    MM_CHECK_ARG(x_dtype == MM_DTYPE_F16 || x_dtype == MM_DTYPE_BF16 || x_dtype == MM_DTYPE_F32,
+                 "%s: x_dtype must be MM_DTYPE_F16, MM_DTYPE_BF16 or MM_DTYPE_F32", who);
     MM_CHECK_ARG(T > 0 && n > 0 && topk > 0 && n <= T * topk, "%s: bad T/n/topk", who);
+    MM_CHECK_ARG((size_t)n * 2 * (L->H > L->I ? L->H : L->I) * 2 < ((size_t)1 << 31), "%s: too many routes", who);
     MM_CHECK_ARG(max_rows > 0 && max_rows <= GV_MAX_ROWS, "%s: max_rows must be in [1, %d]", who, GV_MAX_ROWS);
     const bool perm = offsets != nullptr;
     MM_CHECK_ARG(perm ? (order && active && nactive) : n <= GV_ROUTE_MAX,
                  "%s: more than %d routes need the permutation (offsets, order, active, nactive)", who, GV_ROUTE_MAX);
-    MM_CHECK_ARG(ws && ws_bytes >= carve(nullptr, n, L->H, L->I).bytes, "%s: workspace too small (%zu < %zu)", who, ws_bytes,
-                 carve(nullptr, n, L->H, L->I).bytes);
+    const size_t need = carve(nullptr, n, L->E, L->H, L->I).bytes;
+    MM_CHECK_ARG(ws && ws_bytes >= need, "%s: workspace too small (%zu < %zu)", who, ws_bytes, need);
     return MM_OK;
 }
 
-static GemvArgs base_args(const mm_layer_t* L, int n, int topk, const int64_t* ids, const int32_t* offsets,
-                          const int32_t* order, const int32_t* active, const int32_t* nactive)
+static void launch_prep(const mm_layer_t* L, const Ws& w, const void* x, int x_dtype, int rescale, int n, int topk,
+                        const int64_t* ids, const int32_t* offsets, const int32_t* order, const int32_t* active,
+                        const int32_t* nactive, hipStream_t s)
 {
-    GemvArgs a{};
-    a.suh13 = L->suh13;
-    a.ids = ids; a.offsets = offsets; a.order = order; a.active = active; a.nactive = nactive;
-    a.H = L->H; a.I = L->I; a.E = L->E; a.n = n; a.topk = topk;
-    a.max_active = n < L->E ? n : L->E;
-    return a;
+    const int nb = prep_blocks(L->H);
+    PrepArgs p{ x, ids, offsets, order, active, nactive, L->gate_ptr, L->up_ptr, L->down_ptr, L->suh13,
+                w.rec, w.counts, w.pos_of, w.route_at, w.xa, w.xsum, n, topk, L->E, L->H, nb, x_dtype, rescale };
+    hipLaunchKernelGGL(k_route_prep, dim3(2 * n * nb), dim3(256), 0, s, p);
 }
 
-static void run_gate_up(const mm_layer_t* L, GemvArgs a, const void* x, const Ws& w, int mt, hipStream_t s, int parts)
+template <int MODE>
+static void launch_partial(const mm_layer_t* L, const Ws& w, int n, hipStream_t s)
 {
-    a.wptr0 = L->gate_ptr; a.wptr1 = L->up_ptr; a.xin = (const uint16_t*)x; a.part = w.part_gu;
-    a.K = L->H; a.N = L->I; a.ncb = L->I / GV_COLS; a.kparts = (L->H + GV_KPART - 1) / GV_KPART;
-    if (parts & 1) launch_partial<0>(a, mt, s);
-    GuEpiArgs g{ w.part_gu, a.ids, L->svh13, L->suh2, w.xd, a.n, L->E, L->I, a.kparts, L->limit };
-    if (parts & 2) hipLaunchKernelGGL(k_gu_epilogue, dim3((a.n * (L->I / GV_COLS) + 3) / 4), dim3(256), 0, s, g);
+    const int K = MODE == 0 ? L->H : L->I, N = MODE == 0 ? L->I : L->H;
+    PartArgs p{ w.rec, w.counts, MODE == 0 ? w.xa : w.xd, MODE == 0 ? w.part_gu : w.part_d, n, K, N, N / GV_COLS,
+                piece_cap(n) };
+    const dim3 grid(partial_waves() / GV_WAVES), block(GV_THREADS);
+    if (L->flags & MM_LAYER_EXACT)
+        hipLaunchKernelGGL((k_partial<MODE, true>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((k_partial<MODE, false>), grid, block, 0, s, p);
 }
 
-static int run_down_partial(const mm_layer_t* L, GemvArgs a, const Ws& w, int mt, hipStream_t s, bool launch)
+static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int n, const int64_t* ids, hipStream_t s)
 {
-    a.wptr0 = L->down_ptr; a.wptr1 = nullptr; a.xin = w.xd; a.part = w.part_d;
-    a.K = L->I; a.N = L->H; a.ncb = L->H / GV_COLS; a.kparts = (L->I + GV_KPART - 1) / GV_KPART;
-    if (launch) launch_partial<1>(a, mt, s);
-    return a.kparts;
+    GuEpiArgs g{ w.part_gu, w.xsum, w.counts, w.route_at, ids, L->svh13, L->suh2, w.xd, w.xdsum, n, L->I,
+                 prep_blocks(L->H), partial_waves(), piece_cap(n), (L->flags & MM_LAYER_EXACT) ? 0 : 1, L->limit };
+    hipLaunchKernelGGL(k_gu_epilogue, dim3((n * (L->I / GV_COLS) + 3) / 4), dim3(256), 0, s, g);
+}
+
+static DEpiArgs down_args(const mm_layer_t* L, const Ws& w, int n, int topk, const int64_t* ids, const float* wt,
+                          float* Y, float* out)
+{
+    return DEpiArgs{ w.part_d, w.xdsum, w.counts, w.pos_of, w.route_at, ids, wt, L->svh2, Y, out, n, L->H, L->I, topk,
+                     partial_waves(), piece_cap(n), (L->flags & MM_LAYER_EXACT) ? 0 : 1 };
 }
 
 }  // namespace mm
@@ -666,49 +734,50 @@ extern "C" {
 
 size_t mm_gemv_workspace(int n, int E, int H, int I)
 {
-    (void)E;
-    return carve(nullptr, n, H, I).bytes;
+    if (n <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
+    return carve(nullptr, n, E, H, I).bytes;
 }
 
-int mm_expert_gemv(const mm_layer_t* L, const void* x_fp16, int T, int n, int topk, const int64_t* ids,
-                   const int32_t* offsets, const int32_t* order, const int32_t* active, const int32_t* nactive,
-                   int max_rows, float* Y, void* workspace, size_t workspace_bytes, int phases, mm_stream_t stream)
+int mm_expert_gemv(const mm_layer_t* L, const void* x, int x_dtype, int rescale, int T, int n, int topk,
+                   const int64_t* ids, const int32_t* offsets, const int32_t* order, const int32_t* active,
+                   const int32_t* nactive, int max_rows, float* Y, void* workspace, size_t workspace_bytes, int phases,
+                   mm_stream_t stream)
 {
-    MM_CHECK_ARG(phases >= 1 && phases <= 15, "mm_expert_gemv: phases is a mask of 1, 2, 4, 8");
-    const int rc = check_common(L, x_fp16, T, n, topk, ids, offsets, order, active, nactive, max_rows, workspace,
+    MM_CHECK_ARG(phases >= 1 && phases <= 31, "mm_expert_gemv: phases is a mask of 1, 2, 4, 8, 16");
+    const int rc = check_common(L, x, x_dtype, T, n, topk, ids, offsets, order, active, nactive, max_rows, workspace,
                                 workspace_bytes, "mm_expert_gemv");
     if (rc) return rc;
-    MM_CHECK_ARG(Y, "mm_expert_gemv: null Y");
+    MM_CHECK_ARG(Y || !(phases & 16), "mm_expert_gemv: null Y");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const Ws w = carve(workspace, n, L->H, L->I);
-    const int mt = pick_mt(max_rows);
-    const GemvArgs a = base_args(L, n, topk, ids, offsets, order, active, nactive);
-    if (phases & 3) run_gate_up(L, a, x_fp16, w, mt, s, phases & 3);
-    if (phases & 12)
-    {
-        const int kh = run_down_partial(L, a, w, mt, s, (phases & 4) != 0);
-        DEpiArgs d{ w.part_d, ids, nullptr, L->svh2, Y, nullptr, nullptr, n, L->E, L->H, kh, topk, 0 };
-        if (phases & 8) hipLaunchKernelGGL(k_d_epilogue, dim3((n * (L->H / GV_COLS) + 3) / 4), dim3(256), 0, s, d);
-    }
+    const Ws w = carve(workspace, n, L->E, L->H, L->I);
+    if (phases & 1) launch_prep(L, w, x, x_dtype, rescale, n, topk, ids, offsets, order, active, nactive, s);
+    if (phases & 2) launch_partial<0>(L, w, n, s);
+    if (phases & 4) launch_gu_epilogue(L, w, n, ids, s);
+    if (phases & 8) launch_partial<1>(L, w, n, s);
+    if (phases & 16)
+        hipLaunchKernelGGL(k_down_y, dim3((n * (L->H / GV_COLS) + 3) / 4), dim3(256), 0, s,
+                           down_args(L, w, n, topk, ids, nullptr, Y, nullptr));
     return check_launch("mm_expert_gemv");
 }
 
-int mm_moe_decode(const mm_layer_t* L, const void* x_fp16, int T, int topk, const int64_t* ids, const float* w, int max_rows,
-                  float* out, void* x_next_fp16, int rescale, void* workspace, size_t workspace_bytes, mm_stream_t stream)
+int mm_moe_decode(const mm_layer_t* L, const void* x, int x_dtype, int rescale, int T, int topk, const int64_t* ids,
+                  const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes, mm_stream_t stream)
 {
+    MM_CHECK_ARG(topk > 0 && topk <= MAX_TOPK, "mm_moe_decode: topk must be in [1, %d]", MAX_TOPK);
     const int n = T * topk;
-    const int rc = check_common(L, x_fp16, T, n, topk, ids, nullptr, nullptr, nullptr, nullptr, max_rows, workspace,
+    const int rc = check_common(L, x, x_dtype, T, n, topk, ids, nullptr, nullptr, nullptr, nullptr, max_rows, workspace,
                                 workspace_bytes, "mm_moe_decode");
     if (rc) return rc;
     MM_CHECK_ARG(w && out, "mm_moe_decode: null pointer");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const Ws ws = carve(workspace, n, L->H, L->I);
-    const int mt = pick_mt(max_rows);
-    const GemvArgs a = base_args(L, n, topk, ids, nullptr, nullptr, nullptr, nullptr);
-    run_gate_up(L, a, x_fp16, ws, mt, s, 3);
-    const int kh = run_down_partial(L, a, ws, mt, s, true);
-    DEpiArgs d{ ws.part_d, ids, w, L->svh2, nullptr, out, (uint16_t*)x_next_fp16, n, L->E, L->H, kh, topk, rescale };
-    hipLaunchKernelGGL(k_d_epilogue_combine, dim3(T), dim3(1024), 0, s, d);
+    const Ws ws = carve(workspace, n, L->E, L->H, L->I);
+    launch_prep(L, ws, x, x_dtype, rescale, n, topk, ids, nullptr, nullptr, nullptr, nullptr, s);
+    launch_partial<0>(L, ws, n, s);
+    launch_gu_epilogue(L, ws, n, ids, s);
+    launch_partial<1>(L, ws, n, s);
+    const int threads = 64 * (topk < 2 ? 2 : topk);
+    hipLaunchKernelGGL(k_down_combine, dim3(T * (L->H / GV_COLS)), dim3(threads), 0, s,
+                       down_args(L, ws, n, topk, ids, w, nullptr, out));
     return check_launch("mm_moe_decode");
 }
 

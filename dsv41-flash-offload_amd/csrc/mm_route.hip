@@ -541,14 +541,6 @@ __global__ __launch_bounds__(256) void k_combine(float* __restrict__ out, const 
 // ---------------------------------------------------------------------------------------------------------
 // Expert input: fp32 -> (optional unit-RMS rescale) -> bf16 (RNE) -> fp16.
 // ---------------------------------------------------------------------------------------------------------
-__device__ __forceinline__ uint16_t f2bf(float f)
-{
-    uint32_t u = __float_as_uint(f);
-    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
-    u += 0x7fffu + ((u >> 16) & 1u);
-    return (uint16_t)(u >> 16);
-}
-
 __global__ __launch_bounds__(256) void k_prepare_input(const float* __restrict__ x, int H, int rescale,
                                                        uint16_t* __restrict__ xb, uint16_t* __restrict__ xh)
 {
@@ -571,59 +563,6 @@ __global__ __launch_bounds__(256) void k_prepare_input(const float* __restrict__
         const uint16_t b = f2bf(row[h] * scale);
         if (xb) xb[(size_t)t * H + h] = b;
         xh[(size_t)t * H + h] = f2h(__uint_as_float((uint32_t)b << 16));
-    }
-}
-
-// Combine + next expert input in one launch: one workgroup per token keeps the whole output row, so the
-// unit-RMS rescale needs no second pass over memory.
-__global__ __launch_bounds__(1024) void k_combine_prepare(float* __restrict__ out, const float* __restrict__ Y,
-                                                          const int64_t* __restrict__ ids, const float* __restrict__ w,
-                                                          int k, int H, int E, int rescale, uint16_t* __restrict__ xh)
-{
-    __shared__ float red[16];
-    const int t = blockIdx.x;
-    float ss = 0.0f;
-    constexpr int PER = 4;      // H <= 4 * 4 * 1024 columns handled per thread in registers
-    float4 acc[PER];
-    for (int i = 0; i < PER; ++i)
-    {
-        const int h = (threadIdx.x + i * blockDim.x) * 4;
-        acc[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-        if (h >= H) continue;
-        for (int j = 0; j < k; ++j)
-        {
-            const int s = t * k + j;
-            const int64_t e = ids[s];
-            if (e < 0 || e >= E) continue;
-            const float wj = w[s];
-            const float4 y = *reinterpret_cast<const float4*>(Y + (size_t)s * H + h);
-            acc[i].x = fmaf(wj, y.x, acc[i].x);
-            acc[i].y = fmaf(wj, y.y, acc[i].y);
-            acc[i].z = fmaf(wj, y.z, acc[i].z);
-            acc[i].w = fmaf(wj, y.w, acc[i].w);
-        }
-        *reinterpret_cast<float4*>(out + (size_t)t * H + h) = acc[i];
-        ss = fmaf(acc[i].x, acc[i].x, ss);
-        ss = fmaf(acc[i].y, acc[i].y, ss);
-        ss = fmaf(acc[i].z, acc[i].z, ss);
-        ss = fmaf(acc[i].w, acc[i].w, ss);
-    }
-    float scale = 1.0f;
-    if (rescale)
-    {
-        for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
-        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
-        __syncthreads();
-        float tot = 0.0f;
-        for (int i = 0; i < (int)(blockDim.x >> 6); ++i) tot += red[i];
-        scale = tot > 0.0f ? 1.0f / sqrtf(tot / (float)H) : 1.0f;
-    }
-    for (int i = 0; i < PER; ++i)
-    {
-        const int h = (threadIdx.x + i * blockDim.x) * 4;
-        if (h >= H) continue;
-        const float v[4] = { acc[i].x, acc[i].y, acc[i].z, acc[i].w };
-        for (int c = 0; c < 4; ++c) xh[(size_t)t * H + h + c] = f2h(__uint_as_float((uint32_t)f2bf(v[c] * scale) << 16));
     }
 }
 
@@ -790,16 +729,6 @@ int mm_prepare_input(const float* x, int T, int H, int rescale, void* x_bf16, vo
     if (T == 0) return MM_OK;
     hipLaunchKernelGGL(k_prepare_input, dim3(T), dim3(256), 0, S(stream), x, H, rescale, (uint16_t*)x_bf16, (uint16_t*)x_fp16);
     return check_launch("mm_prepare_input");
-}
-
-int mm_combine_prepare(float* out, const float* Y, const int64_t* ids, const float* w, int T, int k, int H, int E,
-                       int rescale, void* x_fp16, mm_stream_t stream)
-{
-    MM_CHECK_ARG(out && Y && ids && w && x_fp16, "mm_combine_prepare: null pointer");
-    MM_CHECK_ARG(T >= 0 && k > 0 && H > 0 && H % 4 == 0 && H <= 16 * 1024, "mm_combine_prepare: need H %% 4 == 0, H <= 16384");
-    if (T == 0) return MM_OK;
-    hipLaunchKernelGGL(k_combine_prepare, dim3(T), dim3(1024), 0, S(stream), out, Y, ids, w, k, H, E, rescale, (uint16_t*)x_fp16);
-    return check_launch("mm_combine_prepare");
 }
 
 uint64_t mm_expert_seed(uint64_t layer_seed, uint64_t expert) { return mix64(layer_seed * 0x100000001B3ull + expert); }

@@ -24,7 +24,9 @@ class MMLayer(ctypes.Structure):
     """Mirror of mm_layer_t."""
 
     _fields_ = [("gate_ptr", vp), ("up_ptr", vp), ("down_ptr", vp), ("suh13", vp), ("svh13", vp), ("suh2", vp),
-                ("svh2", vp), ("E", i32), ("H", i32), ("I", i32), ("limit", f32)]
+                ("svh2", vp), ("E", i32), ("H", i32), ("I", i32), ("limit", f32), ("flags", i32)]
+
+    EXACT = 1     # MM_LAYER_EXACT: fp16-rounded weights (the reference's EXACT expert) instead of AFFINE
 
 
 # name -> (restype, argtypes)
@@ -40,16 +42,19 @@ _SIGS = {
     "mm_permute": (i32, [vp, vp, i32, i32, i32, vp, vp, vp, vp, vp, vp, vp, vp, vp, sz, vp]),
     "mm_combine": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp]),
     "mm_gemv_workspace": (sz, [i32, i32, i32, i32]),
-    "mm_expert_gemv": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp, sz, i32, vp]),
-    "mm_moe_decode": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, vp, vp, i32, vp, vp, i32, vp, sz, vp]),
+    "mm_expert_gemv": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp, sz,
+                             i32, vp]),
+    "mm_moe_decode": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, sz, vp]),
     "mm_synth_u16": (i32, [vp, u64, u64, u64, vp]),
     "mm_synth_layer": (i32, [ctypes.POINTER(MMLayer), u64, vp]),
     "mm_expert_seed": (u64, [u64, u64]),
     "mm_prepare_input": (i32, [vp, i32, i32, i32, vp, vp, vp]),
-    "mm_combine_prepare": (i32, [vp, vp, vp, vp, i32, i32, i32, i32, i32, vp, vp]),
 }
 
 EXPORTS = tuple(_SIGS)
+
+# element types of a layer input (MM_DTYPE_* in include/mi355moe.h)
+DTYPE_F16, DTYPE_BF16, DTYPE_F32 = 0, 1, 2
 
 
 def load():

@@ -40,18 +40,30 @@ def permute(ids, w, topk, E, stream=None):
     return o
 
 
-def expert_gemv(store, x16, ids, T, n, topk, max_rows, routes=None, stream=None):
-    """Per-route expert outputs Y fp32 [n, H] (flat route order) on the decode path. Routes are found in-kernel
-    from ids, or taken from a permutation (`routes`, from permute())."""
-    dev = x16.device
+def x_dtype_of(x):
+    """MM_DTYPE_* code of a layer input tensor."""
+    import torch
+    codes = {torch.float16: _lib.DTYPE_F16, torch.bfloat16: _lib.DTYPE_BF16, torch.float32: _lib.DTYPE_F32}
+    if x.dtype not in codes:
+        raise TypeError(f"mi355moe: layer input must be fp16, bf16 or fp32 (got {x.dtype})")
+    return codes[x.dtype]
+
+
+def expert_gemv(store, x, ids, T, n, topk, max_rows, routes=None, rescale=False, phases=31, stream=None):
+    """Per-route expert outputs Y fp32 [n, H] (flat route order) on the decode path. x [T, H] is fp16 (used as
+    is), bf16 or fp32 (through bf16). Routes are found in-kernel from ids, or taken from a permutation
+    (`routes`, from permute())."""
+    dev = x.device
     E, H, I = store.E, store.H, store.I
     wsb = _lib.load().mm_gemv_workspace(n, E, H, I)
     ws = torch.zeros(wsb, dtype=torch.uint8, device=dev)
     Y = torch.zeros((n, H), dtype=torch.float32, device=dev)
     ids = ids.reshape(-1).contiguous().long()
+    x = x.contiguous()
     r = routes or {}
-    _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), T, n, topk, _i(ids), _i(r.get("offsets")), _i(r.get("order")),
-              _i(r.get("active")), _i(r.get("nactive")), int(max_rows), _i(Y), _i(ws), wsb, 15, _lib.stream_ptr(stream))
+    _lib.call("mm_expert_gemv", store.mm_layer(), _i(x), x_dtype_of(x), 1 if rescale else 0, T, n, topk, _i(ids),
+              _i(r.get("offsets")), _i(r.get("order")), _i(r.get("active")), _i(r.get("nactive")), int(max_rows),
+              _i(Y), _i(ws), wsb, phases, _lib.stream_ptr(stream))
     return Y
 
 
@@ -63,18 +75,6 @@ def combine(Y, ids, w, T, k, H, E, out=None, stream=None):
         out = torch.empty((T, H), dtype=torch.float32, device=Y.device)
     _lib.call("mm_combine", _i(out), _i(Y), _i(ids), _i(w), T, k, H, E, 1 if acc else 0, _lib.stream_ptr(stream))
     return out
-
-
-def to_expert_input(x):
-    """Expert input fp16 [T, H] from a bf16 / fp16 / fp32 activation (bf16 -> fp16 is exact in range)."""
-    if x.dtype == torch.float16:
-        return x.contiguous()
-    if x.dtype == torch.float32:
-        xf = x.contiguous()
-        x16 = torch.empty(x.shape, dtype=torch.float16, device=x.device)
-        _lib.call("mm_prepare_input", _i(xf), x.shape[0], x.shape[1], 0, None, _i(x16), _lib.stream_ptr())
-        return x16
-    return x.contiguous().to(torch.float16)
 
 
 def moe_forward(store, x, ids, w, shared_expert=None, use_permutation=None, stream=None):
@@ -96,8 +96,7 @@ def moe_forward(store, x, ids, w, shared_expert=None, use_permutation=None, stre
         raise NotImplementedError(f"expert with {max_rows} routes: the fat-expert path is required (> {GEMV_MAX_ROWS})")
     if use_permutation is None:
         use_permutation = n > 1024
-    x16 = to_expert_input(x)
-    Y = expert_gemv(store, x16, ids, T, n, k, max(1, max_rows), routes if use_permutation else None, stream)
+    Y = expert_gemv(store, x, ids, T, n, k, max(1, max_rows), routes if use_permutation else None, stream=stream)
     return combine(Y, ids, w, T, k, store.H, store.E, stream=stream)
 
 
@@ -144,16 +143,16 @@ class DecodeRunner:
                   _i(self.order), None, None, None, _i(self.active), _i(self.nactive), _i(self.pws), self.pws_bytes,
                   _lib.stream_ptr(stream))
 
-    def experts(self, store, x16=None, ids=None, phases=15, use_permutation=False, stream=None):
-        """The expert kernels (phases: mask of 1 gate/up partial, 2 gate/up epilogue, 4 down partial, 8 down
-        epilogue); routes found in-kernel from ids (or from route()'s permutation)."""
-        x16 = self.x16 if x16 is None else x16
+    def experts(self, store, x=None, ids=None, phases=31, use_permutation=False, rescale=False, stream=None):
+        """The expert kernels (phases: mask of 1 route prep, 2 gate/up partial sums, 4 gate/up epilogue, 8 down
+        partial sums, 16 down epilogue -> Y); routes found in-kernel from ids (or from route()'s permutation)."""
+        x = self.x16 if x is None else x
         ids = self.ids if ids is None else ids
         p = use_permutation
-        _lib.call("mm_expert_gemv", store.mm_layer(), _i(x16), self.T, self.n, self.k, _i(ids),
-                  _i(self.offsets) if p else None, _i(self.order) if p else None, _i(self.active) if p else None,
-                  _i(self.nactive) if p else None, self.max_rows, _i(self.Y), _i(self.gws), self.gws_bytes, phases,
-                  _lib.stream_ptr(stream))
+        _lib.call("mm_expert_gemv", store.mm_layer(), _i(x), x_dtype_of(x), 1 if rescale else 0, self.T, self.n,
+                  self.k, _i(ids), _i(self.offsets) if p else None, _i(self.order) if p else None,
+                  _i(self.active) if p else None, _i(self.nactive) if p else None, self.max_rows, _i(self.Y),
+                  _i(self.gws), self.gws_bytes, phases, _lib.stream_ptr(stream))
 
     def combine(self, ids=None, w=None, out=None, stream=None):
         ids = self.ids if ids is None else ids
@@ -163,31 +162,22 @@ class DecodeRunner:
                   _lib.stream_ptr(stream))
         return out
 
-    def combine_prepare(self, ids=None, w=None, out=None, x16_next=None, rescale=True, stream=None):
-        """combine, then the next layer's fp16 input (bf16 rounding, optional unit-RMS rescale) in one launch."""
+    def layer(self, store, x=None, ids=None, w=None, out=None, rescale=False, stream=None):
+        """One decode MoE layer through mm_moe_decode (5 launches: route prep, gate/up partial sums + epilogue,
+        down partial sums, down epilogue fused with the weighted combine). x is fp16, bf16 or fp32; a chain of
+        layers passes the previous out (fp32), with rescale for the unit-RMS step between layers."""
+        x = self.x16 if x is None else x
         ids = self.ids if ids is None else ids
         w = self.w if w is None else w
         out = self.out if out is None else out
-        x16_next = self.x16 if x16_next is None else x16_next
-        _lib.call("mm_combine_prepare", _i(out), _i(self.Y), _i(ids), _i(w), self.T, self.k, self.H, self.Eall,
-                  1 if rescale else 0, _i(x16_next), _lib.stream_ptr(stream))
+        _lib.call("mm_moe_decode", store.mm_layer(), _i(x), x_dtype_of(x), 1 if rescale else 0, self.T, self.k,
+                  _i(ids), _i(w), self.max_rows, _i(out), _i(self.gws), self.gws_bytes, _lib.stream_ptr(stream))
         return out
 
-    def layer(self, store, x16=None, ids=None, w=None, out=None, x16_next=None, rescale=True, stream=None):
-        """One decode MoE layer through mm_moe_decode (4 launches: gate/up partial + epilogue, down partial,
-        down epilogue fused with the combine and, if x16_next is given, the next layer's input)."""
-        x16 = self.x16 if x16 is None else x16
-        ids = self.ids if ids is None else ids
-        w = self.w if w is None else w
-        out = self.out if out is None else out
-        _lib.call("mm_moe_decode", store.mm_layer(), _i(x16), self.T, self.k, _i(ids), _i(w), self.max_rows, _i(out),
-                  _i(x16_next), 1 if rescale else 0, _i(self.gws), self.gws_bytes, _lib.stream_ptr(stream))
-        return out
-
-    def run(self, store, x16=None, ids=None, w=None, out=None, use_permutation=False, stream=None):
+    def run(self, store, x=None, ids=None, w=None, out=None, use_permutation=False, rescale=False, stream=None):
         """One layer as separate steps: expert MLP (in-kernel routing, or the permutation with use_permutation)
         -> Y -> combine. ids/w default to the runner's buffers."""
         if use_permutation:
             self.route(ids, w, stream)
-        self.experts(store, x16, ids, 15, use_permutation, stream)
+        self.experts(store, x, ids, 31, use_permutation, rescale, stream)
         return self.combine(ids, w, out, stream)

@@ -24,10 +24,11 @@ def trellis_words(K, N):
 class ExpertStore:
     """All experts of one layer resident in device memory."""
 
-    def __init__(self, E, H, I, device="cuda", limit=10.0):
+    def __init__(self, E, H, I, device="cuda", limit=10.0, exact=False):
         if H % 128 or I % 128:
             raise ValueError(f"H and I must be multiples of 128 (H={H}, I={I})")
         self.E, self.H, self.I, self.limit = E, H, I, float(limit)
+        self.exact = bool(exact)      # fp16-rounded weights (EXACT) instead of the AFFINE codebook evaluation
         dev = torch.device(device)
         it, ot = H // 16, I // 16
         self.w13_trellis = torch.empty((E, 2, it, ot, KW), dtype=torch.int16, device=dev)
@@ -59,7 +60,7 @@ class ExpertStore:
             self._c = _lib.MMLayer(self._exl3_ptrs["gate_trellis"].data_ptr(), self._exl3_ptrs["up_trellis"].data_ptr(),
                                    self._exl3_ptrs["down_trellis"].data_ptr(), self.w13_suh.data_ptr(),
                                    self.w13_svh.data_ptr(), self.w2_suh.data_ptr(), self.w2_svh.data_ptr(), self.E,
-                                   self.H, self.I, self.limit)
+                                   self.H, self.I, self.limit, _lib.MMLayer.EXACT if self.exact else 0)
         return self._c
 
     # ------------------------------------------------------------------------------------------ synthetic

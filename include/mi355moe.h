@@ -31,6 +31,11 @@ extern "C" {
 
 typedef void* mm_stream_t;
 
+/* Element types of a layer input x [T][H]. */
+#define MM_DTYPE_F16 0
+#define MM_DTYPE_BF16 1
+#define MM_DTYPE_F32 2
+
 /* Library version (major*10000 + minor*100 + patch). */
 int mm_version(void);
 
@@ -107,31 +112,43 @@ typedef struct mm_layer
     const uint16_t* svh2;       /* fp16 [E][H] */
     int E, H, I;
     float limit;                /* SwiGLU clamp (0 = off); reference default 10 */
+    int flags;                  /* MM_LAYER_* bits */
 } mm_layer_t;
 
-/* Bytes of device workspace mm_expert_gemv / mm_moe_decode need for n routes (K-part partial sums and the
- * transformed down-projection inputs). */
+/* mm_layer_t.flags. Without MM_LAYER_EXACT the decode path evaluates the codebook as the reference's AFFINE
+ * expert does (kernels/cpu_avx2/ft_core.h:267-293): unrounded w = KINV * (1024 + bytesum) + KBIAS, applied once
+ * per output through the input sum (sum_k x_k w_k = KINV * sum_k x_k (1024 + s_k) + KBIAS * sum_k x_k). With it,
+ * every weight is rounded to fp16 first, as the reference's EXACT expert and the exllamav3 kernel do
+ * (ft_core.h:75-83); that costs two more VALU operations per 16x16 tile. */
+#define MM_LAYER_EXACT 1
+
+/* Bytes of device workspace mm_expert_gemv / mm_moe_decode need for n routes over E experts (per-expert
+ * records, sorted positions, transformed inputs, K-part partial sums). */
 size_t mm_gemv_workspace(int n, int E, int H, int I);
 
 /* Decode expert path (replaces exllamav3 exl3_moe on the decode split, patches/vllm-exl3-host-dma.patch:323-445):
- * for every route s < n with 0 <= ids[s] < E (token s / topk), computes the expert SwiGLU MLP on x fp16 [T][H]
- * with fused EXL3 trellis decode and writes Y fp32 [n][H] row s (rows of other routes are left untouched).
- * Routes are found in-kernel from ids when offsets is NULL (n <= 1024); otherwise offsets/order/active/nactive
- * from mm_permute over the same routes are used. max_rows bounds the routes of any one expert (<= 256).
- * phases is a mask of the four launches, run in this order on the same workspace: 1 = gate/up partial sums,
- * 2 = gate/up epilogue (output transforms, SwiGLU, down-input transform), 4 = down partial sums, 8 = down
- * epilogue (output transform into Y); 15 = the whole expert MLP. */
-int mm_expert_gemv(const mm_layer_t* layer, const void* x_fp16, int T, int n, int topk, const int64_t* ids,
-                   const int32_t* offsets, const int32_t* order, const int32_t* active, const int32_t* nactive,
-                   int max_rows, float* Y, void* workspace, size_t workspace_bytes, int phases, mm_stream_t stream);
+ * for every route s < n with 0 <= ids[s] < E (token s / topk), computes the expert SwiGLU MLP with fused EXL3
+ * trellis decode and writes Y fp32 [n][H] row s (rows of other routes are left untouched).
+ * The expert input of token t is x[t] (x_dtype MM_DTYPE_*) converted to fp16: fp16 input is used as is, other
+ * types go through bf16 (RNE); with rescale != 0 the row is first scaled to unit RMS (any type), as
+ * mm_prepare_input does. Routes are found in-kernel from ids when offsets is NULL (n <= 1024); otherwise
+ * offsets/order/active/nactive from mm_permute over the same routes are used. max_rows bounds the routes of any
+ * one expert (<= 256). phases is a mask of the five launches, run in this order on the same workspace:
+ * 1 = route prep and input transform, 2 = gate/up partial sums, 4 = gate/up epilogue (output transforms, SwiGLU,
+ * down-input transform), 8 = down partial sums, 16 = down epilogue into Y; 31 = the whole expert MLP. */
+int mm_expert_gemv(const mm_layer_t* layer, const void* x, int x_dtype, int rescale, int T, int n, int topk,
+                   const int64_t* ids, const int32_t* offsets, const int32_t* order, const int32_t* active,
+                   const int32_t* nactive, int max_rows, float* Y, void* workspace, size_t workspace_bytes, int phases,
+                   mm_stream_t stream);
 
 /* One decode MoE layer (the fused-MoE call of the decode split, patches/vllm-exl3-host-dma.patch:315-449, with the
  * weighted combine of patches/vllm-exl3-host-dma.patch:327-342 made deterministic): routes ids int64 [T*topk]
- * with weights w fp32 [T*topk] (T*topk <= 1024; ids outside [0, E) contribute nothing) ->
- * out fp32 [T][H] = sum_j w[t,j] * expert_{ids[t,j]}(x_t). If x_next_fp16 != NULL it also receives the next
- * layer's fp16 input fp16(bf16(out_t * s_t)), s_t = 1/RMS(out_t) if rescale else 1. */
-int mm_moe_decode(const mm_layer_t* layer, const void* x_fp16, int T, int topk, const int64_t* ids, const float* w,
-                  int max_rows, float* out, void* x_next_fp16, int rescale, void* workspace, size_t workspace_bytes,
+ * with weights w fp32 [T*topk] (topk <= 16, T*topk <= 1024; ids outside [0, E) contribute nothing) ->
+ * out fp32 [T][H] = sum_j w[t,j] * expert_{ids[t,j]}(x_t), summed in ascending j with fp32 fma (equal to
+ * mm_combine over mm_expert_gemv's rows). x, x_dtype and rescale as for mm_expert_gemv: a chain of layers
+ * passes the previous layer's out with MM_DTYPE_F32. */
+int mm_moe_decode(const mm_layer_t* layer, const void* x, int x_dtype, int rescale, int T, int topk,
+                  const int64_t* ids, const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes,
                   mm_stream_t stream);
 
 /* ----------------------------------------------------------------------------------------- utility */
@@ -149,11 +166,6 @@ uint64_t mm_expert_seed(uint64_t layer_seed, uint64_t expert);
  * row to unit RMS first (the decode-chain workload's between-layer step): x16 = fp16(bf16(x * s_t)),
  * s_t = 1/sqrt(mean(x_t^2)) if rescale else 1. Also writes bf16 [T][H] if x_bf16 != NULL. */
 int mm_prepare_input(const float* x, int T, int H, int rescale, void* x_bf16, void* x_fp16, mm_stream_t stream);
-
-/* mm_combine (accumulate = 0) followed by mm_prepare_input on its output, in one launch (one workgroup per
- * token): out fp32 [T][H], and the next expert input x_fp16 [T][H] (bf16 rounding, optional unit-RMS rescale). */
-int mm_combine_prepare(float* out, const float* Y, const int64_t* ids, const float* w, int T, int k, int H, int E,
-                       int rescale, void* x_fp16, mm_stream_t stream);
 
 #ifdef __cplusplus
 }

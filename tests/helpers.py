@@ -4,10 +4,10 @@ import numpy as np
 import oracle as O
 
 
-def make_store(E, H, I, layer_seed, device="cuda", limit=10.0):
+def make_store(E, H, I, layer_seed, device="cuda", limit=10.0, exact=False):
     import torch
     from mi355moe.store import ExpertStore
-    st = ExpertStore(E, H, I, device=device, limit=limit).synthesize(layer_seed)
+    st = ExpertStore(E, H, I, device=device, limit=limit, exact=exact).synthesize(layer_seed)
     torch.cuda.synchronize()
     return st
 

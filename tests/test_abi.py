@@ -43,12 +43,15 @@ def test_argument_errors_without_device_work():
     assert rc == -1 and b"E <= 1024" in L.mm_last_error()
     rc = L.mm_permute(None, None, 10, 8, 0, None, None, None, None, None, None, None, None, None, 0, None)
     assert rc == -1
-    rc = L.mm_expert_gemv(None, None, 1, 1, 1, None, None, None, None, None, 1, None, None, 0, 3, None)
+    rc = L.mm_expert_gemv(None, None, 0, 0, 1, 1, 1, None, None, None, None, None, 1, None, None, 0, 31, None)
     assert rc == -1 and b"incomplete layer" in L.mm_last_error()
     with pytest.raises(RuntimeError, match="mm_combine"):
         _lib.call("mm_combine", None, None, None, None, 1, 1, 4096, 8, 0, None)
     assert L.mm_permute_workspace(100, 384) == 0 and L.mm_permute_workspace(131072, 384) > 0
-    assert L.mm_gemv_workspace(36, 385, 4096, 2048) >= 36 * 2048 * 2 + 4 * 36 * 2 * 2048 * 4
+    # transformed gate/up inputs, 8 K parts of gate/up partial sums, the down input, 4 K parts of down partials
+    assert L.mm_gemv_workspace(36, 385, 4096, 2048) >= (36 * 2 * 4096 * 2 + 8 * 36 * 2 * 2048 * 4 + 36 * 2048 * 2
+                                                        + 4 * 36 * 4096 * 4)
+    assert L.mm_gemv_workspace(0, 385, 4096, 2048) == 0
 
 
 def test_expert_seed_matches_oracle():

@@ -16,14 +16,16 @@ def _t(a, dev):
     return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
 
 
-def test_expert_matches_reference_golden(dev):
-    """Two experts of the compiled reference's golden file, through the HIP path (single route each)."""
+@pytest.mark.parametrize("exact", [False, True])
+def test_expert_matches_reference_golden(dev, exact):
+    """Two experts of the compiled reference's golden file, through the HIP path (single route each), with the
+    AFFINE codebook evaluation and with fp16-rounded (EXACT) weights."""
     import torch
     from mi355moe import moe
     g = np.load(os.path.join(GOLD, "expert_4096x2048.npz"), allow_pickle=False)
     H, I = int(g["H"]), int(g["I"])
     E = 256
-    st = make_store(E, H, I, int(g["layer_seed"]), device=dev)
+    st = make_store(E, H, I, int(g["layer_seed"]), device=dev, exact=exact)
     for j in (0, 1):
         e = int(g[f"e{j}"])
         st.w13_suh[e, 0].copy_(_t(g[f"suh_g{j}"], dev)); st.w13_svh[e, 0].copy_(_t(g[f"svh_g{j}"], dev))
@@ -33,24 +35,25 @@ def test_expert_matches_reference_golden(dev):
             st.limit = float(lim)
             st._c = None
             x = _t(g[f"x{j}"][None, :].astype(np.float16), dev)
-            print(f"golden expert {e} limit {lim}", flush=True)
+            print(f"golden expert {e} limit {lim} exact {exact}", flush=True)
             out = moe.moe_forward(st, x, torch.tensor([[e]], device=dev), torch.ones((1, 1), device=dev))
             torch.cuda.synchronize()
             ok, m = within_tolerance(out.cpu().numpy()[0], g[f"y{j}_lim{lim}"])
             assert ok, m
 
 
+@pytest.mark.parametrize("exact", [False, True])
 @pytest.mark.parametrize("H,I,E,T,k", [(256, 256, 8, 3, 2), (1024, 384, 16, 5, 4), (2048, 1152, 12, 6, 3)])
-def test_small_shapes_vs_oracle(dev, H, I, E, T, k):
+def test_small_shapes_vs_oracle(dev, H, I, E, T, k, exact):
     import torch
     from mi355moe import moe
     seed = 4242 + H
-    st = make_store(E, H, I, seed, device=dev)
+    st = make_store(E, H, I, seed, device=dev, exact=exact)
     rng = np.random.default_rng(H + I)
     ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
     w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
     x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
-    print(f"small shape H={H} I={I} E={E} T={T} k={k}", flush=True)
+    print(f"small shape H={H} I={I} E={E} T={T} k={k} exact={exact}", flush=True)
     out = moe.moe_forward(st, _t(x16, dev), _t(ids, dev), _t(w, dev))
     torch.cuda.synchronize()
     ref = OracleLayer(st, seed).forward(x16.astype(np.float32), ids, w)
@@ -82,18 +85,18 @@ def test_per_route_outputs_and_masked_routes(dev):
     assert np.array_equal(outs[0], outs[1])
 
 
-@pytest.mark.parametrize("T", [1, 4])
-def test_full_shape_layer_with_shared_expert(dev, T):
+@pytest.mark.parametrize("T,exact", [(1, False), (4, False), (4, True)])
+def test_full_shape_layer_with_shared_expert(dev, T, exact):
     """One layer at the benchmark shape (H 4096, I 2048, 384 routed + 1 shared, top-8, Zipf routing)."""
     import torch
     from mi355moe import moe, workload
     H, I, E = 4096, 2048, 384
     seed = 1000 + T
-    st = make_store(E + 1, H, I, seed, device=dev)
+    st = make_store(E + 1, H, I, seed, device=dev, exact=exact)
     ids, w = workload.zipf_routing(T, 8, E, seed=2000 + T)
     x = workload.activations(T, H, seed=7)
     x16 = x.astype(np.float16)
-    print(f"full shape T={T}", flush=True)
+    print(f"full shape T={T} exact={exact}", flush=True)
     out = moe.moe_forward(st, _t(x16, dev), _t(ids, dev), _t(w, dev), shared_expert=E)
     torch.cuda.synchronize()
     ids_ext = np.concatenate([ids, np.full((T, 1), E)], 1)
@@ -118,31 +121,53 @@ def test_deterministic_and_runner_matches(dev):
     R.x16.copy_(x16)
     c = R.run(st).clone()
     d = R.run(st, use_permutation=True).clone()
-    xn = torch.empty_like(R.x16)
-    f = R.layer(st, x16_next=xn).clone()
+    f = R.layer(st).clone()
     torch.cuda.synchronize()
     assert torch.equal(a, b) and torch.equal(a, c) and torch.equal(c, d) and torch.equal(a, f)
-    # the fused next-input matches mm_combine_prepare on the same output
-    from mi355moe import _lib
-    out2 = torch.empty_like(f)
-    x2 = torch.empty_like(xn)
-    _lib.call("mm_combine_prepare", out2.data_ptr(), R.Y.data_ptr(), R.ids.data_ptr(), R.w.data_ptr(), T, R.k, H, R.Eall, 1,
-              x2.data_ptr(), _lib.stream_ptr())
+
+
+def test_layer_input_types_and_rescale(dev):
+    """The layer's own input conversion equals converting first: fp32 with rescale vs mm_prepare_input, bf16 vs
+    torch's bf16 -> fp16; the chain step (previous out fed back with rescale) is bit-reproducible."""
+    import torch
+    from mi355moe import _lib, moe, workload
+    H, I, E, T = 1024, 512, 48, 4
+    st = make_store(E + 1, H, I, 77, device=dev)
+    ids, w = workload.zipf_routing(T, 8, E, seed=6)
+    R = moe.DecodeRunner(E, H, I, T, 8, device=dev)
+    R.set_routes(_t(ids, dev), _t(w, dev))
+    xf = _t((np.random.default_rng(3).normal(0, 3.0, (T, H))).astype(np.float32), dev)
+    x16 = torch.empty((T, H), dtype=torch.float16, device=dev)
+    _lib.call("mm_prepare_input", xf.data_ptr(), T, H, 1, None, x16.data_ptr(), _lib.stream_ptr())
+    a = R.layer(st, x=xf, rescale=True).clone()
+    b = R.layer(st, x=x16).clone()
+    xb = xf.to(torch.bfloat16)
+    c = R.layer(st, x=xb).clone()
+    d = R.layer(st, x=xb.half()).clone()
+    e1 = R.layer(st, x=a, rescale=True).clone()
+    e2 = R.layer(st, x=a, rescale=True).clone()
     torch.cuda.synchronize()
-    assert torch.equal(out2, f) and torch.equal(x2, xn)
+    assert torch.equal(a, b) and torch.equal(c, d) and torch.equal(e1, e2)
+    ref = OracleLayer(st, 77).forward(x16.cpu().numpy().astype(np.float32), np.concatenate([ids, np.full((T, 1), E)], 1),
+                                      np.concatenate([w, np.ones((T, 1), np.float32)], 1))
+    ok, m = within_tolerance(a.cpu().numpy(), ref)
+    assert ok, m
 
 
-def test_many_routes_per_expert_chunks(dev):
-    """An expert with more routes than one chunk (rows > 8) and the permutation path (> 1024 routes)."""
+@pytest.mark.parametrize("T,k,E", [(200, 6, 6), (60, 4, 8)])
+def test_many_routes_per_expert_chunks(dev, T, k, E):
+    """Experts with more routes than one MFMA pass (16): through the permutation (> 1024 routes) and through the
+    in-kernel routing."""
     import torch
     from mi355moe import moe
-    H, I, E, T, k = 512, 256, 6, 200, 6
-    seed = 321
+    H, I = 512, 256
+    seed = 321 + T
     st = make_store(E, H, I, seed, device=dev)
     rng = np.random.default_rng(9)
-    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)    # each expert ~200 routes
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int64)
     w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
     x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
+    print(f"many routes T={T} k={k} E={E}", flush=True)
     out = moe.moe_forward(st, _t(x16, dev), _t(ids, dev), _t(w, dev))
     torch.cuda.synchronize()
     ref = OracleLayer(st, seed).forward(x16.astype(np.float32), ids, w)
@@ -150,22 +175,15 @@ def test_many_routes_per_expert_chunks(dev):
     assert ok, m
 
 
-def test_combine_prepare_matches_parts(dev):
+def test_prepare_input_matches_numpy(dev):
     import torch
-    from mi355moe import _lib, moe
-    T, k, H, E = 4, 9, 4096, 385
-    rng = np.random.default_rng(2)
-    Y = _t(rng.normal(0, 1, (T * k, H)).astype(np.float32), dev)
-    ids = _t(rng.integers(0, E, (T, k)).astype(np.int64), dev)
-    w = _t(rng.uniform(0, 1, (T, k)).astype(np.float32), dev)
-    ref = moe.combine(Y, ids, w, T, k, H, E)
-    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    from mi355moe import _lib
+    T, H = 4, 4096
+    x = np.random.default_rng(2).normal(0, 2, (T, H)).astype(np.float32)
     x16 = torch.empty((T, H), dtype=torch.float16, device=dev)
-    _lib.call("mm_combine_prepare", out.data_ptr(), Y.data_ptr(), ids.data_ptr(), w.data_ptr(), T, k, H, E, 1,
-              x16.data_ptr(), _lib.stream_ptr())
+    _lib.call("mm_prepare_input", _t(x, dev).data_ptr(), T, H, 1, None, x16.data_ptr(), _lib.stream_ptr())
     torch.cuda.synchronize()
-    assert torch.equal(out, ref)
-    o = ref.cpu().numpy().astype(np.float64)
+    o = x.astype(np.float64)
     scaled = (o / np.sqrt((o * o).mean(1, keepdims=True))).astype(np.float32)
     bf = (scaled.view(np.uint32) + 0x7FFF + ((scaled.view(np.uint32) >> 16) & 1)) & 0xFFFF0000
     expect = bf.view(np.float32).astype(np.float16)
