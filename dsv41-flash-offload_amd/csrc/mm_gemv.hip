@@ -125,6 +125,15 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
+// Sum of p[0 .. count) by one wave: one load per lane (all in flight together), then a fixed reduction tree.
+__device__ __forceinline__ float wave_sum_of(const float* p, int count)
+{
+    const int lane = threadIdx.x & 63;
+    float v = 0.0f;
+    for (int i = lane; i < count; i += 64) v += p[i];
+    return wave_sum(v);
+}
+
 // ------------------------------------------------------------------------------------------ 1. route prep
 
 struct PrepArgs
@@ -143,6 +152,7 @@ struct PrepArgs
     int32_t* counts;          // [2]: active experts, routed (valid) routes
     int32_t* pos_of;          // [n] sorted position of each route, -1 if its id is outside [0, E)
     int32_t* route_at;        // [n] route at each sorted position
+    int32_t* e_at;            // [n] expert at each sorted position
     uint16_t* xa;             // [n][2][H] fp16 in operand order
     float* xsum;              // [n][2][nb] sums of xa over each workgroup's rows
     int n, topk, E, H, nb, x_dtype, rescale;
@@ -155,35 +165,58 @@ __device__ __forceinline__ float load_x(const void* x, int dtype, size_t i)
     return static_cast<const float*>(x)[i];
 }
 
-__device__ __forceinline__ int block_sum_int(int v, int (*tmp)[4], int slot)
+__device__ __forceinline__ int wave_sum_int(int v)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
 #pragma unroll
     for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    if (lane == 0) tmp[wave][slot] = v;
-    __syncthreads();
-    return tmp[0][slot] + tmp[1][slot] + tmp[2][slot] + tmp[3][slot];
+    return v;
 }
 
+// Every load that does not depend on another is issued before the first barrier (the route's id, all ids for
+// the position, the token row for the rescale, this wave's block of it), and the routing counts and the row's
+// sum of squares share one reduction, so the kernel costs about two memory round trips.
 __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
 {
     __shared__ uint32_t s_bm[32];
-    __shared__ int s_red[4][4];
+    __shared__ int s_cnt[4][4];
     __shared__ float s_ss[4];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int blk = blockIdx.x % a.nb, m = (blockIdx.x / a.nb) & 1, idx = blockIdx.x / (2 * a.nb);
     const bool writer = m == 0 && blk == 0;      // the one workgroup of a route that writes its routing data
-    int s, pos, e;
-    if (!a.offsets)
+    const bool perm = a.offsets != nullptr;
+    // routing from the permutation: the workgroups of index idx own sorted position idx
+    const int nvalid_perm = perm ? a.offsets[a.E] : 0;
+    const int s = perm ? a.order[idx] : idx;
+    const int64_t e64 = a.ids[s];
+    const int t = s / a.topk;
+    const size_t row = (size_t)t * a.H;
+    const int h0 = blk * PREP_ROWS + wave * 128;
+    float va = 0.f, vb = 0.f, ss = 0.f;
+    if (h0 < a.H)
     {
-        // routing from the ids: position = routes of lower experts + earlier routes of the same expert
-        if (tid < 32) s_bm[tid] = 0;
-        __syncthreads();
-        s = idx;
-        const int64_t e64 = a.ids[s];
-        const bool valid = e64 >= 0 && e64 < a.E;
-        e = valid ? (int)e64 : -1;
-        int less = 0, same = 0, rank = 0, nv = 0;
+        va = load_x(a.x, a.x_dtype, row + h0 + lane);
+        vb = load_x(a.x, a.x_dtype, row + h0 + lane + 64);
+    }
+    if (a.rescale)
+        for (int h = tid; h < a.H; h += 256)
+        {
+            const float v = load_x(a.x, a.x_dtype, row + h);
+            ss = fmaf(v, v, ss);
+        }
+    const bool valid = perm ? idx < nvalid_perm : (e64 >= 0 && e64 < a.E);
+    const int e = valid ? (int)e64 : -1;
+    float sa = 0.f, sb = 0.f;
+    if (valid && h0 < a.H)
+    {
+        const uint16_t* su = a.suh13 + ((size_t)e * 2 + m) * a.H;
+        sa = h2f(su[h0 + lane]);
+        sb = h2f(su[h0 + lane + 64]);
+    }
+    if (tid < 32) s_bm[tid] = 0;
+    __syncthreads();
+    // in-kernel routing: position = routes of lower experts + earlier routes of the same expert
+    int less = 0, same = 0, rank = 0, nv = 0;
+    if (!perm)
         for (int i = tid; i < a.n; i += 256)
         {
             const int64_t v = a.ids[i];
@@ -194,113 +227,88 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
             same += v == e;
             rank += (v == e) && (i < s);
         }
-        less = block_sum_int(less, s_red, 0);
-        same = block_sum_int(same, s_red, 1);
-        rank = block_sum_int(rank, s_red, 2);
-        nv = block_sum_int(nv, s_red, 3);
-        if (tid == 0 && (writer || blockIdx.x == 0))
+    less = wave_sum_int(less);
+    same = wave_sum_int(same);
+    rank = wave_sum_int(rank);
+    nv = wave_sum_int(nv);
+    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
+    if (lane == 0)
+    {
+        s_cnt[wave][0] = less;
+        s_cnt[wave][1] = same;
+        s_cnt[wave][2] = rank;
+        s_cnt[wave][3] = nv;
+        s_ss[wave] = ss;
+    }
+    __syncthreads();
+    less = s_cnt[0][0] + s_cnt[1][0] + s_cnt[2][0] + s_cnt[3][0];
+    same = s_cnt[0][1] + s_cnt[1][1] + s_cnt[2][1] + s_cnt[3][1];
+    rank = s_cnt[0][2] + s_cnt[1][2] + s_cnt[2][2] + s_cnt[3][2];
+    nv = s_cnt[0][3] + s_cnt[1][3] + s_cnt[2][3] + s_cnt[3][3];
+    const int pos = perm ? idx : less + rank;
+    if (tid == 0 && (writer || blockIdx.x == 0))
+    {
+        if (blockIdx.x == 0)
         {
-            int nact = 0, below = 0;
-            for (int wd = 0; wd < 32; ++wd)
+            int nact = 0;
+            if (!perm)
+                for (int wd = 0; wd < 32; ++wd) nact += __popc(s_bm[wd]);
+            a.counts[0] = perm ? a.nactive_in[0] : nact;
+            a.counts[1] = perm ? nvalid_perm : nv;
+        }
+        if (writer)
+        {
+            a.pos_of[s] = valid ? pos : -1;
+            if (valid)
             {
-                const uint32_t bits = s_bm[wd];
-                nact += __popc(bits);
-                if (valid && wd < (e >> 5)) below += __popc(bits);
-            }
-            if (blockIdx.x == 0)
-            {
-                a.counts[0] = nact;
-                a.counts[1] = nv;
-            }
-            if (writer)
-            {
-                if (!valid)
-                    a.pos_of[s] = -1;
-                else
+                a.route_at[pos] = s;
+                a.e_at[pos] = e;
+                // the expert's first route writes its record
+                int ai = -1, cnt = 0;
+                if (!perm && rank == 0)
                 {
-                    a.pos_of[s] = less + rank;
-                    a.route_at[less + rank] = s;
-                    if (rank == 0)
-                    {
-                        below += __popc(s_bm[e >> 5] & ((1u << (e & 31)) - 1u));
-                        ExpertRec r{ e, same, less, 0, { a.wtab0[e], a.wtab1[e], a.wtab2[e] }, 0 };
-                        a.rec[below] = r;
-                    }
+                    ai = 0;
+                    for (int wd = 0; wd < (e >> 5); ++wd) ai += __popc(s_bm[wd]);
+                    ai += __popc(s_bm[e >> 5] & ((1u << (e & 31)) - 1u));
+                    cnt = same;
+                }
+                else if (perm && pos == a.offsets[e])
+                {
+                    const int na = a.nactive_in[0];
+                    ai = 0;
+                    while (ai < na && a.active[ai] != e) ++ai;
+                    if (ai == na) ai = -1;
+                    cnt = a.offsets[e + 1] - pos;
+                }
+                if (ai >= 0)
+                {
+                    ExpertRec r{ e, cnt, pos, 0, { a.wtab0[e], a.wtab1[e], a.wtab2[e] }, 0 };
+                    a.rec[ai] = r;
                 }
             }
         }
-        if (!valid) return;
-        pos = less + rank;
     }
-    else
-    {
-        // routing from the permutation: the workgroups of index idx own sorted position idx
-        pos = idx;
-        const int nvalid = a.offsets[a.E];
-        s = a.order[pos];
-        if (tid == 0)
-        {
-            if (blockIdx.x == 0)
-            {
-                a.counts[0] = a.nactive_in[0];
-                a.counts[1] = nvalid;
-            }
-            if (writer)
-            {
-                a.pos_of[s] = pos < nvalid ? pos : -1;
-                if (pos < nvalid) a.route_at[pos] = s;
-            }
-        }
-        if (pos >= nvalid) return;
-        e = (int)a.ids[s];
-        if (tid == 0 && writer && pos == a.offsets[e])
-        {
-            const int na = a.nactive_in[0];
-            int ai = 0;
-            while (ai < na && a.active[ai] != e) ++ai;
-            if (ai < na)
-            {
-                ExpertRec r{ e, a.offsets[e + 1] - pos, pos, 0, { a.wtab0[e], a.wtab1[e], a.wtab2[e] }, 0 };
-                a.rec[ai] = r;
-            }
-        }
-    }
+    if (!valid) return;
 
     // the route's expert input: x16 = fp16(bf16(x_t * s_t)) (fp16 input without rescale is taken as is);
-    // s_t = 1 / RMS(x_t) in the reduction order of mm_prepare_input
-    const int t = s / a.topk;
-    const size_t row = (size_t)t * a.H;
+    // s_t = 1 / RMS(x_t), the per-wave sums added as mm_prepare_input adds them
     float scale = 1.0f;
     if (a.rescale)
     {
-        float ss = 0.0f;
-        for (int h = tid; h < a.H; h += 256)
-        {
-            const float v = load_x(a.x, a.x_dtype, row + h);
-            ss = fmaf(v, v, ss);
-        }
-        for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
-        if (lane == 0) s_ss[wave] = ss;
-        __syncthreads();
         const float tot = (s_ss[0] + s_ss[1]) + (s_ss[2] + s_ss[3]);
         scale = tot > 0.0f ? 1.0f / sqrtf(tot / (float)a.H) : 1.0f;
-        __syncthreads();      // s_ss is reused below
     }
-    const bool as_is = a.x_dtype == MM_DTYPE_F16 && !a.rescale;
-    const uint16_t* su = a.suh13 + ((size_t)e * 2 + m) * a.H;
-    uint16_t* dst = a.xa + ((size_t)pos * 2 + m) * a.H;
-    const int h0 = blk * PREP_ROWS + wave * 128;
+    __syncthreads();      // s_ss is reused below
     float bsum = 0.0f;
     if (h0 < a.H)
     {
-        float va = load_x(a.x, a.x_dtype, row + h0 + lane);
-        float vb = load_x(a.x, a.x_dtype, row + h0 + lane + 64);
-        if (!as_is)
+        if (!(a.x_dtype == MM_DTYPE_F16 && !a.rescale))
         {
             va = r16(bf16_value(va * scale));
             vb = r16(bf16_value(vb * scale));
         }
-        prep_block_wave(va, vb, h2f(su[h0 + lane]), h2f(su[h0 + lane + 64]));
+        prep_block_wave(va, vb, sa, sb);
+        uint16_t* dst = a.xa + ((size_t)pos * 2 + m) * a.H;
         dst[operand_index(h0 + lane)] = f2h(va);
         dst[operand_index(h0 + lane + 64)] = f2h(vb);
         bsum = wave_sum(va + vb);
@@ -450,8 +458,7 @@ struct GuEpiArgs
     const float* part;        // [pieces][n][2][I]
     const float* xsum;        // [n][2][nb]
     const int32_t* counts;
-    const int32_t* route_at;
-    const int64_t* ids;
+    const int32_t* e_at;
     const uint16_t* svh13;    // [E][2][I]
     const uint16_t* suh2;     // [E][I]
     uint16_t* xd;             // [n][I] fp16 in operand order
@@ -470,9 +477,10 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     const int pos = item / ncb, cb = item % ncb;
     if (pos >= a.counts[1]) return;
     const int pps = pieces_per_segment(a.nwaves, a.counts[0] * 2 * ncb, a.cap);
-    const int64_t e = a.ids[a.route_at[pos]];
+    const int e = a.e_at[pos];
     const int c = cb * GV_COLS;
     float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
+#pragma unroll 8
     for (int q = 0; q < pps; ++q)
     {
         const float* pg = a.part + (((size_t)q * a.n + pos) * 2 + 0) * a.I + c;
@@ -484,12 +492,8 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     }
     if (a.affine)
     {
-        float sg = 0.f, su = 0.f;
-        for (int q = 0; q < a.nb; ++q)
-        {
-            sg += a.xsum[((size_t)pos * 2 + 0) * a.nb + q];
-            su += a.xsum[((size_t)pos * 2 + 1) * a.nb + q];
-        }
+        const float sg = wave_sum_of(a.xsum + ((size_t)pos * 2 + 0) * a.nb, a.nb);
+        const float su = wave_sum_of(a.xsum + ((size_t)pos * 2 + 1) * a.nb, a.nb);
         const float ki = kinv_f(), kb = kbias_f();
         ga = fmaf(ki, ga, kb * sg);
         gb = fmaf(ki, gb, kb * sg);
@@ -535,6 +539,7 @@ __device__ __forceinline__ void down_block(const DEpiArgs& a, int pos, int c, in
     const int pps = pieces_per_segment(a.nwaves, a.counts[0] * (a.H / GV_COLS), a.cap);
     ya = 0.f;
     yb = 0.f;
+#pragma unroll 8
     for (int q = 0; q < pps; ++q)
     {
         const float* pd = a.part + ((size_t)q * a.n + pos) * a.H + c;
@@ -543,8 +548,7 @@ __device__ __forceinline__ void down_block(const DEpiArgs& a, int pos, int c, in
     }
     if (a.affine)
     {
-        float sx = 0.f;
-        for (int q = 0; q < a.I / GV_COLS; ++q) sx += a.xdsum[(size_t)pos * (a.I / GV_COLS) + q];
+        const float sx = wave_sum_of(a.xdsum + (size_t)pos * (a.I / GV_COLS), a.I / GV_COLS);
         const float ki = kinv_f(), kb = kbias_f();
         ya = fmaf(ki, ya, kb * sx);
         yb = fmaf(ki, yb, kb * sx);
@@ -610,6 +614,7 @@ struct Ws
     int32_t* counts;
     int32_t* pos_of;
     int32_t* route_at;
+    int32_t* e_at;
     uint16_t* xa;
     float* xsum;
     float* part_gu;
@@ -632,22 +637,22 @@ static Ws carve(void* base, int n, int E, int H, int I)
 {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t na = (size_t)(n < E ? n : E), cap = (size_t)piece_cap(n);
-    const size_t sizes[10] = { al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al((size_t)n * 4),
-                               al((size_t)n * 2 * H * 2), al((size_t)n * 2 * prep_blocks(H) * 4),
+    const size_t sizes[11] = { al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al((size_t)n * 4),
+                               al((size_t)n * 4), al((size_t)n * 2 * H * 2), al((size_t)n * 2 * prep_blocks(H) * 4),
                                al(cap * n * 2 * I * 4), al((size_t)n * I * 2), al((size_t)n * (I / GV_COLS) * 4),
                                al(cap * n * H * 4) };
     char* p = static_cast<char*>(base);
-    char* at[10];
+    char* at[11];
     size_t off = 0;
-    for (int i = 0; i < 10; ++i)
+    for (int i = 0; i < 11; ++i)
     {
         at[i] = p ? p + off : nullptr;
         off += sizes[i];
     }
     return { reinterpret_cast<ExpertRec*>(at[0]), reinterpret_cast<int32_t*>(at[1]), reinterpret_cast<int32_t*>(at[2]),
-             reinterpret_cast<int32_t*>(at[3]), reinterpret_cast<uint16_t*>(at[4]), reinterpret_cast<float*>(at[5]),
-             reinterpret_cast<float*>(at[6]), reinterpret_cast<uint16_t*>(at[7]), reinterpret_cast<float*>(at[8]),
-             reinterpret_cast<float*>(at[9]), off };
+             reinterpret_cast<int32_t*>(at[3]), reinterpret_cast<int32_t*>(at[4]), reinterpret_cast<uint16_t*>(at[5]),
+             reinterpret_cast<float*>(at[6]), reinterpret_cast<float*>(at[7]), reinterpret_cast<uint16_t*>(at[8]),
+             reinterpret_cast<float*>(at[9]), reinterpret_cast<float*>(at[10]), off };
 }
 
 // Waves of one partial launch: the whole GPU once (WAVES_PER_CU per CU), a multiple of 8 workgroups.
@@ -695,7 +700,7 @@ static void launch_prep(const mm_layer_t* L, const Ws& w, const void* x, int x_d
 {
     const int nb = prep_blocks(L->H);
     PrepArgs p{ x, ids, offsets, order, active, nactive, L->gate_ptr, L->up_ptr, L->down_ptr, L->suh13,
-                w.rec, w.counts, w.pos_of, w.route_at, w.xa, w.xsum, n, topk, L->E, L->H, nb, x_dtype, rescale };
+                w.rec, w.counts, w.pos_of, w.route_at, w.e_at, w.xa, w.xsum, n, topk, L->E, L->H, nb, x_dtype, rescale };
     hipLaunchKernelGGL(k_route_prep, dim3(2 * n * nb), dim3(256), 0, s, p);
 }
 
@@ -712,9 +717,9 @@ static void launch_partial(const mm_layer_t* L, const Ws& w, int n, hipStream_t 
         hipLaunchKernelGGL((k_partial<MODE, false>), grid, block, 0, s, p);
 }
 
-static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int n, const int64_t* ids, hipStream_t s)
+static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int n, hipStream_t s)
 {
-    GuEpiArgs g{ w.part_gu, w.xsum, w.counts, w.route_at, ids, L->svh13, L->suh2, w.xd, w.xdsum, n, L->I,
+    GuEpiArgs g{ w.part_gu, w.xsum, w.counts, w.e_at, L->svh13, L->suh2, w.xd, w.xdsum, n, L->I,
                  prep_blocks(L->H), partial_waves(), piece_cap(n), (L->flags & MM_LAYER_EXACT) ? 0 : 1, L->limit };
     hipLaunchKernelGGL(k_gu_epilogue, dim3((n * (L->I / GV_COLS) + 3) / 4), dim3(256), 0, s, g);
 }
@@ -752,7 +757,7 @@ int mm_expert_gemv(const mm_layer_t* L, const void* x, int x_dtype, int rescale,
     const Ws w = carve(workspace, n, L->E, L->H, L->I);
     if (phases & 1) launch_prep(L, w, x, x_dtype, rescale, n, topk, ids, offsets, order, active, nactive, s);
     if (phases & 2) launch_partial<0>(L, w, n, s);
-    if (phases & 4) launch_gu_epilogue(L, w, n, ids, s);
+    if (phases & 4) launch_gu_epilogue(L, w, n, s);
     if (phases & 8) launch_partial<1>(L, w, n, s);
     if (phases & 16)
         hipLaunchKernelGGL(k_down_y, dim3((n * (L->H / GV_COLS) + 3) / 4), dim3(256), 0, s,
@@ -773,7 +778,7 @@ int mm_moe_decode(const mm_layer_t* L, const void* x, int x_dtype, int rescale, 
     const Ws ws = carve(workspace, n, L->E, L->H, L->I);
     launch_prep(L, ws, x, x_dtype, rescale, n, topk, ids, nullptr, nullptr, nullptr, nullptr, s);
     launch_partial<0>(L, ws, n, s);
-    launch_gu_epilogue(L, ws, n, ids, s);
+    launch_gu_epilogue(L, ws, n, s);
     launch_partial<1>(L, ws, n, s);
     const int threads = 64 * (topk < 2 ? 2 : topk);
     hipLaunchKernelGGL(k_down_combine, dim3(T * (L->H / GV_COLS)), dim3(threads), 0, s,
