@@ -26,7 +26,7 @@
 // per-weight rounding is spent. With MM_LAYER_EXACT every weight is rounded to fp16 first (v_pk_fma_f16), the
 // reference's EXACT expert (ft_core.h:977-1011). fp16 activations, fp32 accumulation, fp16 rounding at the
 // reference's points in both.
-#include "mm_common.h"
+#include "mm_decode.h"
 
 namespace mm {
 
@@ -42,21 +42,6 @@ constexpr int WAVES_PER_CU = 16;      // partial kernels: 4 workgroups of 4 wave
 constexpr int PREP_ROWS = 512;        // input rows per route-prep workgroup
 constexpr int MAX_TOPK = 16;
 
-typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
-typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
-typedef float float4_t __attribute__((ext_vector_type(4)));
-
-// One active expert of a call: its id, route count, first sorted position and matrix addresses.
-struct ExpertRec
-{
-    int32_t e, cnt, first, pad;
-    int64_t w[3];             // gate, up, down trellis
-    int64_t pad2;
-};
-
-__device__ __forceinline__ float kinv_f() { return h2f(KINV_BITS); }
-__device__ __forceinline__ float kbias_f() { return h2f(KBIAS_BITS); }
-
 // Row ranges per segment of a partial launch: as many equal pieces as fit one wave each (at least 1, at most
 // cap). Kernels 2-5 derive it from the same inputs, so they agree on the layout of the partial sums.
 __device__ __forceinline__ int pieces_per_segment(int nwaves, int nseg, int cap)
@@ -65,112 +50,7 @@ __device__ __forceinline__ int pieces_per_segment(int nwaves, int nseg, int cap)
     return p < 1 ? 1 : (p > cap ? cap : p);
 }
 
-// ------------------------------------------------------------------------------------------------ decode
-
-// The multiply-accumulate runs on v_mfma_f32_16x16x32_f16 over two tile rows at a time: A = transformed inputs
-// [16 routes][32 rows], B = two decoded 16x16 tiles stacked along k, D = [16 routes][16 columns]. Lane l of B
-// holds column n = l & 15 and MFMA k-group g = l >> 4 (8 values). A dot product does not depend on the order of
-// its terms, so the k-group need not be adjacent rows: k-group g is rows (2g, 2g+1, 2g+8, 2g+9) of the first tile
-// and the same rows of the second, which in column n are the 4 consecutive trellis states i0 .. i0+3 of each
-// tile with i0 = 32 (n & 7) + 8 g + 4 (n >> 3) (PERM, ft_core.h:48-61). A carries the same rows of the inputs,
-// so each lane decodes 4 adjacent states per tile and nothing moves between lanes.
-//
-// The 4 states span 25 stream bits ending at e = 3 i0 + 11, which lie in tile dwords b - 1 and b (b = e >> 5;
-// dword -1 is dword 23: the stream wraps). One v_alignbit puts state i0 + 3 - j at bits 3j .. 3j + 15.
-// The (1024 + bytesum) fp16 codes of a state pair come out packed from v_sad_u8 / v_sad_hi_u8 with 0x6400 in
-// both accumulator halves; EXACT applies KINV, KBIAS with one v_pk_fma_f16 (a single rounding).
-template <bool EXACT>
-__device__ __forceinline__ half4_t decode4(uint32_t hi, uint32_t lo, uint32_t sh)
-{
-    const uint32_t X = __builtin_amdgcn_alignbit(hi, lo, sh);
-    const uint32_t p0 = __builtin_amdgcn_ubfe(X, 9, 16) * MUL1;
-    const uint32_t p1 = __builtin_amdgcn_ubfe(X, 6, 16) * MUL1;
-    const uint32_t p2 = __builtin_amdgcn_ubfe(X, 3, 16) * MUL1;
-    const uint32_t p3 = (X & 0xffffu) * MUL1;
-    const uint32_t v01 = __builtin_amdgcn_sad_hi_u8(p1, 0u, __builtin_amdgcn_sad_u8(p0, 0u, 0x64006400u));
-    const uint32_t v23 = __builtin_amdgcn_sad_hi_u8(p3, 0u, __builtin_amdgcn_sad_u8(p2, 0u, 0x64006400u));
-    half2_t w01 = __builtin_bit_cast(half2_t, v01), w23 = __builtin_bit_cast(half2_t, v23);
-    if constexpr (EXACT)
-    {
-        const half2_t kinv = { __builtin_bit_cast(_Float16, KINV_BITS), __builtin_bit_cast(_Float16, KINV_BITS) };
-        const half2_t kbias = { __builtin_bit_cast(_Float16, KBIAS_BITS), __builtin_bit_cast(_Float16, KBIAS_BITS) };
-        w01 = __builtin_elementwise_fma(w01, kinv, kbias);
-        w23 = __builtin_elementwise_fma(w23, kinv, kbias);
-    }
-    return half4_t{ w01[0], w01[1], w23[0], w23[1] };
-}
-
-// MFMA operand order of each 16-row group of an input row: dword 2g + h holds rows (2g + 8h, 2g + 8h + 1), so
-// the lane of k-group g reads its four rows (2g, 2g+1, 2g+8, 2g+9) with one 8-byte load.
-__device__ __forceinline__ int operand_index(int k)
-{
-    const int d = (k & 15) >> 1;
-    return (k & ~15) + 2 * (2 * (d & 3) + (d >> 2)) + (k & 1);
-}
-
-// Waits written as inline asm with a memory clobber, so the compiler neither moves LDS accesses across them
-// nor drops them: buffer-to-LDS loads are counted by vmcnt but their LDS writes are invisible to the compiler.
-template <int N>
-__device__ __forceinline__ void wait_vmcnt()
-{
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-__device__ __forceinline__ void wait_lgkm0() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
-
-__device__ __forceinline__ float wave_sum(float v)
-{
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    return v;
-}
-
-// Sum of p[0 .. count) by one wave: one load per lane (all in flight together), then a fixed reduction tree.
-__device__ __forceinline__ float wave_sum_of(const float* p, int count)
-{
-    const int lane = threadIdx.x & 63;
-    float v = 0.0f;
-    for (int i = lane; i < count; i += 64) v += p[i];
-    return wave_sum(v);
-}
-
 // ------------------------------------------------------------------------------------------ 1. route prep
-
-struct PrepArgs
-{
-    const void* x;            // [T][H], element type x_dtype
-    const int64_t* ids;       // [n]
-    const int32_t* offsets;   // permutation (null: routing found here from ids)
-    const int32_t* order;
-    const int32_t* active;
-    const int32_t* nactive_in;
-    const int64_t* wtab0;     // gate, up, down pointer tables
-    const int64_t* wtab1;
-    const int64_t* wtab2;
-    const uint16_t* suh13;    // [E][2][H]
-    ExpertRec* rec;           // [max_active]
-    int32_t* counts;          // [2]: active experts, routed (valid) routes
-    int32_t* pos_of;          // [n] sorted position of each route, -1 if its id is outside [0, E)
-    int32_t* route_at;        // [n] route at each sorted position
-    int32_t* e_at;            // [n] expert at each sorted position
-    uint16_t* xa;             // [n][2][H] fp16 in operand order
-    float* xsum;              // [n][2][nb] sums of xa over each workgroup's rows
-    int n, topk, E, H, nb, x_dtype, rescale;
-};
-
-__device__ __forceinline__ float load_x(const void* x, int dtype, size_t i)
-{
-    if (dtype == MM_DTYPE_F16) return h2f(static_cast<const uint16_t*>(x)[i]);
-    if (dtype == MM_DTYPE_BF16) return __uint_as_float((uint32_t) static_cast<const uint16_t*>(x)[i] << 16);
-    return static_cast<const float*>(x)[i];
-}
-
-__device__ __forceinline__ int wave_sum_int(int v)
-{
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    return v;
-}
 
 // Every load that does not depend on another is issued before the first barrier (the route's id, all ids for
 // the position, the token row for the rescale, this wave's block of it), and the routing counts and the row's
@@ -383,7 +263,7 @@ __global__ __launch_bounds__(GV_THREADS, 4) void k_partial(PartArgs a)
             const int nr = min(16, cnt - r0);
             // this lane's A row: routes past nr repeat a valid one and their outputs are never stored
             const int pos = rc.first + r0 + min(col, nr - 1);
-            const uint32_t xoff = (uint32_t)(((size_t)pos * NMAT + m) * a.K * 2) + (uint32_t)g * 8;
+            const uint32_t xoff = (uint32_t)(((size_t)pos * NMAT + m) * a.K * 2) + (uint32_t)g * 16;
             float4_t acc[8];
 #pragma unroll
             for (int c = 0; c < 8; ++c) acc[c] = float4_t{ 0.f, 0.f, 0.f, 0.f };
@@ -396,7 +276,9 @@ __global__ __launch_bounds__(GV_THREADS, 4) void k_partial(PartArgs a)
                 const uint32_t tr = (uint32_t)(tr0 + t);
                 __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, &ring[(wave * GV_RING + j) * SLOT], 12,
                                                          (uint32_t)lane * 12, in ? tr * row_bytes + wcol : wbytes, 0, 0);
-                areg[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xres, xoff, in ? tr * 32 : xbytes, 0));
+                // operand order: tile row tr's 4 inputs of k-group g at byte 64 (tr / 2) + 16 g + 8 (tr % 2)
+                const uint32_t xrow = (tr >> 1) * 64 + (tr & 1) * 8;
+                areg[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xres, xoff, in ? xrow : xbytes, 0));
             };
             // rows j and j + 1 (ring slots) through one MFMA per tile; a row past the range has zero inputs
             auto pair_mma = [&](int j) {
@@ -624,7 +506,12 @@ struct Ws
     size_t bytes;
 };
 
-static int prep_blocks(int H) { return (H + PREP_ROWS - 1) / PREP_ROWS; }
+int prep_blocks(int H) { return (H + PREP_ROWS - 1) / PREP_ROWS; }
+
+void launch_route_prep(const PrepArgs& p, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_route_prep, dim3(2 * p.n * p.nb), dim3(256), 0, s, p);
+}
 
 // Most row ranges per segment a partial launch may use: bounded so the partial sums stay a few MB.
 static int piece_cap(int n)
@@ -701,7 +588,7 @@ static void launch_prep(const mm_layer_t* L, const Ws& w, const void* x, int x_d
     const int nb = prep_blocks(L->H);
     PrepArgs p{ x, ids, offsets, order, active, nactive, L->gate_ptr, L->up_ptr, L->down_ptr, L->suh13,
                 w.rec, w.counts, w.pos_of, w.route_at, w.e_at, w.xa, w.xsum, n, topk, L->E, L->H, nb, x_dtype, rescale };
-    hipLaunchKernelGGL(k_route_prep, dim3(2 * n * nb), dim3(256), 0, s, p);
+    launch_route_prep(p, s);
 }
 
 template <int MODE>

@@ -45,6 +45,9 @@ _SIGS = {
     "mm_expert_gemv": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp, sz,
                              i32, vp]),
     "mm_moe_decode": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, sz, vp]),
+    "mm_prefill_workspace": (sz, [i32, i32, i32, i32]),
+    "mm_grouped_gemm": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, i32, vp, vp, sz, vp]),
+    "mm_moe_prefill": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, i32, i32, vp, vp, sz, vp]),
     "mm_synth_u16": (i32, [vp, u64, u64, u64, vp]),
     "mm_synth_layer": (i32, [ctypes.POINTER(MMLayer), u64, vp]),
     "mm_expert_seed": (u64, [u64, u64]),

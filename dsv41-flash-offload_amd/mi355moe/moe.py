@@ -77,27 +77,79 @@ def combine(Y, ids, w, T, k, H, E, out=None, stream=None):
     return out
 
 
-def moe_forward(store, x, ids, w, shared_expert=None, use_permutation=None, stream=None):
-    """out fp32 [T, H] = sum_j w[t, j] * expert_{ids[t, j]}(x_t) (+ expert `shared_expert` with weight 1).
-
-    Routes with ids outside [0, E) contribute nothing. The decode path serves up to GEMV_MAX_ROWS routes
-    per expert. Routing is found in-kernel for up to 1024 routes, else through permute()."""
-    T = x.shape[0]
+def _with_shared(ids, w, T, shared_expert):
     ids = ids.reshape(T, -1).long()
     w = w.reshape(T, -1).float()
     if shared_expert is not None:
         ids = torch.cat([ids, torch.full((T, 1), int(shared_expert), dtype=torch.long, device=ids.device)], 1)
         w = torch.cat([w, torch.ones((T, 1), dtype=torch.float32, device=w.device)], 1)
+    return ids.contiguous(), w.contiguous()
+
+
+def moe_forward(store, x, ids, w, shared_expert=None, use_permutation=None, fat_threshold=GEMV_MAX_ROWS, stream=None):
+    """out fp32 [T, H] = sum_j w[t, j] * expert_{ids[t, j]}(x_t) (+ expert `shared_expert` with weight 1).
+
+    Routes with ids outside [0, E) contribute nothing. As the reference's fused-MoE call does
+    (patches/vllm-exl3-host-dma.patch:241-290), experts with more than `fat_threshold` routes (at most
+    GEMV_MAX_ROWS) go to the fat-expert grouped GEMM, added to the decode path's sum; the others run on the
+    decode path, whose routing is found in-kernel for up to 1024 routes, else through permute()."""
+    T = x.shape[0]
+    ids, w = _with_shared(ids, w, T, shared_expert)
     k = ids.shape[1]
     n = T * k
+    fat_threshold = min(int(fat_threshold), GEMV_MAX_ROWS)
     routes = permute(ids, w, k, store.E, stream)
-    max_rows = int(routes["counts"][: store.E].max().item()) if n else 0
-    if max_rows > GEMV_MAX_ROWS:
-        raise NotImplementedError(f"expert with {max_rows} routes: the fat-expert path is required (> {GEMV_MAX_ROWS})")
+    counts = routes["counts"][: store.E]
+    max_rows = int(counts.max().item()) if n else 0
+    if max_rows > fat_threshold:
+        valid = (ids >= 0) & (ids < store.E)
+        fat = valid & (counts.long()[ids.clamp(0, store.E - 1)] > fat_threshold)
+        std_ids = ids.masked_fill(fat, -1)
+        out = moe_forward(store, x, std_ids, w, use_permutation=use_permutation, fat_threshold=fat_threshold,
+                          stream=stream) if bool((valid & ~fat).any().item()) else torch.zeros(
+                              (T, store.H), dtype=torch.float32, device=x.device)
+        return moe_prefill(store, x, ids.masked_fill(~fat, -1), w, cap=fat_threshold, out=out, stream=stream)
     if use_permutation is None:
         use_permutation = n > 1024
     Y = expert_gemv(store, x, ids, T, n, k, max(1, max_rows), routes if use_permutation else None, stream=stream)
     return combine(Y, ids, w, T, k, store.H, store.E, stream=stream)
+
+
+def _prefill_ws(store, n, dev):
+    wsb = _lib.load().mm_prefill_workspace(n, store.E, store.H, store.I)
+    return torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev), wsb
+
+
+def grouped_gemm(store, x, ids, cap=0, stream=None):
+    """Fat-expert path: per-route expert outputs Y fp32 [n, H] (flat route order) of every route whose expert has
+    more than `cap` routes (other rows stay zero). Weights decoded as fp16, multiplied on MFMA."""
+    T = x.shape[0]
+    ids = ids.reshape(T, -1).contiguous().long()
+    k = ids.shape[1]
+    n = T * k
+    x = x.contiguous()
+    ws, wsb = _prefill_ws(store, n, x.device)
+    Y = torch.zeros((n, store.H), dtype=torch.float32, device=x.device)
+    _lib.call("mm_grouped_gemm", store.mm_layer(), _i(x), x_dtype_of(x), T, k, _i(ids), int(cap), _i(Y), _i(ws), wsb,
+              _lib.stream_ptr(stream))
+    return Y
+
+
+def moe_prefill(store, x, ids, w, cap=0, out=None, shared_expert=None, stream=None):
+    """Prefill MoE layer on the fat-expert path: out fp32 [T, H] (+)= sum_j w[t, j] * expert_{ids[t, j]}(x_t)
+    over the routes whose expert has more than `cap` routes. With `out` given the sum is added to it (the
+    reference's apply_exl3_batched_fat accumulation, patches/vllm-exl3-host-dma.patch:182-201)."""
+    T = x.shape[0]
+    ids, w = _with_shared(ids, w, T, shared_expert)
+    k = ids.shape[1]
+    x = x.contiguous()
+    ws, wsb = _prefill_ws(store, T * k, x.device)
+    acc = out is not None
+    if out is None:
+        out = torch.empty((T, store.H), dtype=torch.float32, device=x.device)
+    _lib.call("mm_moe_prefill", store.mm_layer(), _i(x), x_dtype_of(x), T, k, _i(ids), _i(w), int(cap), 1 if acc else 0,
+              _i(out), _i(ws), wsb, _lib.stream_ptr(stream))
+    return out
 
 
 class DecodeRunner:

@@ -151,6 +151,30 @@ int mm_moe_decode(const mm_layer_t* layer, const void* x, int x_dtype, int resca
                   const int64_t* ids, const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes,
                   mm_stream_t stream);
 
+/* ------------------------------------------------------------------------------ fat experts (prefill) */
+
+/* Bytes of device workspace mm_grouped_gemm / mm_moe_prefill need for n routes over E experts (permutation,
+ * per-expert records, transformed inputs, the down input and per-route outputs). */
+size_t mm_prefill_workspace(int n, int E, int H, int I);
+
+/* Fat-expert grouped GEMM (replaces apply_exl3_batched_fat's per-expert reconstruct + 128x128 GEMM,
+ * patches/vllm-exl3-host-dma.patch:182-201, and runtime/dma_gemm.py:5-26 run_batch, which feeds it): for every
+ * route s < T*topk whose expert (0 <= ids[s] < E) has more than cap routes in the call, computes the expert
+ * SwiGLU MLP and writes Y fp32 [T*topk][H] row s; other rows are left untouched. The weights are decoded into LDS
+ * as fp16 (the reconstruct's rounding, ft_core.h:75-83) once per 128 routes and multiplied on MFMA; fp16
+ * activations, fp32 accumulation, fp16 rounding at the reference's points. x, x_dtype as for mm_expert_gemv
+ * (no rescale). Needs H a multiple of 256, I of 128, E <= 1024. */
+int mm_grouped_gemm(const mm_layer_t* layer, const void* x, int x_dtype, int T, int topk, const int64_t* ids, int cap,
+                    float* Y, void* workspace, size_t workspace_bytes, mm_stream_t stream);
+
+/* Prefill MoE layer: mm_grouped_gemm, then out fp32 [T][H] = (accumulate ? out : 0) + sum_j w[t,j] * y_{t,j}
+ * over the routes j whose expert has more than cap routes, fp32 fma in ascending j. cap = 0, accumulate = 0 is
+ * the whole layer (equal to mm_combine over the routes' rows); cap = the fat threshold with accumulate = 1 adds the
+ * fat experts to an out that already holds the other routes, as apply_exl3_batched_fat does. */
+int mm_moe_prefill(const mm_layer_t* layer, const void* x, int x_dtype, int T, int topk, const int64_t* ids,
+                   const float* w, int cap, int accumulate, float* out, void* workspace, size_t workspace_bytes,
+                   mm_stream_t stream);
+
 /* ----------------------------------------------------------------------------------------- utility */
 
 /* Synthetic trellis words: word i of a stream with `seed` is bits 16*(i%4)..+15 of
