@@ -3,99 +3,196 @@
 // patches/vllm-exl3-host-dma.patch:182-201, runtime/dma_gemm.py:5-26, which reconstruct fp16 weights and run a
 // 128x128 GEMM).
 //
-// A workgroup (8 waves) owns a tile of 128 routes (sorted positions of one expert) x 256 output columns:
-//   gate/up (k_fat<0>): gate columns 128 c .. 128 c + 127 and the same up columns, so the epilogue holds both and
-//                       applies the output transforms, SwiGLU and the down-input transform of that 128-block
-//                       (the transforms act within 128-blocks);
-//   down    (k_fat<1>): two 128-blocks of H; the epilogue applies the output transform and writes per-route rows.
-// Per 32-row step (two tile rows) the workgroup loads the routes' transformed inputs (buffer-to-LDS, 4 steps
-// ahead) and the 32 trellis tiles of its columns (768-byte rows, buffer-to-LDS, 12 steps ahead), every wave
-// decodes 4 tiles into the MFMA B layout (fp16 weights rounded as the reference's EXACT expert), and each wave
-// multiplies a 64 x 64 sub-tile on v_mfma_f32_16x16x32_f16. The weights are decoded once per 128 routes.
+// Launches: mm_permute (sorted positions) -> k_fat_prep (transformed inputs per sorted position) -> k_fat_plan
+// (expert records and the two tile lists) -> k_fat<0, 8>, k_fat<0, 4> (gate/up) -> k_fat<1, 8>, k_fat<1, 4> (down)
+// -> k_fat_combine.
+//
+// A workgroup (8 waves, two per SIMD) owns a tile of 256 routes (sorted positions of one expert; 128 for an
+// expert's last <= 128 routes) x 256 output columns:
+//   gate/up (MODE 0): gate columns 128 c .. 128 c + 127 and the same up columns, so the epilogue holds both and
+//                     applies the output transforms, SwiGLU and the down-input transform of that 128-block (the
+//                     transforms act within 128-blocks);
+//   down    (MODE 1): two 128-blocks of H; the epilogue applies the output transform and writes per-route rows.
+// Per 32-row step (two tile rows) the inputs (buffer-to-LDS, FT_PA - 1 steps ahead) and the 32 trellis tiles of
+// the columns (768-byte rows, buffer-to-LDS, FT_PT steps ahead) are staged in LDS by loader waves; every wave
+// decodes 4 tiles of the next step into the MFMA B layout (fp16 weights, rounded as the reconstruct does) in
+// between its v_mfma_f32_16x16x32_f16 over a (BM / 2) x 64 sub-tile (128 accumulators per lane), so one wave's
+// decode runs while the other wave of its SIMD multiplies. The weights are decoded once per tile.
 #include "mm_decode.h"
 
 namespace mm {
 
-constexpr int FT_BM = 128;          // routes per tile
+constexpr int FT_BIG = 256;         // routes per tile (8 row blocks per row-wave)
+constexpr int FT_SMALL = 128;       // routes per tile for an expert's remainder of at most 128 routes
 constexpr int FT_BN = 256;          // output columns per tile
 constexpr int FT_WAVES = 8;
 constexpr int FT_THREADS = 64 * FT_WAVES;
-constexpr int FT_PA = 4;            // input steps in flight
-constexpr int FT_PT = 12;           // trellis steps in flight
+constexpr int FT_PA = 3;            // input ring stages (loads run FT_PA - 1 steps ahead)
+constexpr int FT_PT = 5;            // trellis steps in flight
 constexpr int FT_TS = FT_PT + 1;    // trellis ring slots
 constexpr int FT_PLAN_MAX = 1024;   // active experts the plan kernel handles
 
 struct FatArgs
 {
-    const ExpertRec* rec;
-    const int32_t* counts;        // [0] active experts
-    const int32_t* tile_off;      // [max_active + 1] first tile of each active expert (exclusive prefix)
+    const ExpertRec* rec;         // [max_active] active experts (permutation order)
+    const int32_t* nactive;       // [1]
+    const int32_t* tile_off;      // [max_active + 1] first tile of each active expert in this launch's list
+    const int32_t* big_off;       // [max_active + 1] 224-route tiles (a 96-route tile follows them)
     const uint16_t* xa;           // mode 0: [n][2][H]; mode 1: [n][I] (operand order)
     const uint16_t* svh13;        // [E][2][I]
     const uint16_t* suh2;         // [E][I]
     const uint16_t* svh2;         // [E][H]
-    const int32_t* route_at;      // [n]
+    const int32_t* route_at;      // [n] flat route index of each sorted position
     uint16_t* xd;                 // mode 0 output [n][I] (operand order)
     float* Y;                     // mode 1 output [n_routes][H] (per route)
     int H, I, K, N, nunits, max_active;
     float limit;
 };
 
-// Tiles of each active expert with more than cap routes: tile_off[a] = tiles of experts 0 .. a-1.
-__global__ __launch_bounds__(FT_PLAN_MAX) void k_fat_plan(const ExpertRec* rec, const int32_t* counts, int32_t* tile_off,
+// Transformed inputs of every fat route, one workgroup per sorted position (the expert's 2 x H/128 blocks, 4
+// waves): xa[pos][m] = r16(FWHT(x16 * suh_m) * HAD) per 128-block in operand order (ft_core.h:96-102), where
+// x16 is fp16 input as is, or bf16 / fp32 input rounded through bf16.
+__global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, const int64_t* ids, const int32_t* counts,
+                                                  const int32_t* offsets, const int32_t* order, const uint16_t* suh13,
+                                                  uint16_t* xa, int topk, int E, int H, int cap)
+{
+    const int pos = blockIdx.x;
+    if (pos >= offsets[E]) return;
+    const int s = order[pos];
+    const int e = (int)ids[s];
+    if (counts[e] <= cap) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const size_t row = (size_t)(s / topk) * H;
+    const int nb = H / 128;
+#pragma unroll 4
+    for (int b = wave; b < 2 * nb; b += 4)
+    {
+        const int m = b / nb, h0 = (b % nb) * 128;
+        float va = load_x(x, x_dtype, row + h0 + lane);
+        float vb = load_x(x, x_dtype, row + h0 + lane + 64);
+        const uint16_t* su = suh13 + ((size_t)e * 2 + m) * H + h0;
+        const float sa = h2f(su[lane]), sb = h2f(su[lane + 64]);
+        if (x_dtype != MM_DTYPE_F16)
+        {
+            va = r16(bf16_value(va));
+            vb = r16(bf16_value(vb));
+        }
+        prep_block_wave(va, vb, sa, sb);
+        uint16_t* dst = xa + ((size_t)pos * 2 + m) * H;
+        dst[operand_index(h0 + lane)] = f2h(va);
+        dst[operand_index(h0 + lane + 64)] = f2h(vb);
+    }
+}
+
+// Expert records and the tile lists of the experts with more than cap routes. An expert of c routes gets
+// c / 256 tiles of 256 routes; a remainder r = c % 256 takes one more 256-route tile if r > 128 (a 256-route step
+// costs less than two 128-route steps), else one 128-route tile. off_big / off_small = tiles of active experts
+// 0 .. a-1 in each list.
+__global__ __launch_bounds__(FT_PLAN_MAX) void k_fat_plan(const int32_t* counts, const int32_t* offsets,
+                                                         const int32_t* active, const int32_t* nactive,
+                                                         const int64_t* gate, const int64_t* up, const int64_t* down,
+                                                         ExpertRec* rec, int32_t* off_big, int32_t* off_small,
                                                          int max_active, int cap)
 {
-    __shared__ int s_w[FT_PLAN_MAX / 64];
+    __shared__ int s_w[2][FT_PLAN_MAX / 64];
     const int a = threadIdx.x, lane = a & 63, wave = a >> 6;
-    const int nact = counts[0];
-    const int c = (a < nact && a < max_active) ? rec[a].cnt : 0;
-    const int tiles = c > cap ? (c + FT_BM - 1) / FT_BM : 0;
-    int incl = tiles;
+    const int nact = min(nactive[0], max_active);
+    int c = 0;
+    if (a < nact)
+    {
+        const int e = active[a];
+        c = counts[e];
+        ExpertRec r{ e, c, offsets[e], 0, { gate[e], up[e], down[e] }, 0 };
+        rec[a] = r;
+    }
+    int tb = 0, ts = 0;
+    if (c > cap)
+    {
+        const int r = c % FT_BIG;
+        tb = c / FT_BIG + (r > FT_SMALL ? 1 : 0);
+        ts = (r > 0 && r <= FT_SMALL) ? 1 : 0;
+    }
+    int ib = tb, is = ts;
 #pragma unroll
     for (int d = 1; d < 64; d <<= 1)
     {
-        const int o = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += o;
+        const int o1 = __shfl_up(ib, d, 64), o2 = __shfl_up(is, d, 64);
+        if (lane >= d)
+        {
+            ib += o1;
+            is += o2;
+        }
     }
-    if (lane == 63) s_w[wave] = incl;
+    if (lane == 63)
+    {
+        s_w[0][wave] = ib;
+        s_w[1][wave] = is;
+    }
     __syncthreads();
-    int before = 0, total = 0;
+    int bb = 0, bs = 0, nb = 0, ns = 0;
     for (int w = 0; w < FT_PLAN_MAX / 64; ++w)
     {
-        if (w < wave) before += s_w[w];
-        total += s_w[w];
+        if (w < wave)
+        {
+            bb += s_w[0][w];
+            bs += s_w[1][w];
+        }
+        nb += s_w[0][w];
+        ns += s_w[1][w];
     }
-    if (a < max_active) tile_off[a] = before + incl - tiles;
-    if (a == 0) tile_off[max_active] = total;
+    if (a < max_active)
+    {
+        off_big[a] = bb + ib - tb;
+        off_small[a] = bs + is - ts;
+    }
+    if (a == 0)
+    {
+        off_big[max_active] = nb;
+        off_small[max_active] = ns;
+    }
 }
 
-template <int MODE>
+// LDS position of 16-byte chunk g of row r of an input stage (64-byte rows): the 16 rows one MFMA operand read
+// covers fall in distinct 16-byte bank groups both for 8 lanes over 32 banks and for 16 lanes over 64 banks.
+__device__ __forceinline__ int chunk_pos(int g, int r) { return g ^ (((r >> 1) ^ (r >> 2)) & 3); }
+
+// MB = 16-row blocks per row-wave: tiles of BM = 32 MB routes (256 or 128). 8 waves: wave (wm, wn) = (w >> 2,
+// w & 3) multiplies rows (BM / 2) wm .. + BM / 2 - 1 by column tiles 4 wn .. 4 wn + 3 of 16; waves 0 .. 3 also
+// load the trellis (chunk w: tile row w >> 1 of matrix / block w & 1) and waves 4 .. 7 the inputs, so each wave's
+// loads are of one kind and complete in issue order within their own lead; wave w decodes tiles 4 (w & 1) .. + 3
+// of chunk w >> 1. Rows past the tile's routes read zero inputs.
+template <int MODE, int MB>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
 {
+    constexpr int BM = 32 * MB;
     constexpr int NA = MODE == 0 ? 2 : 1;                        // input matrices (gate, up share the tile)
-    constexpr int LA = 2 * NA;                                   // input loads per loader wave and step
-    constexpr int A_STAGE = NA * FT_BM * 64;                     // bytes of one step's inputs
+    constexpr int A_STAGE = NA * BM * 64;                        // one step's inputs
+    constexpr int LA = A_STAGE / 1024 / 4;                       // input loads (1 KB each) per loader wave and step
     constexpr int T_SLOT = 4 * 1024;                             // one step's trellis: 4 chunks of 8 tiles
-    constexpr int B_BUF = 16 * 64 * 16;                          // decoded B of one step
-    constexpr int A_BYTES = FT_PA * A_STAGE, T_BYTES = FT_TS * T_SLOT, B_BYTES = 2 * B_BUF;
-    constexpr int C_STRIDE = FT_BN * 2 + 16;                     // epilogue tile row (fp16), padded
-    constexpr int MAIN = A_BYTES + T_BYTES + B_BYTES;
-    constexpr int SMEM = MAIN > FT_BM * C_STRIDE ? MAIN : FT_BM * C_STRIDE;
+    constexpr int B_BUF = 16 * 64 * 16;                          // decoded B of one step: 16 tiles x 64 lanes
+    constexpr int A_BYTES = FT_PA * A_STAGE, T_BYTES = FT_TS * T_SLOT;
+    constexpr int MAIN = A_BYTES + T_BYTES + 2 * B_BUF;
+    constexpr int CS = BM + 2;                                   // transposed C tile: column stride in halves
+    constexpr int SMEM = MAIN > FT_BN * CS * 2 ? MAIN : FT_BN * CS * 2;
     static_assert(SMEM <= 160 * 1024, "LDS");
+    static_assert(((CS / 2) & 1) == 1, "odd dword stride: conflict-free column reads");
+    static_assert(MB % 2 == 0, "one decoded tile per two row blocks");
     __shared__ __align__(16) uint8_t smem[SMEM];
     uint8_t* Aring = smem;
     uint8_t* Tring = smem + A_BYTES;
     uint8_t* Bdec = smem + A_BYTES + T_BYTES;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    // ---- tile. Consecutive tiles (the column blocks of one 128-route block, then the next block of the same
-    // expert) go to one XCD, so they share its L2 for the inputs and the trellis.
-    const int nblk = gridDim.x;                                  // a multiple of 8
-    const int L = (int)(blockIdx.x & 7) * (nblk >> 3) + (int)(blockIdx.x >> 3);
-    const int nact = min(a.counts[0], a.max_active);
+    // ---- tile. The grid is sized for the most tiles a call can have; the work = tiles x column blocks of this
+    // call is spread evenly over the 8 XCDs (workgroup b runs on XCD b % 8), and consecutive work items (the
+    // column blocks of one route block, then the next block of the same expert) stay on one XCD, so they share
+    // its L2 for the inputs and the trellis.
+    const int nact = min(a.nactive[0], a.max_active);
     const int total = a.tile_off[nact];
+    const int work = total * a.nunits, per_xcd = (work + 7) >> 3;
+    const int L = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+    if ((int)(blockIdx.x >> 3) >= per_xcd || L >= work) return;
     const int mt = L / a.nunits, nu = L % a.nunits;
-    if (mt >= total) return;
     int lo = 0, hi = nact - 1;
     while (lo < hi)
     {
@@ -103,10 +200,12 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
         if (a.tile_off[mid] <= mt) lo = mid; else hi = mid - 1;
     }
     const ExpertRec* rp = a.rec + lo;
-    const int row0 = (mt - a.tile_off[lo]) * FT_BM;
-    const int rows = __builtin_amdgcn_readfirstlane(min(FT_BM, rp->cnt - row0));
+    // an expert's 256-route tiles come first; its 128-route tile (if any) follows them
+    const int row0 = BM == FT_BIG ? (mt - a.tile_off[lo]) * BM : (a.big_off[lo + 1] - a.big_off[lo]) * FT_BIG;
+    const int rows = __builtin_amdgcn_readfirstlane(min(BM, rp->cnt - row0));
     const int pos0 = __builtin_amdgcn_readfirstlane(rp->first + row0);
     const int e = __builtin_amdgcn_readfirstlane(rp->e);
+    const int S = a.K / 32;
 
     // ---- buffer descriptors (wave-uniform bases through readfirstlane, each half widened as uint32_t)
     auto uniform_ptr = [](const void* p) {
@@ -115,170 +214,204 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
         const uint32_t h = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
         return reinterpret_cast<void*>((uintptr_t)((uint64_t)l | ((uint64_t)h << 32)));
     };
+    const bool tloader = wave < 4;
+    // trellis loader (waves 0 .. 3): chunk q = wave of step s is tile row 2 s + (q >> 1) of matrix q & 1 (gate/up)
+    // or of column block 2 nu + (q & 1) (down), 8 tiles = 768 bytes, 12 bytes per lane stored 16 bytes apart.
+    // Steps past the end reload the last row into the free slot, so every step issues one load.
+    const int tq = wave & 3;
+    const uint32_t row_bytes = (uint32_t)(a.N / 16) * 96, wbytes = (uint32_t)(a.K / 16) * row_bytes;
+    const void* wbase = (const void*)(uintptr_t)(MODE == 0 ? ((tq & 1) ? rp->w[1] : rp->w[0]) : rp->w[2]);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(wbase), (short)0, (int)wbytes,
+                                                                          0x00020000);
+    const uint32_t wcol = MODE == 0 ? (uint32_t)nu * 768 : (uint32_t)(2 * nu + (tq & 1)) * 768;
+    auto load_trellis = [&](int s) {
+        const uint32_t tr = (uint32_t)(2 * min(s, S - 1) + (tq >> 1));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, Tring + (size_t)(s % FT_TS) * T_SLOT + (size_t)tq * 1024, 12,
+                                                 tr * row_bytes + wcol + (uint32_t)lane * 12, 0, 0, 0);
+    };
+    // input loader (waves 4 .. 7): LA loads of 16 rows each (4 lanes per 64-byte row step); chunk g of row r goes
+    // to chunk_pos(g, r). Rows past the tile's routes and steps past the end read out of range (zero, no access).
     const uint32_t a_row = (uint32_t)NA * a.K * 2;                       // bytes per route of the inputs
     const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
         uniform_ptr(a.xa + (size_t)pos0 * NA * a.K), (short)0, (int)((uint32_t)rows * a_row), 0x00020000);
-    const uint32_t row_bytes = (uint32_t)(a.N / 16) * 96, wbytes = (uint32_t)(a.K / 16) * row_bytes;
-    // trellis loader waves 0 .. 3 move chunk q = wave of every step: tile row 2 s + (q >> 1) of matrix q & 1
-    // (gate/up) or of column block 2 nu + (q & 1) (down), 8 tiles = 768 bytes
-    const int tb = wave & 1, tt = (wave >> 1) & 1;
-    const void* wbase = (const void*)(uintptr_t)(MODE == 0 ? (tb ? rp->w[1] : rp->w[0]) : rp->w[2]);
-    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(wbase), (short)0, (int)wbytes,
-                                                                          0x00020000);
-    const uint32_t wcol = MODE == 0 ? (uint32_t)nu * 768 : (uint32_t)(2 * nu + tb) * 768;
-    auto load_trellis = [&](int s) {       // 12 bytes per lane, stored 16 bytes apart
-        const uint32_t tr = (uint32_t)(2 * s + tt);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, Tring + (size_t)(s % FT_TS) * T_SLOT + (size_t)wave * 1024, 12,
-                                                 tr * row_bytes + wcol + (uint32_t)lane * 12, 0, 0, 0);
-    };
-    // input loader waves 4 .. 7: LA loads of 16 rows each (4 lanes per 64-byte row step). The 16-byte chunks of
-    // row r sit at chunk ^ ((r >> 2) & 3) so the MFMA operand reads spread over the LDS banks. Rows past the
-    // tile's routes are out of the descriptor's range and read as zero.
     auto load_inputs = [&](int s) {
         const int st = s % FT_PA;
+        const uint32_t ks = s < S ? (uint32_t)s * 64 : 0x40000000u;  // the range is below 2^30
 #pragma unroll
         for (int u = 0; u < LA; ++u)
         {
-            const int li = (wave - 4) * LA + u;                        // 0 .. 8 NA - 1
-            const int am = li >> 3, rb = li & 7;
+            const int li = (wave - 4) * LA + u;                        // 0 .. NA BM / 16 - 1
+            const int am = li / (BM / 16), rb = li % (BM / 16);
             const int r = rb * 16 + (lane >> 2), p = lane & 3;
-            const uint32_t voff = (uint32_t)r * a_row + (uint32_t)am * a.K * 2 + (uint32_t)s * 64 +
-                                  (uint32_t)(p ^ ((r >> 2) & 3)) * 16;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, Aring + (size_t)st * A_STAGE + ((size_t)am * FT_BM + rb * 16) * 64,
+            const uint32_t voff = (uint32_t)r * a_row + (uint32_t)am * a.K * 2 + (uint32_t)chunk_pos(p, r) * 16 + ks;
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, Aring + (size_t)st * A_STAGE + ((size_t)am * BM + rb * 16) * 64,
                                                      16, voff, 0, 0, 0);
         }
     };
 
-    // ---- decode: wave w owns chunk w >> 1 (tile row t, matrix or block b), tiles 4 (w & 1) .. + 3
+    // ---- decode: wave w owns chunk w >> 1 (tile row t = w >> 2 of matrix / block b = (w >> 1) & 1), tiles
+    // 4 (w & 1) .. + 3; lane (col, g) decodes states i0 .. i0+3 of column col in a tile
     const int col = lane & 15, g = lane >> 4;
     const int i0 = 32 * (col & 7) + 8 * g + 4 * (col >> 3);
     const int eb = 3 * i0 + 11;
     const int blo = eb >> 5, bhi = (blo + 23) % 24;
     const int llo = 4 * (blo / 3) + blo % 3, lhi = 4 * (bhi / 3) + bhi % 3;
     const uint32_t sh = 31u - (uint32_t)(eb & 31);
-    auto decode = [&](int s) {
-        const int q = wave >> 1, t = q >> 1, b = q & 1;
-        const uint32_t* slot = reinterpret_cast<const uint32_t*>(Tring + (size_t)(s % FT_TS) * T_SLOT + (size_t)q * 1024);
-        uint8_t* bd = Bdec + (size_t)(s & 1) * B_BUF;
+    const int dq = wave >> 1;
+    const uint32_t* tword = reinterpret_cast<const uint32_t*>(Tring + (size_t)dq * 1024) + (wave & 1) * 4 * 32;
+    uint8_t* bdst = Bdec + ((size_t)((dq & 1) * 8 + (wave & 1) * 4) * 64 + lane) * 16 + (dq >> 1) * 8;
+    // ---- MFMA: rows (BM / 2) wm + 16 i + col of input matrix wn >> 1 (gate/up), B tiles 4 wn .. + 3
+    const int wm = wave >> 2, wn = wave & 3;
+    const uint8_t* bsrc = Bdec + ((size_t)(wn * 4) * 64 + lane) * 16;
+    int aoff[MB];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+    {
+        const int r = wm * (BM / 2) + 16 * i + col;
+        aoff[i] = ((MODE == 0 ? (wn >> 1) : 0) * BM + r) * 64 + chunk_pos(g, r) * 16;
+    }
+    float4_t acc[MB][4];
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+
+    // Trellis loaders issue steps 0 .. FT_PT - 1 ahead of the loop and step s + FT_PT in step s: at the top of
+    // step s at most FT_PT - 2 of their loads may be outstanding (step s + 1 is complete). Input loaders issue
+    // steps 0 .. FT_PA - 2 ahead and step s + FT_PA - 1 in step s: at most (FT_PA - 2) LA outstanding (step s is
+    // complete). One barrier per step then publishes the loads and the tiles decoded in step s - 1.
+    if (tloader)
+    {
+        for (int s = 0; s < FT_PT; ++s) load_trellis(s);
+        wait_vmcnt<FT_PT - 1>();                                  // step 0
+    }
+    else
+        for (int s = 0; s < FT_PA - 1; ++s) load_inputs(s);
+    lds_barrier();
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+        *reinterpret_cast<half4_t*>(bdst + u * 1024) = decode4<true>(tword[u * 32 + lhi], tword[u * 32 + llo], sh);
+    for (int s = 0; s < S; ++s)
+    {
+        if (tloader) wait_vmcnt<FT_PT - 2>(); else wait_vmcnt<(FT_PA - 2) * LA>();
+        lds_barrier();
+        if (tloader) load_trellis(s + FT_PT); else load_inputs(s + FT_PA - 1);
+        // one step: the trellis words of step s + 1 and the B fragments of step s first, then per row block its 4
+        // MFMAs (operand read from LDS just before), one tile of step s + 1 decoded after every two blocks
+        const uint32_t* tw = tword + (size_t)((s + 1) % FT_TS) * (T_SLOT / 4);
+        uint32_t th[4], tl[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
         {
-            const int c = (wave & 1) * 4 + u;
-            const half4_t wv = decode4<true>(slot[c * 32 + lhi], slot[c * 32 + llo], sh);
-            *reinterpret_cast<half4_t*>(bd + ((size_t)(b * 8 + c) * 64 + lane) * 16 + t * 8) = wv;
+            th[u] = tw[u * 32 + lhi];
+            tl[u] = tw[u * 32 + llo];
         }
-    };
-    // ---- MFMA sub-tile of wave w: rows 64 (w >> 2) .. + 63, column tiles 4 (w & 3) .. + 3 of the 16
-    const int wm = wave >> 2, wn = wave & 3;
-    const int am_mfma = MODE == 0 ? (wn >> 1) : 0;
-    float4_t acc[4][4];
+        const uint8_t* as = Aring + (size_t)(s % FT_PA) * A_STAGE;
+        const uint8_t* bs = bsrc + (size_t)(s & 1) * B_BUF;
+        uint8_t* bd = bdst + (size_t)((s + 1) & 1) * B_BUF;
+        half8_t B[4];
 #pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
+        for (int j = 0; j < 4; ++j) B[j] = *reinterpret_cast<const half8_t*>(bs + j * 1024);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[mb][i] = float4_t{ 0.f, 0.f, 0.f, 0.f };
-    auto mfma = [&](int s) {
-        const uint8_t* as = Aring + (size_t)(s % FT_PA) * A_STAGE + (size_t)am_mfma * FT_BM * 64;
-        const uint8_t* bs = Bdec + (size_t)(s & 1) * B_BUF;
-        half8_t A[4], B[4];
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
+        for (int i = 0; i < MB; ++i)
         {
-            const int r = wm * 64 + mb * 16 + col;
-            A[mb] = *reinterpret_cast<const half8_t*>(as + (size_t)r * 64 + ((g ^ ((r >> 2) & 3)) * 16));
-        }
+            const half8_t A = *reinterpret_cast<const half8_t*>(as + aoff[i]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            B[i] = *reinterpret_cast<const half8_t*>(bs + ((size_t)(wn * 4 + i) * 64 + lane) * 16);
-#pragma unroll
-        for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[mb][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[mb], B[i], acc[mb][i], 0, 0, 0);
-    };
-
-    // ---- main loop over 32-row steps. Loads run ahead: inputs of step s + FT_PA - 1 and trellis of step
-    // s + FT_PT are issued in iteration s, into the ring slots that iteration s - 1 finished with. Iteration s
-    // waits for its own loads (vmcnt counts in issue order), meets the other waves at the one barrier, multiplies
-    // step s and decodes step s + 1 into the other B buffer.
-    const int S = a.K / 32;
-    if (wave < 4)
-    {
-        for (int s = 0; s < FT_PT && s < S; ++s) load_trellis(s);
-        if (S >= FT_PT) wait_vmcnt<FT_PT - 1>(); else wait_vmcnt<0>();     // step 0 arrived
-    }
-    else
-        for (int s = 0; s < FT_PA - 1 && s < S; ++s) load_inputs(s);
-    __syncthreads();
-    decode(0);
-    for (int s = 0; s < S; ++s)
-    {
-        if (wave < 4)
-        {
-            if (s + FT_PT - 1 < S) wait_vmcnt<FT_PT - 2>(); else wait_vmcnt<0>();    // trellis of step s + 1
-        }
-        else
-        {
-            if (s + 2 < S) wait_vmcnt<(FT_PA - 2) * LA>();                           // inputs of step s
-            else if (s + 1 < S) wait_vmcnt<LA>();
-            else wait_vmcnt<0>();
-        }
-        __syncthreads();
-        if (wave < 4)
-        {
-            if (s + FT_PT < S) load_trellis(s + FT_PT);
-        }
-        else if (s + FT_PA - 1 < S)
-            load_inputs(s + FT_PA - 1);
-        mfma(s);
-        if (s + 1 < S) decode(s + 1);
-    }
-    __syncthreads();
-
-    // ---- epilogue through an fp16 tile in LDS (the output transforms round y to fp16 first)
-    uint8_t* C = smem;
-#pragma unroll
-    for (int mb = 0; mb < 4; ++mb)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[i][j], 0, 0, 0);
+            if (i % (MB / 4) == MB / 4 - 1)
             {
-                const int r = wm * 64 + mb * 16 + 4 * g + v, cc = (wn * 4 + i) * 16 + col;
-                *reinterpret_cast<uint16_t*>(C + (size_t)r * C_STRIDE + cc * 2) = f2h(acc[mb][i][v]);
+                const int u = i / (MB / 4);
+                *reinterpret_cast<half4_t*>(bd + u * 1024) = decode4<true>(th[u], tl[u], sh);
             }
+        }
+    }
+    wait_vmcnt<0>();
+    lds_barrier();
+
+    // ---- epilogue through a transposed fp16 C tile in LDS (column c at c * CS halves; the output transforms
+    // round y to fp16 first), four rows per wave at a time
+    uint16_t* C = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+    for (int i = 0; i < MB; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            const int c = (wn * 4 + j) * 16 + col, r = wm * (BM / 2) + 16 * i + 4 * g;
+            uint32_t* d = reinterpret_cast<uint32_t*>(C + (size_t)c * CS + r);
+            d[0] = (uint32_t)f2h(acc[i][j][0]) | ((uint32_t)f2h(acc[i][j][1]) << 16);
+            d[1] = (uint32_t)f2h(acc[i][j][2]) | ((uint32_t)f2h(acc[i][j][3]) << 16);
+        }
     __syncthreads();
-    for (int r = wave; r < rows; r += FT_WAVES)
+    // value of column c for rows r0 + 2 h, r0 + 2 h + 1 (h = 0, 1)
+    auto pair = [&](int c, int r0, int h, float& v0, float& v1) {
+        const uint32_t d = *reinterpret_cast<const uint32_t*>(C + (size_t)c * CS + r0 + 2 * h);
+        v0 = h2f((uint16_t)(d & 0xffffu));
+        v1 = h2f((uint16_t)(d >> 16));
+    };
+    for (int r0 = 4 * wave; r0 < rows; r0 += 4 * FT_WAVES)
     {
-        const uint16_t* cr = reinterpret_cast<const uint16_t*>(C + (size_t)r * C_STRIDE);
-        const int pos = pos0 + r;
         if constexpr (MODE == 0)
         {
             const int c0 = nu * 128;
-            float ga = h2f(cr[lane]), gb = h2f(cr[lane + 64]);
-            float ua = h2f(cr[128 + lane]), ub = h2f(cr[128 + lane + 64]);
+            float ga[4], gb[4], ua[4], ub[4];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+            {
+                pair(lane, r0, h, ga[2 * h], ga[2 * h + 1]);
+                pair(lane + 64, r0, h, gb[2 * h], gb[2 * h + 1]);
+                pair(128 + lane, r0, h, ua[2 * h], ua[2 * h + 1]);
+                pair(128 + lane + 64, r0, h, ub[2 * h], ub[2 * h + 1]);
+            }
             const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c0;
             const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c0;
-            out_block_wave(ga, gb, h2f(svg[lane]), h2f(svg[lane + 64]));
-            out_block_wave(ua, ub, h2f(svu[lane]), h2f(svu[lane + 64]));
-            float xa = r16(act_gu(ga, ua, a.limit));
-            float xb = r16(act_gu(gb, ub, a.limit));
             const uint16_t* sd = a.suh2 + (size_t)e * a.I + c0;
-            prep_block_wave(xa, xb, h2f(sd[lane]), h2f(sd[lane + 64]));
-            uint16_t* dst = a.xd + (size_t)pos * a.I;
-            dst[operand_index(c0 + lane)] = f2h(xa);
-            dst[operand_index(c0 + lane + 64)] = f2h(xb);
+            const float sga = h2f(svg[lane]), sgb = h2f(svg[lane + 64]);
+            const float sua = h2f(svu[lane]), sub = h2f(svu[lane + 64]);
+            const float sda = h2f(sd[lane]), sdb = h2f(sd[lane + 64]);
+            float xa[4], xb[4];
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+            {
+                out_block_wave(ga[v], gb[v], sga, sgb);
+                out_block_wave(ua[v], ub[v], sua, sub);
+                xa[v] = r16(act_gu(ga[v], ua[v], a.limit));
+                xb[v] = r16(act_gu(gb[v], ub[v], a.limit));
+                prep_block_wave(xa[v], xb[v], sda, sdb);
+            }
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (r0 + v < rows)
+                {
+                    uint16_t* dst = a.xd + (size_t)(pos0 + r0 + v) * a.I;
+                    dst[operand_index(c0 + lane)] = f2h(xa[v]);
+                    dst[operand_index(c0 + lane + 64)] = f2h(xb[v]);
+                }
         }
         else
         {
-            float* yr = a.Y + (size_t)a.route_at[pos] * a.H;
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb)
             {
                 const int c0 = (2 * nu + hb) * 128;
-                float ya = h2f(cr[hb * 128 + lane]), yb = h2f(cr[hb * 128 + lane + 64]);
+                float ya[4], yb[4];
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                {
+                    pair(hb * 128 + lane, r0, h, ya[2 * h], ya[2 * h + 1]);
+                    pair(hb * 128 + lane + 64, r0, h, yb[2 * h], yb[2 * h + 1]);
+                }
                 const uint16_t* sv = a.svh2 + (size_t)e * a.H + c0;
-                out_block_wave(ya, yb, h2f(sv[lane]), h2f(sv[lane + 64]));
-                yr[c0 + lane] = ya;
-                yr[c0 + lane + 64] = yb;
+                const float sva = h2f(sv[lane]), svb = h2f(sv[lane + 64]);
+#pragma unroll
+                for (int v = 0; v < 4; ++v) out_block_wave(ya[v], yb[v], sva, svb);
+#pragma unroll
+                for (int v = 0; v < 4; ++v)
+                    if (r0 + v < rows)
+                    {
+                        float* yr = a.Y + (size_t)a.route_at[pos0 + r0 + v] * a.H;
+                        yr[c0 + lane] = ya[v];
+                        yr[c0 + lane + 64] = yb[v];
+                    }
             }
         }
     }
@@ -322,13 +455,9 @@ struct FatWs
     void* pws;            // permutation workspace
     size_t pws_bytes;
     ExpertRec* rec;       // [min(n, E)]
-    int32_t* pcounts;     // [2]  route prep
-    int32_t* pos_of;      // [n]
-    int32_t* route_at;    // [n]
-    int32_t* e_at;        // [n]
+    int32_t* off_big;     // [min(n, E) + 1]
+    int32_t* off_small;   // [min(n, E) + 1]
     uint16_t* xa;         // [n][2][H]
-    float* xsum;          // [n][2][nb]
-    int32_t* tile_off;    // [min(n, E) + 1]
     uint16_t* xd;         // [n][I]
     float* Y;             // [n][H]
     size_t bytes;
@@ -339,23 +468,23 @@ static FatWs fat_carve(void* base, int n, int E, int H, int I)
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t na = (size_t)(n < E ? n : E);
     const size_t pwsb = mm_permute_workspace(n, E);
-    const size_t sizes[17] = { al((size_t)(E + 1) * 4), al((size_t)(E + 2) * 4), al((size_t)n * 4), al((size_t)E * 4), al(4),
-                               al(pwsb), al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al((size_t)n * 4),
-                               al((size_t)n * 4), al((size_t)n * 2 * H * 2), al((size_t)n * 2 * prep_blocks(H) * 4),
-                               al((na + 1) * 4), al((size_t)n * I * 2), al((size_t)n * H * 4), 0 };
+    constexpr int NS = 12;
+    const size_t sizes[NS] = { al((size_t)(E + 1) * 4), al((size_t)(E + 2) * 4), al((size_t)n * 4), al((size_t)E * 4),
+                               al(4), al(pwsb), al(na * sizeof(ExpertRec)), al((na + 1) * 4), al((na + 1) * 4),
+                               al((size_t)n * 2 * H * 2), al((size_t)n * I * 2), al((size_t)n * H * 4) };
     char* p = static_cast<char*>(base);
-    char* at[17];
+    char* at[NS];
     size_t off = 0;
-    for (int i = 0; i < 17; ++i)
+    for (int i = 0; i < NS; ++i)
     {
         at[i] = p ? p + off : nullptr;
         off += sizes[i];
     }
     FatWs w;
     w.counts = (int32_t*)at[0]; w.offsets = (int32_t*)at[1]; w.order = (int32_t*)at[2]; w.active = (int32_t*)at[3];
-    w.nactive = (int32_t*)at[4]; w.pws = at[5]; w.pws_bytes = pwsb; w.rec = (ExpertRec*)at[6]; w.pcounts = (int32_t*)at[7];
-    w.pos_of = (int32_t*)at[8]; w.route_at = (int32_t*)at[9]; w.e_at = (int32_t*)at[10]; w.xa = (uint16_t*)at[11];
-    w.xsum = (float*)at[12]; w.tile_off = (int32_t*)at[13]; w.xd = (uint16_t*)at[14]; w.Y = (float*)at[15];
+    w.nactive = (int32_t*)at[4]; w.pws = at[5]; w.pws_bytes = pwsb; w.rec = (ExpertRec*)at[6];
+    w.off_big = (int32_t*)at[7]; w.off_small = (int32_t*)at[8]; w.xa = (uint16_t*)at[9]; w.xd = (uint16_t*)at[10];
+    w.Y = (float*)at[11];
     w.bytes = off;
     return w;
 }
@@ -368,6 +497,7 @@ static int fat_check(const mm_layer_t* L, const void* x, int x_dtype, int T, int
     MM_CHECK_ARG(L->E > 0 && L->E <= FT_PLAN_MAX && L->H % 256 == 0 && L->I % 128 == 0 && L->H > 0 && L->I > 0,
                  "%s: need 0 < E <= %d, H a multiple of 256 and I of 128", who, FT_PLAN_MAX);
     MM_CHECK_ARG((size_t)(L->H / 16) * (L->I / 16) * 96 < ((size_t)1 << 31), "%s: matrix larger than 2 GiB", who);
+    MM_CHECK_ARG((size_t)FT_BIG * 2 * L->H * 2 < ((size_t)1 << 30), "%s: H too large", who);
     MM_CHECK_ARG(x && ids, "%s: null pointer", who);
     MM_CHECK_ARG(x_dtype == MM_DTYPE_F16 || x_dtype == MM_DTYPE_BF16 || x_dtype == MM_DTYPE_F32,
                  "%s: x_dtype must be MM_DTYPE_F16, MM_DTYPE_BF16 or MM_DTYPE_F32", who);
@@ -377,7 +507,7 @@ static int fat_check(const mm_layer_t* L, const void* x, int x_dtype, int T, int
     return MM_OK;
 }
 
-// Permutation, route prep, plan and both GEMMs: Y rows of every route whose expert has more than cap routes.
+// Permutation, input prep, plan and both GEMMs: Y rows of every route whose expert has more than cap routes.
 static int fat_run(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids, int cap,
                    const FatWs& ws, hipStream_t s)
 {
@@ -385,20 +515,25 @@ static int fat_run(const mm_layer_t* L, const void* x, int x_dtype, int T, int t
     int rc = mm_permute(ids, nullptr, n, topk, E, ws.counts, ws.offsets, ws.order, nullptr, nullptr, nullptr, ws.active,
                         ws.nactive, ws.pws, ws.pws_bytes, s);
     if (rc) return rc;
-    PrepArgs p{ x, ids, ws.offsets, ws.order, ws.active, ws.nactive, L->gate_ptr, L->up_ptr, L->down_ptr, L->suh13,
-                ws.rec, ws.pcounts, ws.pos_of, ws.route_at, ws.e_at, ws.xa, ws.xsum, n, topk, E, L->H, prep_blocks(L->H),
-                x_dtype, 0 };
-    launch_route_prep(p, s);
-    hipLaunchKernelGGL(k_fat_plan, dim3(1), dim3(FT_PLAN_MAX), 0, s, ws.rec, ws.pcounts, ws.tile_off, na, cap);
-    // tiles: at most one partial tile per active expert beyond the full ones
-    const int tiles_max = (n + FT_BM - 1) / FT_BM + na;
-    FatArgs g{ ws.rec, ws.pcounts, ws.tile_off, ws.xa, L->svh13, L->suh2, L->svh2, ws.route_at, ws.xd, ws.Y,
+    hipLaunchKernelGGL(k_fat_prep, dim3(n), dim3(256), 0, s, x, x_dtype, ids, ws.counts, ws.offsets, ws.order, L->suh13,
+                       ws.xa, topk, E, L->H, cap);
+    hipLaunchKernelGGL(k_fat_plan, dim3(1), dim3(FT_PLAN_MAX), 0, s, ws.counts, ws.offsets, ws.active, ws.nactive,
+                       L->gate_ptr, L->up_ptr, L->down_ptr, ws.rec, ws.off_big, ws.off_small, na, cap);
+    // a 256-route tile holds more than 128 routes: at most n / 129 of them; one 128-route tile per active expert
+    const int max_big = n / (FT_SMALL + 1), max_small = na;
+    auto grid = [](int tiles, int units) { return dim3((unsigned)(((size_t)tiles * units + 7) & ~(size_t)7)); };    // >= 8 per_xcd
+    FatArgs g{ ws.rec, ws.nactive, ws.off_big, ws.off_big, ws.xa, L->svh13, L->suh2, L->svh2, ws.order, ws.xd, ws.Y,
                L->H, L->I, L->H, L->I, L->I / 128, na, L->limit };
-    auto grid = [&](int units) { return dim3((unsigned)(((size_t)tiles_max * units + 7) & ~(size_t)7)); };
-    hipLaunchKernelGGL(k_fat<0>, grid(g.nunits), dim3(FT_THREADS), 0, s, g);
+    FatArgs gs = g;
+    gs.tile_off = ws.off_small;
+    if (max_big > 0) hipLaunchKernelGGL((k_fat<0, FT_BIG / 32>), grid(max_big, g.nunits), dim3(FT_THREADS), 0, s, g);
+    hipLaunchKernelGGL((k_fat<0, FT_SMALL / 32>), grid(max_small, g.nunits), dim3(FT_THREADS), 0, s, gs);
     FatArgs d = g;
     d.xa = ws.xd; d.K = L->I; d.N = L->H; d.nunits = L->H / 256;
-    hipLaunchKernelGGL(k_fat<1>, grid(d.nunits), dim3(FT_THREADS), 0, s, d);
+    FatArgs ds = d;
+    ds.tile_off = ws.off_small;
+    if (max_big > 0) hipLaunchKernelGGL((k_fat<1, FT_BIG / 32>), grid(max_big, d.nunits), dim3(FT_THREADS), 0, s, d);
+    hipLaunchKernelGGL((k_fat<1, FT_SMALL / 32>), grid(max_small, d.nunits), dim3(FT_THREADS), 0, s, ds);
     return check_launch("fat path");
 }
 
