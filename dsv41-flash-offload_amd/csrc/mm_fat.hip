@@ -38,7 +38,7 @@ struct FatArgs
     const int32_t* nactive;       // [1]
     const int32_t* tile_off;      // [max_active + 1] first tile of each active expert in this launch's list
     const int32_t* big_off;       // [max_active + 1] 224-route tiles (a 96-route tile follows them)
-    const uint16_t* xa;           // mode 0: [n][2][H]; mode 1: [n][I] (operand order)
+    const uint16_t* xa;           // mode 0: [n][H/32][gate 32, up 32]; mode 1: [n][I] (operand order)
     const uint16_t* svh13;        // [E][2][I]
     const uint16_t* suh2;         // [E][I]
     const uint16_t* svh2;         // [E][H]
@@ -50,8 +50,10 @@ struct FatArgs
 };
 
 // Transformed inputs of every fat route, one workgroup per sorted position (the expert's 2 x H/128 blocks, 4
-// waves): xa[pos][m] = r16(FWHT(x16 * suh_m) * HAD) per 128-block in operand order (ft_core.h:96-102), where
-// x16 is fp16 input as is, or bf16 / fp32 input rounded through bf16.
+// waves, each transforming 4 blocks at a time so their shuffles overlap): r16(FWHT(x16 * suh_m) * HAD) per
+// 128-block (ft_core.h:96-102), where x16 is fp16 input as is, or bf16 / fp32 input rounded through bf16. Row pos
+// of xa holds, per 32-element step, the gate step then the up step in operand order (128 bytes: one cache line
+// per step, which the gate/up kernel loads whole).
 __global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, const int64_t* ids, const int32_t* counts,
                                                   const int32_t* offsets, const int32_t* order, const uint16_t* suh13,
                                                   uint16_t* xa, int topk, int E, int H, int cap)
@@ -64,23 +66,38 @@ __global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, co
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const size_t row = (size_t)(s / topk) * H;
     const int nb = H / 128;
-#pragma unroll 4
-    for (int b = wave; b < 2 * nb; b += 4)
+    for (int b0 = wave * 4; b0 < 2 * nb; b0 += 16)
     {
-        const int m = b / nb, h0 = (b % nb) * 128;
-        float va = load_x(x, x_dtype, row + h0 + lane);
-        float vb = load_x(x, x_dtype, row + h0 + lane + 64);
-        const uint16_t* su = suh13 + ((size_t)e * 2 + m) * H + h0;
-        const float sa = h2f(su[lane]), sb = h2f(su[lane + 64]);
-        if (x_dtype != MM_DTYPE_F16)
+        float va[4], vb[4], sa[4], sb[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
         {
-            va = r16(bf16_value(va));
-            vb = r16(bf16_value(vb));
+            const int b = b0 + k, m = b / nb, h0 = (b % nb) * 128;
+            va[k] = load_x(x, x_dtype, row + h0 + lane);
+            vb[k] = load_x(x, x_dtype, row + h0 + lane + 64);
+            const uint16_t* su = suh13 + ((size_t)e * 2 + m) * H + h0;
+            sa[k] = h2f(su[lane]);
+            sb[k] = h2f(su[lane + 64]);
         }
-        prep_block_wave(va, vb, sa, sb);
-        uint16_t* dst = xa + ((size_t)pos * 2 + m) * H;
-        dst[operand_index(h0 + lane)] = f2h(va);
-        dst[operand_index(h0 + lane + 64)] = f2h(vb);
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            if (x_dtype != MM_DTYPE_F16)
+            {
+                va[k] = r16(bf16_value(va[k]));
+                vb[k] = r16(bf16_value(vb[k]));
+            }
+            prep_block_wave(va[k], vb[k], sa[k], sb[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+        {
+            const int b = b0 + k, m = b / nb, h0 = (b % nb) * 128;
+            uint16_t* dst = xa + (size_t)pos * 2 * H + m * 32;
+            const int ka = h0 + lane, kb = h0 + lane + 64;
+            dst[(ka >> 5) * 64 + (operand_index(ka) & 31)] = f2h(va[k]);
+            dst[(kb >> 5) * 64 + (operand_index(kb) & 31)] = f2h(vb[k]);
+        }
     }
 }
 
@@ -152,22 +169,29 @@ __global__ __launch_bounds__(FT_PLAN_MAX) void k_fat_plan(const int32_t* counts,
     }
 }
 
-// LDS position of 16-byte chunk g of row r of an input stage (64-byte rows): the 16 rows one MFMA operand read
-// covers fall in distinct 16-byte bank groups both for 8 lanes over 32 banks and for 16 lanes over 64 banks.
-__device__ __forceinline__ int chunk_pos(int g, int r) { return g ^ (((r >> 1) ^ (r >> 2)) & 3); }
+// LDS slot of 16-byte chunk q of row r of an input stage whose rows hold NA x 64 bytes (NA = 2: gate chunks 0 .. 3,
+// up chunks 4 .. 7): the 16 rows one MFMA operand read covers fall in distinct 16-byte bank groups both for 8
+// lanes over 32 banks and for 16 lanes over 64 banks.
+template <int NA>
+__device__ __forceinline__ int chunk_slot(int q, int r)
+{
+    if constexpr (NA == 2) return q ^ (((r >> 1) & 7) ^ ((r & 1) << 2));
+    else return q ^ (((r >> 1) ^ (r >> 2)) & 3);
+}
 
 // MB = 16-row blocks per row-wave: tiles of BM = 32 MB routes (256 or 128). 8 waves: wave (wm, wn) = (w >> 2,
-// w & 3) multiplies rows (BM / 2) wm .. + BM / 2 - 1 by column tiles 4 wn .. 4 wn + 3 of 16; waves 0 .. 3 also
-// load the trellis (chunk w: tile row w >> 1 of matrix / block w & 1) and waves 4 .. 7 the inputs, so each wave's
-// loads are of one kind and complete in issue order within their own lead; wave w decodes tiles 4 (w & 1) .. + 3
-// of chunk w >> 1. Rows past the tile's routes read zero inputs.
+// w & 3) multiplies rows (BM / 2) wm .. + BM / 2 - 1 by column tiles 4 wn .. 4 wn + 3 of 16; every wave loads an
+// eighth of the inputs and waves 0 .. 3 also the trellis (chunk w: tile row w >> 1 of matrix / block w & 1),
+// which runs further ahead; wave w decodes tiles 4 (w & 1) .. + 3 of chunk w >> 1. Rows past the tile's routes
+// read zero inputs.
 template <int MODE, int MB>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
 {
     constexpr int BM = 32 * MB;
     constexpr int NA = MODE == 0 ? 2 : 1;                        // input matrices (gate, up share the tile)
-    constexpr int A_STAGE = NA * BM * 64;                        // one step's inputs
-    constexpr int LA = A_STAGE / 1024 / 4;                       // input loads (1 KB each) per loader wave and step
+    constexpr int SEG = NA * 64;                                 // bytes of one route's step (gate, up)
+    constexpr int A_STAGE = BM * SEG;                            // one step's inputs
+    constexpr int LA = A_STAGE / 1024 / FT_WAVES;                // input loads (1 KB each) per wave and step
     constexpr int T_SLOT = 4 * 1024;                             // one step's trellis: 4 chunks of 8 tiles
     constexpr int B_BUF = 16 * 64 * 16;                          // decoded B of one step: 16 tiles x 64 lanes
     constexpr int A_BYTES = FT_PA * A_STAGE, T_BYTES = FT_TS * T_SLOT;
@@ -229,24 +253,19 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, Tring + (size_t)(s % FT_TS) * T_SLOT + (size_t)tq * 1024, 12,
                                                  tr * row_bytes + wcol + (uint32_t)lane * 12, 0, 0, 0);
     };
-    // input loader (waves 4 .. 7): LA loads of 16 rows each (4 lanes per 64-byte row step); chunk g of row r goes
-    // to chunk_pos(g, r). Rows past the tile's routes and steps past the end read out of range (zero, no access).
+    // inputs (every wave): LA loads of 1 KB = 1024 / SEG rows each (SEG / 16 lanes per row step); chunk q of row r
+    // goes to slot chunk_slot(q, r). Rows past the tile's routes and steps past the end read out of range (zero,
+    // no memory access).
     const uint32_t a_row = (uint32_t)NA * a.K * 2;                       // bytes per route of the inputs
     const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
         uniform_ptr(a.xa + (size_t)pos0 * NA * a.K), (short)0, (int)((uint32_t)rows * a_row), 0x00020000);
-    auto load_inputs = [&](int s) {
+    auto load_input = [&](int s, int u) {
         const int st = s % FT_PA;
-        const uint32_t ks = s < S ? (uint32_t)s * 64 : 0x40000000u;  // the range is below 2^30
-#pragma unroll
-        for (int u = 0; u < LA; ++u)
-        {
-            const int li = (wave - 4) * LA + u;                        // 0 .. NA BM / 16 - 1
-            const int am = li / (BM / 16), rb = li % (BM / 16);
-            const int r = rb * 16 + (lane >> 2), p = lane & 3;
-            const uint32_t voff = (uint32_t)r * a_row + (uint32_t)am * a.K * 2 + (uint32_t)chunk_pos(p, r) * 16 + ks;
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, Aring + (size_t)st * A_STAGE + ((size_t)am * BM + rb * 16) * 64,
-                                                     16, voff, 0, 0, 0);
-        }
+        const uint32_t ks = s < S ? (uint32_t)s * SEG : 0x40000000u; // the range is below 2^30
+        const int li = wave * LA + u;                                  // 0 .. A_STAGE / 1024 - 1
+        const int r = li * (1024 / SEG) + lane / (SEG / 16), slot = lane % (SEG / 16);
+        const uint32_t voff = (uint32_t)r * a_row + (uint32_t)chunk_slot<NA>(slot, r) * 16 + ks;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, Aring + (size_t)st * A_STAGE + (size_t)li * 1024, 16, voff, 0, 0, 0);
     };
 
     // ---- decode: wave w owns chunk w >> 1 (tile row t = w >> 2 of matrix / block b = (w >> 1) & 1), tiles
@@ -268,7 +287,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
     for (int i = 0; i < MB; ++i)
     {
         const int r = wm * (BM / 2) + 16 * i + col;
-        aoff[i] = ((MODE == 0 ? (wn >> 1) : 0) * BM + r) * 64 + chunk_pos(g, r) * 16;
+        aoff[i] = r * SEG + chunk_slot<NA>((MODE == 0 ? (wn >> 1) : 0) * 4 + g, r) * 16;
     }
     float4_t acc[MB][4];
 #pragma unroll
@@ -276,28 +295,35 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{ 0.f, 0.f, 0.f, 0.f };
 
-    // Trellis loaders issue steps 0 .. FT_PT - 1 ahead of the loop and step s + FT_PT in step s: at the top of
-    // step s at most FT_PT - 2 of their loads may be outstanding (step s + 1 is complete). Input loaders issue
-    // steps 0 .. FT_PA - 2 ahead and step s + FT_PA - 1 in step s: at most (FT_PA - 2) LA outstanding (step s is
-    // complete). One barrier per step then publishes the loads and the tiles decoded in step s - 1.
+    // Loads in issue order, per wave: inputs of step 0, [trellis of steps 0 .. FT_PT - 1], inputs of step 1, then
+    // in step s [the trellis of step s + FT_PT] and the inputs of step s + 2 (LA loads, in between the MFMAs);
+    // [..] = waves 0 .. 3 only. At the top of step s the inputs of step s (issued in step s - 2, or before the loop)
+    // are complete once at most LA (+ 1 trellis load for waves 0 .. 3) loads are outstanding: that is exactly what
+    // step s - 1 issued after them (step 0: more than that came after). The trellis of step s + 1 is older than
+    // the inputs of step s (FT_PT - 1 > 2 steps earlier, or before them in the prologue, with more than LA + 1 loads
+    // after it), so it is complete too. One barrier per step then publishes the loads and the tiles decoded in step
+    // s - 1.
+    static_assert(FT_PA == 3 && FT_PT >= 4, "issue order above");
+#pragma unroll
+    for (int u = 0; u < LA; ++u) load_input(0, u);
+    asm volatile("" ::: "memory");                                // keep the issue order
     if (tloader)
-    {
         for (int s = 0; s < FT_PT; ++s) load_trellis(s);
-        wait_vmcnt<FT_PT - 1>();                                  // step 0
-    }
-    else
-        for (int s = 0; s < FT_PA - 1; ++s) load_inputs(s);
+    asm volatile("" ::: "memory");
+#pragma unroll
+    for (int u = 0; u < LA; ++u) load_input(1, u);
+    if (tloader) wait_vmcnt<LA + FT_PT - 1>(); else wait_vmcnt<LA>();          // trellis of step 0
     lds_barrier();
 #pragma unroll
     for (int u = 0; u < 4; ++u)
         *reinterpret_cast<half4_t*>(bdst + u * 1024) = decode4<true>(tword[u * 32 + lhi], tword[u * 32 + llo], sh);
     for (int s = 0; s < S; ++s)
     {
-        if (tloader) wait_vmcnt<FT_PT - 2>(); else wait_vmcnt<(FT_PA - 2) * LA>();
+        if (tloader) wait_vmcnt<LA + 1>(); else wait_vmcnt<LA>();
         lds_barrier();
-        if (tloader) load_trellis(s + FT_PT); else load_inputs(s + FT_PA - 1);
-        // one step: the trellis words of step s + 1 and the B fragments of step s first, then per row block its 4
-        // MFMAs (operand read from LDS just before), one tile of step s + 1 decoded after every two blocks
+        if (tloader) load_trellis(s + FT_PT);
+        // one step: the trellis words of step s + 1 and the operands of step s first, then per row block its 4
+        // MFMAs, one tile of step s + 1 decoded after every MB / 4 blocks
         const uint32_t* tw = tword + (size_t)((s + 1) % FT_TS) * (T_SLOT / 4);
         uint32_t th[4], tl[4];
 #pragma unroll
@@ -309,20 +335,34 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
         const uint8_t* as = Aring + (size_t)(s % FT_PA) * A_STAGE;
         const uint8_t* bs = bsrc + (size_t)(s & 1) * B_BUF;
         uint8_t* bd = bdst + (size_t)((s + 1) & 1) * B_BUF;
-        half8_t B[4];
+        // every operand of the step is read before the step's LDS writes (input loads, decoded tiles): the
+        // compiler keeps LDS accesses that may alias in program order, so reads placed after a write would each
+        // wait a full LDS round trip
+        half8_t B[4], A[MB];
 #pragma unroll
         for (int j = 0; j < 4; ++j) B[j] = *reinterpret_cast<const half8_t*>(bs + j * 1024);
 #pragma unroll
+        for (int i = 0; i < MB; ++i) A[i] = *reinterpret_cast<const half8_t*>(as + aoff[i]);
+#pragma unroll
         for (int i = 0; i < MB; ++i)
         {
-            const half8_t A = *reinterpret_cast<const half8_t*>(as + aoff[i]);
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B[j], acc[i][j], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], acc[i][j], 0, 0, 0);
+            if (i % (MB / LA) == 0) load_input(s + FT_PA - 1, i / (MB / LA));
             if (i % (MB / 4) == MB / 4 - 1)
             {
                 const int u = i / (MB / 4);
                 *reinterpret_cast<half4_t*>(bd + u * 1024) = decode4<true>(th[u], tl[u], sh);
             }
+        }
+        // schedule: the LDS reads first, then one MFMA followed by two VALU instructions (the decode, which needs
+        // about that many per MFMA), so a wave keeps its MFMA pipe busy between its own decode instructions
+        __builtin_amdgcn_sched_group_barrier(0x0100, 4 + MB + 8, 0);
+#pragma unroll
+        for (int k = 0; k < 4 * MB; ++k)
+        {
+            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);
         }
     }
     wait_vmcnt<0>();
