@@ -83,6 +83,204 @@ def cpu_baseline(routes, T, H, I, E, layer_seed, budget_s=15.0):
             "mode": {0: "AFFINE", 1: "EXACT", 2: "I16"}.get(mode, str(mode)), "experts": len(experts)}
 
 
+def bench_prefill(store, E, H, I, reps, tokens=16384, k=8, cap=32):
+    """The 16k-token prefill layer: skewed routing (64 hot experts take 60 % of the assignments), every routed
+    expert above `cap` routes on the fat-expert grouped GEMM. Returns timings and MFMA utilisation."""
+    import numpy as np
+    import torch
+    from mi355moe import _lib, moe, workload
+    dev = torch.device("cuda", 0)
+    ids, w = workload.skewed_routing(tokens, k, E, seed=2000)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    fat = counts > cap
+    flops = float(2.0 * counts[fat].sum() * 3 * H * I)
+    x = torch.from_numpy(workload.activations(tokens, H, seed=7)).to(dev).to(torch.bfloat16)
+    idd, wd = torch.from_numpy(ids).to(dev), torch.from_numpy(w).to(dev)
+    n = tokens * k
+    ws, wsb = moe._prefill_ws(store, n, dev)
+    out = torch.empty((tokens, H), dtype=torch.float32, device=dev)
+    Y = torch.empty((n, H), dtype=torch.float32, device=dev)
+
+    def layer():
+        _lib.call("mm_moe_prefill", store.mm_layer(), x.data_ptr(), _lib.DTYPE_BF16, tokens, k, idd.data_ptr(),
+                  wd.data_ptr(), cap, 0, out.data_ptr(), ws.data_ptr(), wsb, _lib.stream_ptr())
+
+    def grouped():
+        _lib.call("mm_grouped_gemm", store.mm_layer(), x.data_ptr(), _lib.DTYPE_BF16, tokens, k, idd.data_ptr(), cap,
+                  Y.data_ptr(), ws.data_ptr(), wsb, _lib.stream_ptr())
+
+    def timed(fn):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+    t_layer = timed(layer)
+    t_grouped = timed(grouped)
+    peak = 2.5e15
+    return {"workload": f"prefill {tokens} tokens through one MoE layer, top-{k} skewed routing (64 hot experts take "
+                        f"60 %), experts above {cap} routes on the grouped GEMM, bf16 input",
+            "tokens": tokens, "fat_experts": int(fat.sum()), "fat_routes": int(counts[fat].sum()),
+            "fat_flops": flops, "ms_layer": round(t_layer, 4), "ms_grouped_gemm": round(t_grouped, 4),
+            "tok_s": round(tokens / (t_layer * 1e-3), 1),
+            "mfma_util_layer": round(flops / (t_layer * 1e-3) / peak, 4),
+            "mfma_util_grouped_gemm": round(flops / (t_grouped * 1e-3) / peak, 4),
+            "mfma_peak_tflops": peak / 1e12, "dtype": "fp16 MFMA, fp32 accumulation", "reps": reps}
+
+
+def bench_cache(args):
+    """Capacity-limited expert cache: 40 layers whose routed experts live in pinned host memory, a 709-slot HBM
+    cache (elastic, replanned every 16 decode steps), decode T=4 steps interleaved with 8,192-token prefill
+    chunks (one chunk every `--chunk-every` decode steps) whose host-resident experts stream through 8 staging
+    slots of 8 experts. Routing Zipf(1.1) per layer, the ranking reshuffled by 5 % every 64 steps."""
+    import numpy as np
+    import torch
+    from mi355moe import _lib, cache, ct_vllm, exl3, workload
+    from mi355moe.hostmem import HostBuffer
+    from mi355moe.store import ExpertStore
+
+    dev = torch.device("cuda", 0)
+    H, I, E, K, T, L = 4096, 2048, 384, 8, 4, args.layers
+    TP, NH = args.chunk_tokens, max(1, min(args.home_layers, L))
+    os.environ.update({"DSV41_CT_LAYERS": str(L), "DSV41_EC_SLOTS": str(args.slots), "DSV41_EC_EVERY": "16",
+                       "DSV41_EC_ADMIT": "48", "DSV41_EC_DECAY": "0.9", "DSV41_EC_HYST": "1.0",
+                       "DSV41_EC_WARMUP": str(args.ec_warmup), "DSV41_EC_ASYNC": "1",
+                       "DSV41_EC_PREFILL_TOKENS": "512", "DSV41_EC_REWARM_AFTER": "4", "DSV41_EC_ELASTIC": "1",
+                       "DSV41_EC_MARGIN_MB": "1500"})
+    exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS = 1, 8, 8, 513
+    exl3.FAT_EXPERT_THRESHOLD = 32
+    rows = cache.ExpertRows(H, I)
+    t0 = time.time()
+    bufs = [HostBuffer(E * rows.row_bytes) for _ in range(NH)]
+    log(f"cache: {NH} pinned host homes ({NH * E * rows.row_bytes / 1e9:.1f} GB) {time.time() - t0:.1f}s")
+    ct_vllm.reset()
+    ct_vllm.install(exl3)
+    method = exl3.Exl3MoEMethod()
+    stores, shared = [], []
+    for l in range(L):
+        st = ExpertStore(E, H, I, device=dev, limit=10.0, host_home=cache.HostHome(E, H, I, buffer=bufs[l % NH]))
+        st.synthesize(1000 + l, trellis=l < NH)
+        method.process_weights_after_loading(st)
+        stores.append(st)
+        shared.append(ExpertStore(1, H, I, device=dev, limit=10.0).synthesize(5000 + l))
+    torch.cuda.synchronize()
+    c = ct_vllm.EC["cache"]
+    assert c is not None and ct_vllm.S["started"]
+    log(f"cache: {L} layers registered {time.time() - t0:.1f}s")
+    # pinned -> HBM copy-engine peak (one 2 GB transfer)
+    nb = min(2 << 30, bufs[0].nbytes)
+    dst = torch.empty(nb, dtype=torch.uint8, device=dev)
+    cache.stage_copy([(dst.data_ptr(), bufs[0].ptr, nb)])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    cache.stage_copy([(dst.data_ptr(), bufs[0].ptr, nb)])
+    e1.record()
+    torch.cuda.synchronize()
+    h2d_peak = nb / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del dst
+    log(f"cache: pinned H2D copy peak {h2d_peak:.1f} GB/s")
+
+    rng = np.random.default_rng(2000)
+    perms = [np.random.default_rng(2000 + l).permutation(E) for l in range(L)]
+    prank = None
+    ones = torch.ones((T, 1), dtype=torch.float32, device=dev)
+    zeros = torch.zeros((T, 1), dtype=torch.long, device=dev)
+    xb = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
+    x16 = torch.empty((T, H), dtype=torch.float16, device=dev)
+    exl3._DMA_TIMING = []
+    c.timing = []
+
+    def run_layers(x, ids_w, tokens):
+        xbf = torch.empty((tokens, H), dtype=torch.bfloat16, device=dev)
+        xh = torch.empty((tokens, H), dtype=torch.float16, device=dev)
+        src = x
+        for l in range(L):
+            ids, w = ids_w(l)
+            out = exl3.apply_exl3_fused_moe(src, ids, w, stores[l], None, None, 10.0)
+            so = torch.zeros((tokens, 1), dtype=torch.long, device=dev)
+            out += exl3.apply_exl3_fused_moe(src, so, torch.ones((tokens, 1), device=dev), shared[l], None, None, 10.0)
+            _lib.call("mm_prepare_input", out.data_ptr(), tokens, H, 1, xbf.data_ptr(), xh.data_ptr(), _lib.stream_ptr())
+            src = xbf
+        return src
+
+    stats = {"decode_steps": 0, "decode_s": 0.0, "prefill_chunks": 0, "prefill_s": 0.0}
+    x0 = torch.from_numpy(workload.activations(T, H, seed=7)).to(dev).to(torch.bfloat16)
+    total_steps = args.cache_steps
+    step = 0
+    hit0 = None
+    t_all = time.perf_counter()
+    while step < total_steps:
+        if step % 64 == 0 and step:
+            perms = [workload.drift(p, rng) for p in perms]
+        if args.chunk_every and step % args.chunk_every == args.chunk_every // 2:
+            if prank is None:
+                prank = workload.zipf_ids(TP, K, E, np.random.default_rng(3000), np.arange(E))
+            ct_vllm.before_step(TP)
+            xp = torch.from_numpy(np.random.default_rng(step).normal(0, 1, (TP, H)).astype(np.float32)).to(dev).to(torch.bfloat16)
+            pr_ids = torch.from_numpy(prank[0]).to(dev)
+            pr_w = torch.from_numpy(prank[1]).to(dev)
+            perm_d = [torch.from_numpy(p).to(dev) for p in perms]
+            torch.cuda.synchronize()
+            ts = time.perf_counter()
+            run_layers(xp, lambda l: (perm_d[l][pr_ids], pr_w), TP)
+            torch.cuda.synchronize()
+            stats["prefill_s"] += time.perf_counter() - ts
+            stats["prefill_chunks"] += 1
+            ct_vllm.ec_step()
+            log(f"cache: prefill chunk at step {step}: {time.perf_counter() - ts:.2f}s {ct_vllm.ec_summary()}")
+        routes = [workload.zipf_ids(T, K, E, rng, perms[l]) for l in range(L)]
+        rd = [(torch.from_numpy(r[0]).to(dev), torch.from_numpy(r[1]).to(dev)) for r in routes]
+        ct_vllm.before_step(T)
+        torch.cuda.synchronize()
+        ts = time.perf_counter()
+        run_layers(x0, lambda l: rd[l], T)
+        ct_vllm.ec_step()
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - ts
+        if step >= args.cache_warmup:
+            stats["decode_s"] += dt
+            stats["decode_steps"] += 1
+            if hit0 is None:
+                hit0 = ct_vllm.S["stats"].tolist()
+        step += 1
+        if step % 32 == 0:
+            log(f"cache: step {step}/{total_steps} decode {dt * 1e3:.1f} ms {ct_vllm.summary()}")
+    total_s = time.perf_counter() - t_all
+    st = ct_vllm.S["stats"].tolist()
+    hits, misses = st[0] - hit0[0], st[1] - hit0[1]
+    copy_ms = sum(a.elapsed_time(b) for a, b, _ in exl3._DMA_TIMING) + sum(a.elapsed_time(b) for a, b, _ in c.timing)
+    copy_bytes = sum(n for _, _, n in exl3._DMA_TIMING) + sum(n for _, _, n in c.timing)
+    dec_tok_s = T * stats["decode_steps"] / max(stats["decode_s"], 1e-9)
+    pre_tok_s = TP * stats["prefill_chunks"] / max(stats["prefill_s"], 1e-9)
+    res = {
+        "metric": METRIC, "value": round(dec_tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": stats["decode_steps"],
+        "warmup": args.cache_warmup, "ms_per_step": round(stats["decode_s"] * 1e3 / max(1, stats["decode_steps"]), 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic: seeded EXL3 3-bpw trellis + fp16 scales, Zipf(1.1) routing with 5 % rank drift every 64 "
+                "steps, bf16 N(0,1) input",
+        "config": {"workload": f"capacity-limited expert cache: {L} MoE layers (H 4096, I 2048, 384 routed experts "
+                               f"top-8 in pinned host memory + 1 HBM shared expert), {args.slots}-slot HBM cache, "
+                               f"decode T={T} with one {TP}-token prefill chunk every {args.chunk_every} steps, "
+                               "8 staging slots x 8 experts",
+                   "layers": L, "slots": args.slots, "chunk_tokens": TP, "chunk_every": args.chunk_every,
+                   "distinct_host_homes": NH},
+        "hit_rate": round(hits / max(1, hits + misses), 4), "hits": hits, "misses": misses,
+        "h2d_gbs": round(copy_bytes / max(copy_ms * 1e-3, 1e-9) / 1e9, 2), "h2d_bytes": copy_bytes,
+        "h2d_peak_gbs": round(h2d_peak, 2),
+        "decode_tok_s": round(dec_tok_s, 3), "prefill_tok_s": round(pre_tok_s, 1),
+        "moe_tok_s": round((T * stats["decode_steps"] + TP * stats["prefill_chunks"]) /
+                           max(stats["decode_s"] + stats["prefill_s"], 1e-9), 2),
+        "prefill_chunks": stats["prefill_chunks"], "prefill_s": round(stats["prefill_s"], 3),
+        "ec": ct_vllm.ec_summary(), "wall_s": round(total_s, 1),
+    }
+    print(json.dumps(res), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -91,12 +289,26 @@ def main():
     ap.add_argument("--layers", type=int, default=40)
     ap.add_argument("--tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--prefill-reps", type=int, default=5)
+    ap.add_argument("--workload", choices=("decode", "cache"), default="decode",
+                    help="decode: the 40-layer HBM-resident decode step (+ the 16k prefill layer); cache: the "
+                         "capacity-limited expert cache")
+    ap.add_argument("--slots", type=int, default=709)
+    ap.add_argument("--cache-steps", type=int, default=160)
+    ap.add_argument("--chunk-every", type=int, default=64)
+    ap.add_argument("--chunk-tokens", type=int, default=8192)
+    ap.add_argument("--home-layers", type=int, default=4)
+    ap.add_argument("--ec-warmup", type=int, default=16)
+    ap.add_argument("--cache-warmup", type=int, default=48)
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: this build measures one MI355X (got --gpus {args.gpus}, WORLD_SIZE {world}); the multi-GPU "
               "expert-parallel design is documented but not built, so N > 1 is not run.", flush=True)
         sys.exit(2)
+    if args.workload == "cache":
+        return bench_cache(args)
 
     import numpy as np
     import torch
@@ -196,6 +408,47 @@ def main():
     log(f"gate/up kernel: {t_gu * 1e3:.1f} us avg, {gu_gbs:.0f} GB/s; down kernel: {t_d * 1e3:.1f} us avg, "
         f"{d_gbs:.0f} GB/s; step {step_gbs:.0f} GB/s")
 
+    # decode at T = 1 through the same 40 layers (its own routing, runners and graph)
+    r1 = [workload.zipf_routing(1, K_TOP, E, seed=2000 + l) for l in range(L)]
+    run1 = []
+    for l in range(L):
+        R = DecodeRunner(E, H, I, 1, K_TOP, device=dev)
+        R.set_routes(torch.from_numpy(r1[l][0]).to(dev), torch.from_numpy(r1[l][1]).to(dev))
+        run1.append(R)
+    x1 = torch.from_numpy(workload.activations(1, H, seed=7)).to(dev)
+    o1 = [torch.empty((1, H), dtype=torch.float32, device=dev) for _ in range(2)]
+
+    def step1():
+        src = x1
+        for l in range(L):
+            src = run1[l].layer(stores[l], x=src, out=o1[l % 2], rescale=True)
+        return src
+    with torch.cuda.stream(side):
+        step1()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g1 = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g1):
+        step1()
+    for _ in range(args.warmup):
+        g1.replay()
+    torch.cuda.synchronize()
+    ev0.record()
+    for _ in range(args.steps):
+        g1.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    ms1 = ev0.elapsed_time(ev1) / args.steps
+    bytes1 = float(sum((len(np.unique(r[0])) + 1) * BYTES_EXPERT for r in r1))
+    log(f"decode T=1: {ms1:.3f} ms per step, {bytes1 / (ms1 * 1e-3) / 1e9:.0f} GB/s")
+
+    prefill = None
+    if not args.no_prefill:
+        del g_gu, g_d, g1
+        log("prefill: 16384-token layer")
+        prefill = bench_prefill(stores[0], E, H, I, args.prefill_reps)
+        log(f"prefill: {prefill}")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline: reference CPU tier, one layer")
@@ -227,7 +480,11 @@ def main():
                      "frac_of_peak": round(step_gbs / HBM_PEAK_GBS, 4),
                      "down_kernel_gbs": round(d_gbs, 1), "down_avg_launch_us": round(float(t_d) * 1e3, 2)},
         "ms_per_step_wall": round(ms_wall, 4),
+        "decode_t1": {"ms_per_step": round(ms1, 4), "tok_s": round(1 / (ms1 * 1e-3), 2),
+                      "hbm_gbs": round(bytes1 / (ms1 * 1e-3) / 1e9, 1)},
     }
+    if prefill is not None:
+        res["prefill"] = prefill
     if cpu is not None:
         res["cpu_baseline"] = {"value": round(T / (L * cpu["p50_layer_ms"] * 1e-3), 3), "unit": "tok/s",
                                "cores": cpu["cores"], "kind": "reference",

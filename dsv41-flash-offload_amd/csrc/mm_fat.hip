@@ -18,6 +18,8 @@
 // decodes 4 tiles of the next step into the MFMA B layout (fp16 weights, rounded as the reconstruct does) in
 // between its v_mfma_f32_16x16x32_f16 over a (BM / 2) x 64 sub-tile (128 accumulators per lane), so one wave's
 // decode runs while the other wave of its SIMD multiplies. The weights are decoded once per tile.
+#include <algorithm>
+
 #include "mm_decode.h"
 
 namespace mm {
@@ -54,17 +56,10 @@ struct FatArgs
 // 128-block (ft_core.h:96-102), where x16 is fp16 input as is, or bf16 / fp32 input rounded through bf16. Row pos
 // of xa holds, per 32-element step, the gate step then the up step in operand order (128 bytes: one cache line
 // per step, which the gate/up kernel loads whole).
-__global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, const int64_t* ids, const int32_t* counts,
-                                                  const int32_t* offsets, const int32_t* order, const uint16_t* suh13,
-                                                  uint16_t* xa, int topk, int E, int H, int cap)
+__device__ __forceinline__ void fat_prep_row(const void* x, int x_dtype, size_t row, int e, int pos,
+                                             const uint16_t* suh13, uint16_t* xa, int H)
 {
-    const int pos = blockIdx.x;
-    if (pos >= offsets[E]) return;
-    const int s = order[pos];
-    const int e = (int)ids[s];
-    if (counts[e] <= cap) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const size_t row = (size_t)(s / topk) * H;
     const int nb = H / 128;
     for (int b0 = wave * 4; b0 < 2 * nb; b0 += 16)
     {
@@ -99,6 +94,40 @@ __global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, co
             dst[(kb >> 5) * 64 + (operand_index(kb) & 31)] = f2h(vb[k]);
         }
     }
+}
+
+__global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, const int64_t* ids, const int32_t* counts,
+                                                  const int32_t* offsets, const int32_t* order, const uint16_t* suh13,
+                                                  uint16_t* xa, int topk, int E, int H, int cap)
+{
+    const int pos = blockIdx.x;
+    if (pos >= offsets[E]) return;
+    const int s = order[pos];
+    const int e = (int)ids[s];
+    if (counts[e] <= cap) return;
+    fat_prep_row(x, x_dtype, (size_t)(s / topk) * H, e, pos, suh13, xa, H);
+}
+
+// Sorted-route form: position pos belongs to the expert e with offsets[e] <= pos < offsets[e + 1] (binary search
+// over the E + 1 offsets) and to token token_sorted[pos]; only positions of experts with counts[e] > 0 (the
+// selected fat experts) are transformed.
+__global__ __launch_bounds__(256) void k_fatb_prep(const void* x, int x_dtype, const int64_t* token_sorted,
+                                                   const int32_t* counts, const int32_t* offsets,
+                                                   const uint16_t* suh13, uint16_t* xa, int T, int E, int H)
+{
+    const int pos = blockIdx.x;
+    if (pos >= offsets[E]) return;
+    int lo = 0, hi = E;                 // largest e with offsets[e] <= pos
+    while (hi - lo > 1)
+    {
+        const int mid = (lo + hi) >> 1;
+        if (offsets[mid] <= pos) lo = mid; else hi = mid;
+    }
+    const int e = lo;
+    if (counts[e] <= 0 || pos >= offsets[e] + counts[e]) return;
+    const int64_t t = token_sorted[pos];
+    if (t < 0 || t >= T) return;
+    fat_prep_row(x, x_dtype, (size_t)t * H, e, pos, suh13, xa, H);
 }
 
 // Expert records and the tile lists of the experts with more than cap routes. An expert of c routes gets
@@ -483,6 +512,170 @@ __global__ __launch_bounds__(256) void k_fat_combine(float* __restrict__ out, co
     *reinterpret_cast<float4*>(out + (size_t)t * H + h) = acc;
 }
 
+// ------------------------------------------------------------------------------- sorted-route form
+// The reference's fat entry takes the routes already sorted by expert (token_sorted, weight_sorted and per-expert
+// counts, patches/vllm-exl3-host-dma.patch:182-201). Selection, token lists and the combine of that form:
+
+// One block: counts (effective) = counts_in[e] for experts with more than cap routes that are not skipped and whose
+// range lies within the n positions, else 0; offsets = exclusive sums of counts_in (clamped to n), offsets[E] =
+// the routed positions, offsets[E + 1] = n; active = the selected experts in ascending id, nactive their number.
+__global__ __launch_bounds__(FT_PLAN_MAX) void k_fatb_setup(const int32_t* counts_in, const uint8_t* skip, int E, int n,
+                                                           int cap, int32_t* counts, int32_t* offsets, int32_t* active,
+                                                           int32_t* nactive)
+{
+    __shared__ int s_w[2][FT_PLAN_MAX / 64];
+    const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
+    const int c = e < E ? max(counts_in[e], 0) : 0;
+    int ic = c;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1)
+    {
+        const int o = __shfl_up(ic, d, 64);
+        if (lane >= d) ic += o;
+    }
+    if (lane == 63) s_w[0][wave] = ic;
+    __syncthreads();
+    int base = 0, total = 0;
+    for (int w = 0; w < FT_PLAN_MAX / 64; ++w)
+    {
+        if (w < wave) base += s_w[0][w];
+        total += s_w[0][w];
+    }
+    const long long off = (long long)base + ic - c;
+    const bool sel = e < E && c > cap && !(skip && skip[e]) && off + c <= n;
+    int f = sel ? 1 : 0;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1)
+    {
+        const int o = __shfl_up(f, d, 64);
+        if (lane >= d) f += o;
+    }
+    if (lane == 63) s_w[1][wave] = f;
+    __syncthreads();
+    int fb = 0, nf = 0;
+    for (int w = 0; w < FT_PLAN_MAX / 64; ++w)
+    {
+        if (w < wave) fb += s_w[1][w];
+        nf += s_w[1][w];
+    }
+    if (e < E)
+    {
+        offsets[e] = (int)min(off, (long long)n);
+        counts[e] = sel ? c : 0;
+        if (sel) active[fb + f - 1] = e;
+    }
+    if (e == 0)
+    {
+        const int routed = min(total, n);
+        offsets[E] = routed;
+        offsets[E + 1] = n;
+        counts[E] = n - routed;
+        nactive[0] = nf;
+    }
+}
+
+__device__ __forceinline__ int fatb_expert(const int32_t* offsets, int E, int pos)
+{
+    int lo = 0, hi = E;
+    while (hi - lo > 1)
+    {
+        const int mid = (lo + hi) >> 1;
+        if (offsets[mid] <= pos) lo = mid; else hi = mid;
+    }
+    return lo;
+}
+
+__global__ __launch_bounds__(256) void k_fill_i32(int32_t* p, int n, int v)
+{
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = v;
+}
+
+// Per position of a selected expert: FILL = 0 counts the position's token (tcount[t]++) and writes order[pos] =
+// pos (the grouped GEMM's output row); FILL = 1 appends the position to its token's list (any order within a
+// token: the combine visits a list in ascending position).
+template <int FILL>
+__global__ __launch_bounds__(256) void k_fatb_tokens(const int64_t* token_sorted, const int32_t* counts,
+                                                     const int32_t* offsets, int32_t* order, int32_t* tcount,
+                                                     const int32_t* toff, int32_t* tpos, int T, int E, int n)
+{
+    for (int pos = blockIdx.x * blockDim.x + threadIdx.x; pos < n; pos += gridDim.x * blockDim.x)
+    {
+        if (FILL == 0) order[pos] = pos;
+        if (pos >= offsets[E]) continue;
+        const int e = fatb_expert(offsets, E, pos);
+        if (counts[e] <= 0 || pos >= offsets[e] + counts[e]) continue;
+        const int64_t t = token_sorted[pos];
+        if (t < 0 || t >= T) continue;
+        if (FILL == 0)
+            atomicAdd(&tcount[t], 1);
+        else
+            tpos[toff[t] + atomicAdd(&tcount[t], 1)] = pos;
+    }
+}
+
+// One block: toff[0 .. T] = exclusive sums of tcount[0 .. T-1] (each thread sums a contiguous chunk).
+__global__ __launch_bounds__(1024) void k_scan_i32(const int32_t* tcount, int32_t* toff, int T)
+{
+    __shared__ int s_w[16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int per = (T + 1023) / 1024, i0 = min(tid * per, T), i1 = min(i0 + per, T);
+    int sum = 0;
+    for (int i = i0; i < i1; ++i) sum += tcount[i];
+    int inc = sum;
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1)
+    {
+        const int o = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += o;
+    }
+    if (lane == 63) s_w[wave] = inc;
+    __syncthreads();
+    int base = 0, total = 0;
+    for (int w = 0; w < 16; ++w)
+    {
+        if (w < wave) base += s_w[w];
+        total += s_w[w];
+    }
+    int run = base + inc - sum;
+    for (int i = i0; i < i1; ++i)
+    {
+        toff[i] = run;
+        run += tcount[i];
+    }
+    if (tid == 0) toff[T] = total;
+}
+
+// out[t] += sum over the token's selected positions p, in ascending p, of fp32(weight_sorted[p]) * Y[p] (fp32 fma).
+__global__ __launch_bounds__(256) void k_fatb_combine(float* __restrict__ out, const float* __restrict__ Y,
+                                                      const uint16_t* __restrict__ wsorted, const int32_t* __restrict__ toff,
+                                                      const int32_t* __restrict__ tpos, int T, int H)
+{
+    const int t = blockIdx.y;
+    const int h = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+    if (t >= T || h >= H) return;
+    const int b = toff[t], m = toff[t + 1] - b;
+    if (m <= 0) return;
+    float4 acc = *reinterpret_cast<const float4*>(out + (size_t)t * H + h);
+    int prev = -1;
+    for (int i = 0; i < m; ++i)
+    {
+        int p = 0x7fffffff;
+        for (int j = 0; j < m; ++j)
+        {
+            const int q = tpos[b + j];
+            if (q > prev && q < p) p = q;
+        }
+        prev = p;
+        const float wj = h2f(wsorted[p]);
+        const float4 y = *reinterpret_cast<const float4*>(Y + (size_t)p * H + h);
+        acc.x = fmaf(wj, y.x, acc.x);
+        acc.y = fmaf(wj, y.y, acc.y);
+        acc.z = fmaf(wj, y.z, acc.z);
+        acc.w = fmaf(wj, y.w, acc.w);
+    }
+    *reinterpret_cast<float4*>(out + (size_t)t * H + h) = acc;
+}
+
 // ------------------------------------------------------------------------------------------------- host
 
 struct FatWs
@@ -547,16 +740,11 @@ static int fat_check(const mm_layer_t* L, const void* x, int x_dtype, int T, int
     return MM_OK;
 }
 
-// Permutation, input prep, plan and both GEMMs: Y rows of every route whose expert has more than cap routes.
-static int fat_run(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids, int cap,
-                   const FatWs& ws, hipStream_t s)
+// Plan and both GEMMs over the sorted positions in ws (counts, offsets, order, active, nactive filled): Y rows of
+// every position of an active expert with more than cap routes.
+static int fat_gemms(const mm_layer_t* L, int n, int cap, const FatWs& ws, hipStream_t s)
 {
-    const int n = T * topk, E = L->E, na = n < E ? n : E;
-    int rc = mm_permute(ids, nullptr, n, topk, E, ws.counts, ws.offsets, ws.order, nullptr, nullptr, nullptr, ws.active,
-                        ws.nactive, ws.pws, ws.pws_bytes, s);
-    if (rc) return rc;
-    hipLaunchKernelGGL(k_fat_prep, dim3(n), dim3(256), 0, s, x, x_dtype, ids, ws.counts, ws.offsets, ws.order, L->suh13,
-                       ws.xa, topk, E, L->H, cap);
+    const int E = L->E, na = n < E ? n : E;
     hipLaunchKernelGGL(k_fat_plan, dim3(1), dim3(FT_PLAN_MAX), 0, s, ws.counts, ws.offsets, ws.active, ws.nactive,
                        L->gate_ptr, L->up_ptr, L->down_ptr, ws.rec, ws.off_big, ws.off_small, na, cap);
     // a 256-route tile holds more than 128 routes: at most n / 129 of them; one 128-route tile per active expert
@@ -575,6 +763,43 @@ static int fat_run(const mm_layer_t* L, const void* x, int x_dtype, int T, int t
     if (max_big > 0) hipLaunchKernelGGL((k_fat<1, FT_BIG / 32>), grid(max_big, d.nunits), dim3(FT_THREADS), 0, s, d);
     hipLaunchKernelGGL((k_fat<1, FT_SMALL / 32>), grid(max_small, d.nunits), dim3(FT_THREADS), 0, s, ds);
     return check_launch("fat path");
+}
+
+// Permutation, input prep, plan and both GEMMs: Y rows of every route whose expert has more than cap routes.
+static int fat_run(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids, int cap,
+                   const FatWs& ws, hipStream_t s)
+{
+    const int n = T * topk, E = L->E;
+    int rc = mm_permute(ids, nullptr, n, topk, E, ws.counts, ws.offsets, ws.order, nullptr, nullptr, nullptr, ws.active,
+                        ws.nactive, ws.pws, ws.pws_bytes, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_fat_prep, dim3(n), dim3(256), 0, s, x, x_dtype, ids, ws.counts, ws.offsets, ws.order, L->suh13,
+                       ws.xa, topk, E, L->H, cap);
+    return fat_gemms(L, n, cap, ws, s);
+}
+
+// Workspace of the sorted-route form: the fat sections for n positions, then the token lists.
+struct FatbWs
+{
+    FatWs f;
+    int32_t* tcount;     // [T]
+    int32_t* toff;       // [T + 1]
+    int32_t* tpos;       // [n]
+    size_t bytes;
+};
+
+static FatbWs fatb_carve(void* base, int n, int T, int E, int H, int I)
+{
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    FatbWs w;
+    w.f = fat_carve(base, n, E, H, I);
+    char* p = base ? static_cast<char*>(base) + w.f.bytes : nullptr;
+    const size_t s0 = al((size_t)T * 4), s1 = al((size_t)(T + 1) * 4), s2 = al((size_t)n * 4);
+    w.tcount = (int32_t*)p;
+    w.toff = p ? (int32_t*)(p + s0) : nullptr;
+    w.tpos = p ? (int32_t*)(p + s0 + s1) : nullptr;
+    w.bytes = w.f.bytes + s0 + s1 + s2;
+    return w;
 }
 
 }  // namespace mm
@@ -615,6 +840,50 @@ int mm_moe_prefill(const mm_layer_t* L, const void* x, int x_dtype, int T, int t
     hipLaunchKernelGGL(k_fat_combine, grid, dim3(256), 0, s, out, ws.Y, ids, w, ws.counts, T, topk, L->H, L->E, cap,
                        accumulate);
     return check_launch("mm_moe_prefill");
+}
+
+size_t mm_fat_batched_workspace(int n, int T, int E, int H, int I)
+{
+    if (n <= 0 || T <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
+    return fatb_carve(nullptr, n, T, E, H, I).bytes;
+}
+
+int mm_fat_batched(const mm_layer_t* L, const void* x, int x_dtype, int T, int n, const int64_t* token_sorted,
+                   const uint16_t* weight_sorted, const int32_t* counts, const uint8_t* skip, int cap, float* out,
+                   void* workspace, size_t workspace_bytes, mm_stream_t stream)
+{
+    MM_CHECK_ARG(n > 0, "mm_fat_batched: need n > 0 sorted positions");
+    MM_CHECK_ARG(L && L->gate_ptr && L->up_ptr && L->down_ptr && L->suh13 && L->svh13 && L->suh2 && L->svh2,
+                 "mm_fat_batched: incomplete layer");
+    MM_CHECK_ARG(L->E > 0 && L->E <= FT_PLAN_MAX && L->H % 256 == 0 && L->I % 128 == 0 && L->H > 0 && L->I > 0,
+                 "mm_fat_batched: need 0 < E <= %d, H a multiple of 256 and I of 128", FT_PLAN_MAX);
+    MM_CHECK_ARG((size_t)(L->H / 16) * (L->I / 16) * 96 < ((size_t)1 << 31), "mm_fat_batched: matrix larger than 2 GiB");
+    MM_CHECK_ARG(x_dtype == MM_DTYPE_F16 || x_dtype == MM_DTYPE_BF16 || x_dtype == MM_DTYPE_F32,
+                 "mm_fat_batched: x_dtype must be MM_DTYPE_F16, MM_DTYPE_BF16 or MM_DTYPE_F32");
+    MM_CHECK_ARG(x && token_sorted && weight_sorted && counts && out && cap >= 0, "mm_fat_batched: null pointer or negative cap");
+    MM_CHECK_ARG(T > 0 && n < (1 << 30) && T < (1 << 30), "mm_fat_batched: bad T/n");
+    const FatbWs ws = fatb_carve(workspace, n, T, L->E, L->H, L->I);
+    MM_CHECK_ARG(workspace && workspace_bytes >= ws.bytes, "mm_fat_batched: workspace too small (%zu < %zu)",
+                 workspace_bytes, ws.bytes);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const int E = L->E;
+    const unsigned pg = (unsigned)std::min((n + 255) / 256, 4096);
+    hipLaunchKernelGGL(k_fatb_setup, dim3(1), dim3(FT_PLAN_MAX), 0, s, counts, skip, E, n, cap, ws.f.counts,
+                       ws.f.offsets, ws.f.active, ws.f.nactive);
+    hipLaunchKernelGGL(k_fill_i32, dim3((unsigned)std::min((T + 255) / 256, 1024)), dim3(256), 0, s, ws.tcount, T, 0);
+    hipLaunchKernelGGL(k_fatb_tokens<0>, dim3(pg), dim3(256), 0, s, token_sorted, ws.f.counts, ws.f.offsets, ws.f.order,
+                       ws.tcount, ws.toff, ws.tpos, T, E, n);
+    hipLaunchKernelGGL(k_scan_i32, dim3(1), dim3(1024), 0, s, ws.tcount, ws.toff, T);
+    hipLaunchKernelGGL(k_fill_i32, dim3((unsigned)std::min((T + 255) / 256, 1024)), dim3(256), 0, s, ws.tcount, T, 0);
+    hipLaunchKernelGGL(k_fatb_tokens<1>, dim3(pg), dim3(256), 0, s, token_sorted, ws.f.counts, ws.f.offsets, ws.f.order,
+                       ws.tcount, ws.toff, ws.tpos, T, E, n);
+    hipLaunchKernelGGL(k_fatb_prep, dim3(n), dim3(256), 0, s, x, x_dtype, token_sorted, ws.f.counts, ws.f.offsets,
+                       L->suh13, ws.f.xa, T, E, L->H);
+    int r = fat_gemms(L, n, cap, ws.f, s);
+    if (r) return r;
+    const dim3 grid((unsigned)((L->H / 4 + 255) / 256), (unsigned)T);
+    hipLaunchKernelGGL(k_fatb_combine, grid, dim3(256), 0, s, out, ws.f.Y, weight_sorted, ws.toff, ws.tpos, T, L->H);
+    return check_launch("mm_fat_batched");
 }
 
 }  // extern "C"

@@ -48,6 +48,10 @@ _SIGS = {
     "mm_prefill_workspace": (sz, [i32, i32, i32, i32]),
     "mm_grouped_gemm": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, i32, vp, vp, sz, vp]),
     "mm_moe_prefill": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, i32, i32, vp, vp, sz, vp]),
+    "mm_fat_batched_workspace": (sz, [i32, i32, i32, i32, i32]),
+    "mm_fat_batched": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, vp, vp, i32, vp, vp, sz, vp]),
+    "mm_slot_point": (i32, [vp, vp, vp, vp, i32, vp, i32, vp]),
+    "mm_stage_copy": (i32, [vp, vp, vp, i32, vp]),
     "mm_synth_u16": (i32, [vp, u64, u64, u64, vp]),
     "mm_synth_layer": (i32, [ctypes.POINTER(MMLayer), u64, vp]),
     "mm_expert_seed": (u64, [u64, u64]),
@@ -85,6 +89,14 @@ def check(rc, what=""):
 
 def call(name, *args):
     return check(getattr(load(), name)(*args), name)
+
+
+def call_count(name, *args):
+    """Entry points that return a count (>= 0) or a negative error."""
+    rc = getattr(load(), name)(*args)
+    if rc < 0:
+        check(rc, name)
+    return rc
 
 
 def ptr(t):

@@ -1,0 +1,197 @@
+"""The reference's expert-tier hook surface (ct/ct_vllm.py) over this library.
+
+  install(X)                  wraps X.apply_exl3_fused_moe with the split/combine entry and
+                              X.Exl3MoEMethod.process_weights_after_loading with register (ct_vllm.py:446-456)
+  register(layer)             a layer with host-resident experts joins the tier: its slot table (_ct) is set up
+                              (ct_vllm.py:89-117)
+  _fused(x2d, ids, weights, layer, inners, expert_map, limit)
+                              decode-sized calls: mm_split classifies the picks against the slot table (hits /
+                              misses per distinct expert, routed counts for the cache), the fused MoE runs, and
+                              mm_combine_host adds a host partial when one was published (ct_vllm.py:175-223)
+  _ec_point, ec_step, ec_release, ec_rewarm, ec_summary, summary
+                              the slot table and the elastic expert cache (ct_vllm.py:236-443), on
+                              cache.ExpertCache
+  before_step(ntok)           the engine-step hook's part before a step (ct_vllm.py:459-475): release the cache
+                              before prefill-sized steps; the hook calls ec_step after every step
+
+No host worker computes misses here: the split's policy sends no picks to the host (force_n = 0), so every
+routed expert runs on the GPU from its cache slot or, zero-copy, from its pinned host home.
+"""
+import json
+import os
+
+import torch
+
+from . import _lib, cache, exl3
+from .hostmem import HostBuffer
+
+S = {"layers": [], "started": False, "init": False}
+EC = {"cache": None}
+_ORIG = {}
+
+
+def _f(k, d):
+    return float(os.environ.get(k, d))
+
+
+def _init(layer):
+    dev = layer._exl3_ptrs["gate_trellis"].device
+    H = layer.H
+    maxbsz = int(os.environ.get("DSV41_CT_MAXBSZ", "32"))
+    S.update(H=H, I=layer.I, dev=dev, maxbsz=maxbsz, maxpicks=8 * maxbsz)
+    # host mailbox: ctrl int64 [16] | hx fp16 [maxbsz * H] | picks int32 [maxpicks * 3] (ct_vllm.py:62-65)
+    S["mail"] = HostBuffer(128 + maxbsz * H * 2 + S["maxpicks"] * 12)
+    S["ctrl"] = S["mail"].data_ptr(0)
+    S["hx"] = S["mail"].data_ptr(128)
+    S["picks"] = S["mail"].data_ptr(128 + maxbsz * H * 2)
+    S["hout"] = torch.zeros(maxbsz * H, dtype=torch.float32, device=dev)
+    S["dflag"] = torch.zeros(1, dtype=torch.int64, device=dev)
+    S["seqc"] = torch.zeros(1, dtype=torch.int64, device=dev)
+    S["stats"] = torch.zeros(8, dtype=torch.int64, device=dev)
+    # cost-model policy (ct_vllm.py:69-71), with no host worker: force_n = 0 sends nothing to the host
+    S["pol"] = torch.tensor([_f("DSV41_CT_TZC", 0.58), _f("DSV41_CT_THIT", 0.03), _f("DSV41_CT_A", 0.11),
+                             _f("DSV41_CT_B", 0.16), _f("DSV41_CT_TOK", 0.2), _f("DSV41_CT_MAXN", 64), 0.0, 0.0, 0.0],
+                            dtype=torch.float32, device=dev)
+    S["timeout_ns"] = int(_f("DSV41_CT_TIMEOUT_S", 2) * 1e9)
+    S["sel"] = torch.empty(S["maxpicks"], dtype=torch.long, device=dev)
+    S["w"] = torch.empty(S["maxpicks"], dtype=torch.float32, device=dev)
+    S["nlayers"] = int(os.environ.get("DSV41_CT_LAYERS", "40"))
+    S["init"] = True
+
+
+def register(layer, nlayers=None):
+    """Join the tier (layers whose experts have a pinned host home). The tier starts once `nlayers` layers
+    (DSV41_CT_LAYERS, 40) are registered."""
+    if layer.host_home is None:
+        return
+    if not S["init"]:
+        _init(layer)
+    if nlayers is not None:
+        S["nlayers"] = int(nlayers)
+    li = len(S["layers"])
+    if li >= S["nlayers"]:
+        return
+    dev = S["dev"]
+    layer._ct = {"li": li, "E": layer.E, "slotof": layer.slotof,
+                 "score": torch.zeros(layer.E, dtype=torch.float32, device=dev), "counts": layer.counts,
+                 "home": layer.home}
+    S["layers"].append(layer)
+    if len(S["layers"]) == S["nlayers"]:
+        start()
+
+
+def start(**ec_args):
+    if S["started"]:
+        return
+    EC["cache"] = cache.ExpertCache(S["layers"], **ec_args)
+    S["started"] = True
+
+
+def _fused(x2d, ids, weights, layer, inners, expert_map, limit):
+    """Split / fused MoE / combine for decode-sized calls of tier layers; everything else goes to the plugin's
+    own entry unchanged (ct_vllm.py:214-223)."""
+    ct = getattr(layer, "_ct", None)
+    T = x2d.shape[0]
+    orig = _ORIG.get("fused", exl3.apply_exl3_fused_moe)
+    if ct is None or not S["started"] or T > S["maxbsz"] or expert_map is not None or ids.numel() > S["maxpicks"]:
+        return orig(x2d, ids, weights, layer, inners, expert_map, limit)
+    n = ids.numel()
+    so, wo = S["sel"][:n], S["w"][:n]
+    z = x2d if (x2d.dtype == torch.half and x2d.is_contiguous()) else x2d.half().contiguous()
+    idc = ids.contiguous().long()
+    wc = weights.contiguous().float()
+    _lib.call("mm_split", idc.data_ptr(), wc.data_ptr(), z.data_ptr(), n, T, S["H"], ct["E"], ct["slotof"].data_ptr(),
+              ct["score"].data_ptr(), S["pol"].data_ptr(), S["ctrl"], S["hx"], S["picks"], S["seqc"].data_ptr(),
+              ct["li"], so.data_ptr(), wo.data_ptr(), S["dflag"].data_ptr(), S["stats"].data_ptr(),
+              ct["counts"].data_ptr(), None, None, None, _lib.stream_ptr())
+    out = orig(x2d, so.view(ids.shape), wo.view(weights.shape).to(weights.dtype), layer, inners, expert_map, limit)
+    if out.dtype != torch.float32 or not out.is_contiguous():
+        raise RuntimeError("mi355moe ct_vllm: expected the fp32 contiguous routed accumulator")
+    _lib.call("mm_combine_host", out.data_ptr(), out.numel(), S["dflag"].data_ptr(), S["ctrl"], S["hout"].data_ptr(),
+              S["stats"].data_ptr(), S["timeout_ns"], _lib.stream_ptr())
+    return out
+
+
+# ------------------------------------------------------------------------------------------ slot table / cache
+
+def _ec_point(layer, items):
+    """items: [(e, gate_ptr, up_ptr, down_ptr, slot_or_-1)] -> stream-ordered pointer-table + slotof update."""
+    cache.point(layer, items)
+
+
+def ec_step():
+    c = EC["cache"]
+    if c is None or not S["started"]:
+        return
+    c.step()
+
+
+def ec_release():
+    c = EC["cache"]
+    if c is not None:
+        c.release()
+
+
+def ec_rewarm():
+    c = EC["cache"]
+    if c is not None:
+        c.rewarm()
+
+
+def ec_summary():
+    c = EC["cache"]
+    return c.summary() if c is not None else None
+
+
+def summary():
+    if not S["started"]:
+        return None
+    st = S["stats"].tolist()
+    calls = max(1, st[3])
+    return {"calls": st[3], "hits": st[0], "misses": st[1], "cpu_experts": st[2], "cpu_per_call": round(st[2] / calls, 3),
+            "gpu_wait_ms": round(st[4] / 1e6 / max(1, st[5]), 4), "timeouts": st[6],
+            "hit_rate": round(st[0] / max(1, st[0] + st[1]), 4), "ec": ec_summary()}
+
+
+def before_step(ntok):
+    """Before an engine step of `ntok` scheduled tokens: release the cache before prefill-sized steps (elastic
+    cache). ec_step() follows the step."""
+    c = EC["cache"]
+    if c is None:
+        return
+    c.last_ntok = int(ntok)
+    if ntok > c.prefill_tokens and c.elastic:
+        c.release()
+
+
+def install(X):
+    """Wrap the plugin module X (exl3 here, or any module with the same two names)."""
+    if _ORIG:
+        return
+    _ORIG["fused"] = X.apply_exl3_fused_moe
+    X.apply_exl3_fused_moe = _fused
+    orig_pwal = X.Exl3MoEMethod.process_weights_after_loading
+
+    def pwal(self, layer, _o=orig_pwal):
+        _o(self, layer)
+        register(layer)
+    X.Exl3MoEMethod.process_weights_after_loading = pwal
+    _ORIG["pwal"] = orig_pwal
+
+
+def uninstall(X):
+    if not _ORIG:
+        return
+    X.apply_exl3_fused_moe = _ORIG.pop("fused")
+    X.Exl3MoEMethod.process_weights_after_loading = _ORIG.pop("pwal")
+
+
+def reset():
+    """Forget every registered layer and the cache (tests, benchmarks)."""
+    S.clear()
+    S.update({"layers": [], "started": False, "init": False})
+    EC["cache"] = None
+
+
+def dumps():
+    return json.dumps(summary())

@@ -22,26 +22,47 @@ def trellis_words(K, N):
 
 
 class ExpertStore:
-    """All experts of one layer resident in device memory."""
+    """All experts of one layer: trellis in HBM (default), or in a pinned host home (`host_home`, a
+    cache.HostHome) that kernels read over PCIe unless the pointer tables name a cache or staging slot.
+    Scales always live in HBM.
 
-    def __init__(self, E, H, I, device="cuda", limit=10.0, exact=False):
+    Slot-table state (the reference's layer._ct, ct/ct_vllm.py:106-116): `slotof` int32 [E] (cache slot or -1;
+    HBM-resident experts are their own slot), `home` int64 [E, 3] (CPU) home addresses, `counts` int32 [E]
+    routed counts accumulated by the split for the expert cache."""
+
+    def __init__(self, E, H, I, device="cuda", limit=10.0, exact=False, host_home=None):
         if H % 128 or I % 128:
             raise ValueError(f"H and I must be multiples of 128 (H={H}, I={I})")
         self.E, self.H, self.I, self.limit = E, H, I, float(limit)
         self.exact = bool(exact)      # fp16-rounded weights (EXACT) instead of the AFFINE codebook evaluation
         dev = torch.device(device)
         it, ot = H // 16, I // 16
-        self.w13_trellis = torch.empty((E, 2, it, ot, KW), dtype=torch.int16, device=dev)
-        self.w2_trellis = torch.empty((E, ot, it, KW), dtype=torch.int16, device=dev)
+        self.host_home = host_home
+        if host_home is None:
+            self.w13_trellis = torch.empty((E, 2, it, ot, KW), dtype=torch.int16, device=dev)
+            self.w2_trellis = torch.empty((E, ot, it, KW), dtype=torch.int16, device=dev)
+        else:
+            if host_home.E != E or host_home.rows.H != H or host_home.rows.I != I:
+                raise ValueError("ExpertStore: host home shape differs from the layer")
+            self.w13_trellis = self.w2_trellis = None
         self.w13_suh = torch.empty((E, 2, H), dtype=torch.float16, device=dev)
         self.w13_svh = torch.empty((E, 2, I), dtype=torch.float16, device=dev)
         self.w2_suh = torch.empty((E, I), dtype=torch.float16, device=dev)
         self.w2_svh = torch.empty((E, H), dtype=torch.float16, device=dev)
-        self.home = self._home_pointers()
+        self.home = self._home_pointers() if host_home is None else host_home.pointers()
         self._exl3_ptrs = {k: self.home[:, j].to(dev).contiguous() for j, k in
                            enumerate(("gate_trellis", "up_trellis", "down_trellis"))}
-        self.slotof = torch.arange(E, dtype=torch.int32, device=dev)   # every expert HBM-resident
+        if host_home is None:
+            self.slotof = torch.arange(E, dtype=torch.int32, device=dev)   # every expert HBM-resident
+        else:
+            self.slotof = torch.full((E,), -1, dtype=torch.int32, device=dev)
+        self.counts = torch.zeros(E, dtype=torch.int32, device=dev)
         self._c = None
+
+    @property
+    def cold(self):
+        """Experts whose home is in host memory (the reference's _exl3_host13.cold)."""
+        return list(range(self.E)) if self.host_home is not None else []
 
     def _home_pointers(self):
         """int64 [E, 3] (CPU): addresses of each expert's gate / up / down trellis in this store."""
@@ -54,6 +75,15 @@ class ExpertStore:
         hp = np.stack([b13 + e * s13, b13 + e * s13 + sg, b2 + e * s2], axis=1)
         return torch.from_numpy(hp)
 
+    def with_tables(self, gate, up, down):
+        """A view of this layer whose kernels read the trellis through other pointer tables (int64 [E] device
+        tensors): the same scales, shape and flags."""
+        v = object.__new__(ExpertStore)
+        v.__dict__.update(self.__dict__)
+        v._exl3_ptrs = {"gate_trellis": gate, "up_trellis": up, "down_trellis": down}
+        v._c = None
+        return v
+
     def mm_layer(self):
         """The C ABI's mm_layer_t for this store (kept alive by the store)."""
         if self._c is None:
@@ -64,10 +94,12 @@ class ExpertStore:
         return self._c
 
     # ------------------------------------------------------------------------------------------ synthetic
-    def synthesize(self, layer_seed, stream=None):
+    def synthesize(self, layer_seed, stream=None, trellis=True):
         """Seeded synthetic weights: trellis words from the counter-based generator (per expert stream
-        mm_expert_seed(layer_seed, e)), suh = +-1 and svh = fp16(|N(0, 0.02)|) from numpy default_rng."""
-        _lib.call("mm_synth_layer", self.mm_layer(), int(layer_seed), _lib.stream_ptr(stream))
+        mm_expert_seed(layer_seed, e)), suh = +-1 and svh = fp16(|N(0, 0.02)|) from numpy default_rng.
+        trellis=False writes the scales only (a layer sharing another layer's host home)."""
+        if trellis:
+            _lib.call("mm_synth_layer", self.mm_layer(), int(layer_seed), _lib.stream_ptr(stream))
         sc = synth_scales(layer_seed, self.E, self.H, self.I)
         for name, arr in sc.items():
             getattr(self, name).copy_(torch.from_numpy(arr))

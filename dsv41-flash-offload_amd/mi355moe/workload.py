@@ -63,3 +63,27 @@ def skewed_routing(T, k, E, seed, hot=64, hot_share=0.6):
     logits = rng.normal(0.0, 1.0, (T, k))
     w = np.exp(logits - logits.max(1, keepdims=True))
     return ids.astype(np.int64), (w / w.sum(1, keepdims=True)).astype(np.float32)
+
+
+def zipf_ids(T, k, E, rng, perm, s=1.1):
+    """ids int64 [T, k]: k distinct experts per token, Zipf(s) over the expert ranking `perm` (perm[r] = expert of
+    rank r), drawn without replacement by the Gumbel top-k method (the same distribution as successive weighted
+    draws); weights fp32 [T, k] = softmax of N(0, 1) logits."""
+    logp = np.log(zipf_probs(E, s))
+    keys = logp[None, :] + rng.gumbel(size=(T, E))
+    ranks = np.argpartition(-keys, k - 1, axis=1)[:, :k]
+    ids = perm[ranks].astype(np.int64)
+    logits = rng.normal(0.0, 1.0, (T, k))
+    w = np.exp(logits - logits.max(1, keepdims=True))
+    return ids, (w / w.sum(1, keepdims=True)).astype(np.float32)
+
+
+def drift(perm, rng, frac=0.05):
+    """Reshuffle `frac` of the ranking: that share of rank positions, chosen at random, trade experts among
+    themselves."""
+    E = perm.size
+    m = max(2, int(round(frac * E)))
+    pos = rng.choice(E, m, replace=False)
+    out = perm.copy()
+    out[pos] = perm[rng.permutation(pos)]
+    return out

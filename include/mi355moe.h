@@ -177,6 +177,37 @@ int mm_moe_prefill(const mm_layer_t* layer, const void* x, int x_dtype, int T, i
 
 /* ----------------------------------------------------------------------------------------- utility */
 
+/* Fat-expert path on routes already sorted by expert, with the argument meaning of the reference's
+ * apply_exl3_batched_fat(xh, token_sorted, weight_sorted, counts_host, inners, limit, cap, out, use_kernel, skip)
+ * (patches/vllm-exl3-host-dma.patch:182-201): positions offsets[e] .. offsets[e] + counts[e] - 1 (offsets =
+ * exclusive sums of counts) are expert e's routes, position p belongs to token token_sorted[p] (int64 [n]) with
+ * weight weight_sorted[p] (fp16 bits [n]). For every expert with counts[e] > cap and skip[e] == 0 (skip uint8 [E]
+ * may be NULL), out[t] += sum over the expert's positions p of token t of w[p] * expert_e(x_t), added per token in
+ * ascending p (fp32 fma). counts int32 [E] in device memory; the layer's pointer tables give each expert's trellis
+ * (a staging slot, a cache slot or the home copy) and `layer->limit` is the SwiGLU clamp. Experts whose range
+ * passes n are ignored. x [T][H] as for mm_moe_prefill. Requires E <= 1024, H % 256 == 0, I % 128 == 0. */
+size_t mm_fat_batched_workspace(int n, int T, int E, int H, int I);
+int mm_fat_batched(const mm_layer_t* layer, const void* x, int x_dtype, int T, int n, const int64_t* token_sorted,
+                   const uint16_t* weight_sorted, const int32_t* counts, const uint8_t* skip, int cap, float* out,
+                   void* workspace, size_t workspace_bytes, mm_stream_t stream);
+
+/* ------------------------------------------------------------------------------------ expert placement */
+
+/* Slot-table repoint; replaces _ec_point's index_copy_ writes (ct/ct_vllm.py:268-279): items int64 [n][5] =
+ * (e, gate address, up address, down address, slot) in device or host-mapped memory; for each item
+ * gate_ptr[e], up_ptr[e], down_ptr[e] = the addresses and slotof[e] = slot (slotof int32 [E], may be NULL).
+ * Items with e outside [0, E) are skipped; of several items naming one expert the last wins. Stream-ordered:
+ * kernels enqueued after it on `stream` read the new placement, kernels before it the old one. n <= 65536. */
+int mm_slot_point(int64_t* gate_ptr, int64_t* up_ptr, int64_t* down_ptr, int32_t* slotof, int E, const int64_t* items,
+                  int n, mm_stream_t stream);
+
+/* Staging copies; replaces the reference's per-expert copy_(non_blocking=True) of pinned host rows into cache
+ * and staging slots (ct/ct_vllm.py:399-405, patches/vllm-exl3-host-dma.patch:100-124): copy i moves bytes[i]
+ * bytes from src[i] to dst[i] (host arrays of addresses: device memory, or host memory from mm_host_alloc), as
+ * copy-engine transfers (hipMemcpyAsync) enqueued on `stream`. A copy whose source and destination both continue
+ * the previous one is merged into it. Returns the number of transfers enqueued (>= 0) or a negative error. */
+int mm_stage_copy(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int n, mm_stream_t stream);
+
 /* Synthetic trellis words: word i of a stream with `seed` is bits 16*(i%4)..+15 of
  * splitmix64(seed + (i/4 + 1) * 0x9E3779B97F4A7C15). Fills dst[j] = word(start + j) for j < n. */
 int mm_synth_u16(uint16_t* dst, uint64_t n, uint64_t seed, uint64_t start, mm_stream_t stream);
