@@ -83,6 +83,16 @@ def cpu_baseline(routes, T, H, I, E, layer_seed, budget_s=15.0):
             "mode": {0: "AFFINE", 1: "EXACT", 2: "I16"}.get(mode, str(mode)), "experts": len(experts)}
 
 
+def traffic_bytes(L, T):
+    """HBM bytes per launch of the gate/up decode kernel at this workload, from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a calibration copy), or None for another workload."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if L != 40 or T != 4 or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return float(json.load(f)["traffic_bytes_per_launch"])
+
+
 def bench_prefill(store, E, H, I, reps, tokens=16384, k=8, cap=32):
     """The 16k-token prefill layer: skewed routing (64 hot experts take 60 % of the assignments), every routed
     expert above `cap` routes on the fat-expert grouped GEMM. Returns timings and MFMA utilisation."""
@@ -290,6 +300,9 @@ def main():
     ap.add_argument("--tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="after the measurements, copy 1 GiB device to device 3 times (torch copy kernel of known "
+                         "bytes: 1 GiB read + 1 GiB written per launch), to scale HBM byte counters")
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--workload", choices=("decode", "cache"), default="decode",
                     help="decode: the 40-layer HBM-resident decode step (+ the 16k prefill layer); cache: the "
@@ -472,7 +485,7 @@ def main():
                    "layers": L, "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": K_TOP,
                    "shared_experts": 1, "mean_distinct_experts_per_layer": round(float(np.mean(uniq)), 2)},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(L, T),
                      "kernel": "mm::k_partial<0> (gate/up decode GEMV partial sums)",
                      "avg_launch_us": round(float(t_gu) * 1e3, 2),
                      "bytes_per_launch": round(float(bytes_gu.mean()), 1)},
@@ -492,6 +505,13 @@ def main():
                                          f"calls, reference CPU tier mode {cpu['mode']}, p50 {cpu['p50_layer_ms']:.3f} ms "
                                          f"(p90 {cpu['p90_layer_ms']:.3f}) per layer, scaled to {L} layers"}
     print(json.dumps(res), flush=True)
+    if args.copy_calibration:
+        a = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
+        b = torch.empty_like(a)
+        for _ in range(3):
+            b.copy_(a)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 1 GiB device copies done")
 
 
 if __name__ == "__main__":
