@@ -46,54 +46,128 @@ struct FatArgs
     const uint16_t* svh2;         // [E][H]
     const int32_t* route_at;      // [n] flat route index of each sorted position
     uint16_t* xd;                 // mode 0 output [n][I] (operand order)
-    float* Y;                     // mode 1 output [n_routes][H] (per route)
+    float* Y;                     // mode 1 output [n_routes][H] (per route), fp32 or (YH) fp16 bits
     int H, I, K, N, nunits, max_active;
     float limit;
 };
 
-// Transformed inputs of every fat route, one workgroup per sorted position (the expert's 2 x H/128 blocks, 4
-// waves, each transforming 4 blocks at a time so their shuffles overlap): r16(FWHT(x16 * suh_m) * HAD) per
+// Transformed inputs of every fat route, one workgroup per sorted position: r16(FWHT(x16 * suh_m) * HAD) per
 // 128-block (ft_core.h:96-102), where x16 is fp16 input as is, or bf16 / fp32 input rounded through bf16. Row pos
 // of xa holds, per 32-element step, the gate step then the up step in operand order (128 bytes: one cache line
 // per step, which the gate/up kernel loads whole).
+//
+// Wave w transforms matrix w >> 1, blocks (w & 1) * nb / 2 .. , four blocks at a time, 16 lanes per block and
+// 8 elements per lane: lane 4 q + g of a block holds the elements k = 32 q + 2 g + j + 8 h + 16 t (j, h, t in
+// {0, 1}) as v[4 t + 2 h + j], exactly the 8 operand-order positions 8 g .. 8 g + 7 of step q, so it stores them
+// with one 16-byte write. The butterflies keep the reference's order and arithmetic (strides 1, 2, 4, ..., 64,
+// (a, b) -> (a + b, a - b), ft_core.h:89-94): strides 1, 8, 16 pair elements within a lane; strides 2 and 4 pair
+// lanes 4 q + g and 4 q + (g ^ 1 or 2) (DPP quad permutations), strides 32 and 64 lanes q ^ 1 and q ^ 2 of the
+// block (swizzles). The lane holding the upper element of a cross-lane pair forms partner - self as
+// fma(-1, self, partner), the same single rounding.
+__device__ __forceinline__ float xlane(float v, int pattern)
+{
+    if (pattern == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+    if (pattern == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+    if (pattern == 4) return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));
+    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x201F));
+}
+
+template <int XD>
+__device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e, int pos, const uint16_t* suh13,
+                                               uint16_t* xa, int H)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane & 3, q = (lane >> 2) & 3, bl = lane >> 4;
+    const int m = wave >> 1, nb = H / 128;
+    const float s2 = (g & 1) ? -1.0f : 1.0f, s4 = (g & 2) ? -1.0f : 1.0f;
+    const float s32 = (q & 1) ? -1.0f : 1.0f, s64 = (q & 2) ? -1.0f : 1.0f;
+    const uint16_t* su = suh13 + ((size_t)e * 2 + m) * H;
+    uint16_t* dst = xa + (size_t)pos * 2 * H + m * 32 + 8 * g;
+    for (int b = (wave & 1) * (nb / 2) + bl; b < ((wave & 1) + 1) * (nb / 2); b += 4)
+    {
+        const int k0 = b * 128 + 32 * q + 2 * g;
+        float v[8];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+            {
+                const int k = k0 + 8 * h + 16 * t;
+                float x0, x1;
+                if constexpr (XD == MM_DTYPE_F16)
+                {
+                    const uint32_t d = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + row + k);
+                    x0 = h2f((uint16_t)(d & 0xffffu));
+                    x1 = h2f((uint16_t)(d >> 16));
+                }
+                else if constexpr (XD == MM_DTYPE_BF16)
+                {
+                    const uint32_t d = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + row + k);
+                    x0 = r16(__uint_as_float(d << 16));
+                    x1 = r16(__uint_as_float(d & 0xffff0000u));
+                }
+                else
+                {
+                    const float2 f = *reinterpret_cast<const float2*>(static_cast<const float*>(x) + row + k);
+                    x0 = r16(bf16_value(f.x));
+                    x1 = r16(bf16_value(f.y));
+                }
+                const uint32_t sd = *reinterpret_cast<const uint32_t*>(su + k);
+                v[4 * t + 2 * h] = x0 * h2f((uint16_t)(sd & 0xffffu));
+                v[4 * t + 2 * h + 1] = x1 * h2f((uint16_t)(sd >> 16));
+            }
+        // stride 1 (j)
+#pragma unroll
+        for (int i = 0; i < 8; i += 2)
+        {
+            const float a0 = v[i], a1 = v[i + 1];
+            v[i] = a0 + a1;
+            v[i + 1] = a0 - a1;
+        }
+        // strides 2, 4 (lanes g ^ 1, g ^ 2)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(s2, v[i], xlane(v[i], 1));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(s4, v[i], xlane(v[i], 2));
+        // strides 8 (h), 16 (t)
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+            if ((i & 2) == 0)
+            {
+                const float a0 = v[i], a1 = v[i + 2];
+                v[i] = a0 + a1;
+                v[i + 2] = a0 - a1;
+            }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+        {
+            const float a0 = v[i], a1 = v[i + 4];
+            v[i] = a0 + a1;
+            v[i + 4] = a0 - a1;
+        }
+        // strides 32, 64 (lanes q ^ 1, q ^ 2)
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(s32, v[i], xlane(v[i], 4));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(s64, v[i], xlane(v[i], 8));
+        uint4 o;
+        o.x = (uint32_t)f2h(v[0] * HAD) | ((uint32_t)f2h(v[1] * HAD) << 16);
+        o.y = (uint32_t)f2h(v[2] * HAD) | ((uint32_t)f2h(v[3] * HAD) << 16);
+        o.z = (uint32_t)f2h(v[4] * HAD) | ((uint32_t)f2h(v[5] * HAD) << 16);
+        o.w = (uint32_t)f2h(v[6] * HAD) | ((uint32_t)f2h(v[7] * HAD) << 16);
+        *reinterpret_cast<uint4*>(dst + (size_t)(4 * b + q) * 64) = o;
+    }
+}
+
 __device__ __forceinline__ void fat_prep_row(const void* x, int x_dtype, size_t row, int e, int pos,
                                              const uint16_t* suh13, uint16_t* xa, int H)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int nb = H / 128;
-    for (int b0 = wave * 4; b0 < 2 * nb; b0 += 16)
-    {
-        float va[4], vb[4], sa[4], sb[4];
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-        {
-            const int b = b0 + k, m = b / nb, h0 = (b % nb) * 128;
-            va[k] = load_x(x, x_dtype, row + h0 + lane);
-            vb[k] = load_x(x, x_dtype, row + h0 + lane + 64);
-            const uint16_t* su = suh13 + ((size_t)e * 2 + m) * H + h0;
-            sa[k] = h2f(su[lane]);
-            sb[k] = h2f(su[lane + 64]);
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-        {
-            if (x_dtype != MM_DTYPE_F16)
-            {
-                va[k] = r16(bf16_value(va[k]));
-                vb[k] = r16(bf16_value(vb[k]));
-            }
-            prep_block_wave(va[k], vb[k], sa[k], sb[k]);
-        }
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-        {
-            const int b = b0 + k, m = b / nb, h0 = (b % nb) * 128;
-            uint16_t* dst = xa + (size_t)pos * 2 * H + m * 32;
-            const int ka = h0 + lane, kb = h0 + lane + 64;
-            dst[(ka >> 5) * 64 + (operand_index(ka) & 31)] = f2h(va[k]);
-            dst[(kb >> 5) * 64 + (operand_index(kb) & 31)] = f2h(vb[k]);
-        }
-    }
+    if (x_dtype == MM_DTYPE_F16)
+        fat_prep_row_t<MM_DTYPE_F16>(x, row, e, pos, suh13, xa, H);
+    else if (x_dtype == MM_DTYPE_BF16)
+        fat_prep_row_t<MM_DTYPE_BF16>(x, row, e, pos, suh13, xa, H);
+    else
+        fat_prep_row_t<MM_DTYPE_F32>(x, row, e, pos, suh13, xa, H);
 }
 
 __global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, const int64_t* ids, const int32_t* counts,
@@ -213,7 +287,7 @@ __device__ __forceinline__ int chunk_slot(int q, int r)
 // eighth of the inputs and waves 0 .. 3 also the trellis (chunk w: tile row w >> 1 of matrix / block w & 1),
 // which runs further ahead; wave w decodes tiles 4 (w & 1) .. + 3 of chunk w >> 1. Rows past the tile's routes
 // read zero inputs.
-template <int MODE, int MB>
+template <int MODE, int MB, bool YH = false>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
 {
     constexpr int BM = 32 * MB;
@@ -477,9 +551,19 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
                 for (int v = 0; v < 4; ++v)
                     if (r0 + v < rows)
                     {
-                        float* yr = a.Y + (size_t)a.route_at[pos0 + r0 + v] * a.H;
-                        yr[c0 + lane] = ya[v];
-                        yr[c0 + lane + 64] = yb[v];
+                        const size_t yo = (size_t)a.route_at[pos0 + r0 + v] * a.H + c0 + lane;
+                        if constexpr (YH)
+                        {
+                            // the output transform rounded ya, yb to fp16: the half store is exact
+                            uint16_t* yr = reinterpret_cast<uint16_t*>(a.Y);
+                            yr[yo] = f2h(ya[v]);
+                            yr[yo + 64] = f2h(yb[v]);
+                        }
+                        else
+                        {
+                            a.Y[yo] = ya[v];
+                            a.Y[yo + 64] = yb[v];
+                        }
                     }
             }
         }
@@ -487,8 +571,9 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
 }
 
 // Weighted combine of the fat routes: out[t] = (accumulate ? out[t] : 0) + sum_j w_j y_j over the routes j of
-// token t whose expert has more than cap routes, fp32 fma in ascending j (with cap 0 this is mm_combine).
-__global__ __launch_bounds__(256) void k_fat_combine(float* __restrict__ out, const float* __restrict__ Y,
+// token t whose expert has more than cap routes, fp32 fma in ascending j (with cap 0 this is mm_combine). The
+// per-route rows y_j are fp16 (the down GEMM writes them so: its output transform rounds every value to fp16).
+__global__ __launch_bounds__(256) void k_fat_combine(float* __restrict__ out, const uint16_t* __restrict__ Y,
                                                      const int64_t* __restrict__ ids, const float* __restrict__ w,
                                                      const int32_t* __restrict__ counts, int T, int k, int H, int E,
                                                      int cap, int accumulate)
@@ -503,7 +588,9 @@ __global__ __launch_bounds__(256) void k_fat_combine(float* __restrict__ out, co
         const int64_t e = ids[s];
         if (e < 0 || e >= E || counts[e] <= cap) continue;
         const float wj = w[s];
-        const float4 y = *reinterpret_cast<const float4*>(Y + (size_t)s * H + h);
+        const uint2 yb = *reinterpret_cast<const uint2*>(Y + (size_t)s * H + h);
+        const float4 y = make_float4(h2f((uint16_t)(yb.x & 0xffffu)), h2f((uint16_t)(yb.x >> 16)),
+                                     h2f((uint16_t)(yb.y & 0xffffu)), h2f((uint16_t)(yb.y >> 16)));
         acc.x = fmaf(wj, y.x, acc.x);
         acc.y = fmaf(wj, y.y, acc.y);
         acc.z = fmaf(wj, y.z, acc.z);
@@ -646,7 +733,7 @@ __global__ __launch_bounds__(1024) void k_scan_i32(const int32_t* tcount, int32_
 }
 
 // out[t] += sum over the token's selected positions p, in ascending p, of fp32(weight_sorted[p]) * Y[p] (fp32 fma).
-__global__ __launch_bounds__(256) void k_fatb_combine(float* __restrict__ out, const float* __restrict__ Y,
+__global__ __launch_bounds__(256) void k_fatb_combine(float* __restrict__ out, const uint16_t* __restrict__ Y,
                                                       const uint16_t* __restrict__ wsorted, const int32_t* __restrict__ toff,
                                                       const int32_t* __restrict__ tpos, int T, int H)
 {
@@ -667,7 +754,9 @@ __global__ __launch_bounds__(256) void k_fatb_combine(float* __restrict__ out, c
         }
         prev = p;
         const float wj = h2f(wsorted[p]);
-        const float4 y = *reinterpret_cast<const float4*>(Y + (size_t)p * H + h);
+        const uint2 yb = *reinterpret_cast<const uint2*>(Y + (size_t)p * H + h);
+        const float4 y = make_float4(h2f((uint16_t)(yb.x & 0xffffu)), h2f((uint16_t)(yb.x >> 16)),
+                                     h2f((uint16_t)(yb.y & 0xffffu)), h2f((uint16_t)(yb.y >> 16)));
         acc.x = fmaf(wj, y.x, acc.x);
         acc.y = fmaf(wj, y.y, acc.y);
         acc.z = fmaf(wj, y.z, acc.z);
@@ -742,7 +831,7 @@ static int fat_check(const mm_layer_t* L, const void* x, int x_dtype, int T, int
 
 // Plan and both GEMMs over the sorted positions in ws (counts, offsets, order, active, nactive filled): Y rows of
 // every position of an active expert with more than cap routes.
-static int fat_gemms(const mm_layer_t* L, int n, int cap, const FatWs& ws, hipStream_t s)
+static int fat_gemms(const mm_layer_t* L, int n, int cap, const FatWs& ws, hipStream_t s, bool yh)
 {
     const int E = L->E, na = n < E ? n : E;
     hipLaunchKernelGGL(k_fat_plan, dim3(1), dim3(FT_PLAN_MAX), 0, s, ws.counts, ws.offsets, ws.active, ws.nactive,
@@ -760,14 +849,23 @@ static int fat_gemms(const mm_layer_t* L, int n, int cap, const FatWs& ws, hipSt
     d.xa = ws.xd; d.K = L->I; d.N = L->H; d.nunits = L->H / 256;
     FatArgs ds = d;
     ds.tile_off = ws.off_small;
-    if (max_big > 0) hipLaunchKernelGGL((k_fat<1, FT_BIG / 32>), grid(max_big, d.nunits), dim3(FT_THREADS), 0, s, d);
-    hipLaunchKernelGGL((k_fat<1, FT_SMALL / 32>), grid(max_small, d.nunits), dim3(FT_THREADS), 0, s, ds);
+    if (yh)
+    {
+        if (max_big > 0)
+            hipLaunchKernelGGL((k_fat<1, FT_BIG / 32, true>), grid(max_big, d.nunits), dim3(FT_THREADS), 0, s, d);
+        hipLaunchKernelGGL((k_fat<1, FT_SMALL / 32, true>), grid(max_small, d.nunits), dim3(FT_THREADS), 0, s, ds);
+    }
+    else
+    {
+        if (max_big > 0) hipLaunchKernelGGL((k_fat<1, FT_BIG / 32>), grid(max_big, d.nunits), dim3(FT_THREADS), 0, s, d);
+        hipLaunchKernelGGL((k_fat<1, FT_SMALL / 32>), grid(max_small, d.nunits), dim3(FT_THREADS), 0, s, ds);
+    }
     return check_launch("fat path");
 }
 
 // Permutation, input prep, plan and both GEMMs: Y rows of every route whose expert has more than cap routes.
 static int fat_run(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids, int cap,
-                   const FatWs& ws, hipStream_t s)
+                   const FatWs& ws, hipStream_t s, bool yh)
 {
     const int n = T * topk, E = L->E;
     int rc = mm_permute(ids, nullptr, n, topk, E, ws.counts, ws.offsets, ws.order, nullptr, nullptr, nullptr, ws.active,
@@ -775,7 +873,7 @@ static int fat_run(const mm_layer_t* L, const void* x, int x_dtype, int T, int t
     if (rc) return rc;
     hipLaunchKernelGGL(k_fat_prep, dim3(n), dim3(256), 0, s, x, x_dtype, ids, ws.counts, ws.offsets, ws.order, L->suh13,
                        ws.xa, topk, E, L->H, cap);
-    return fat_gemms(L, n, cap, ws, s);
+    return fat_gemms(L, n, cap, ws, s, yh);
 }
 
 // Workspace of the sorted-route form: the fat sections for n positions, then the token lists.
@@ -823,7 +921,7 @@ int mm_grouped_gemm(const mm_layer_t* L, const void* x, int x_dtype, int T, int 
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     FatWs ws = fat_carve(workspace, T * topk, L->E, L->H, L->I);
     ws.Y = Y;
-    return fat_run(L, x, x_dtype, T, topk, ids, cap, ws, s);
+    return fat_run(L, x, x_dtype, T, topk, ids, cap, ws, s, false);
 }
 
 int mm_moe_prefill(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids, const float* w,
@@ -834,10 +932,11 @@ int mm_moe_prefill(const mm_layer_t* L, const void* x, int x_dtype, int T, int t
     MM_CHECK_ARG(w && out && cap >= 0, "mm_moe_prefill: null pointer or negative cap");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const FatWs ws = fat_carve(workspace, T * topk, L->E, L->H, L->I);
-    const int r = fat_run(L, x, x_dtype, T, topk, ids, cap, ws, s);
+    const int r = fat_run(L, x, x_dtype, T, topk, ids, cap, ws, s, true);
     if (r) return r;
     const dim3 grid((unsigned)((L->H / 4 + 255) / 256), (unsigned)T);
-    hipLaunchKernelGGL(k_fat_combine, grid, dim3(256), 0, s, out, ws.Y, ids, w, ws.counts, T, topk, L->H, L->E, cap,
+    hipLaunchKernelGGL(k_fat_combine, grid, dim3(256), 0, s, out, reinterpret_cast<const uint16_t*>(ws.Y), ids, w,
+                       ws.counts, T, topk, L->H, L->E, cap,
                        accumulate);
     return check_launch("mm_moe_prefill");
 }
@@ -879,10 +978,11 @@ int mm_fat_batched(const mm_layer_t* L, const void* x, int x_dtype, int T, int n
                        ws.tcount, ws.toff, ws.tpos, T, E, n);
     hipLaunchKernelGGL(k_fatb_prep, dim3(n), dim3(256), 0, s, x, x_dtype, token_sorted, ws.f.counts, ws.f.offsets,
                        L->suh13, ws.f.xa, T, E, L->H);
-    int r = fat_gemms(L, n, cap, ws.f, s);
+    int r = fat_gemms(L, n, cap, ws.f, s, true);
     if (r) return r;
     const dim3 grid((unsigned)((L->H / 4 + 255) / 256), (unsigned)T);
-    hipLaunchKernelGGL(k_fatb_combine, grid, dim3(256), 0, s, out, ws.f.Y, weight_sorted, ws.toff, ws.tpos, T, L->H);
+    hipLaunchKernelGGL(k_fatb_combine, grid, dim3(256), 0, s, out, reinterpret_cast<const uint16_t*>(ws.f.Y),
+                       weight_sorted, ws.toff, ws.tpos, T, L->H);
     return check_launch("mm_fat_batched");
 }
 
