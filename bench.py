@@ -142,6 +142,89 @@ def bench_prefill(store, E, H, I, reps, tokens=16384, k=8, cap=32):
             "mfma_peak_tflops": peak / 1e12, "dtype": "fp16 MFMA, fp32 accumulation", "reps": reps}
 
 
+def bench_split(calls=10000, per_graph=100):
+    """Split + weighted combine + host-partial combine of one decode call (T=4 x top-8 over 384 experts, Zipf(1.1)
+    routing, a 709-slot cache map with about 40 % of the picked experts resident, the image's cost-model policy,
+    synthetic expert rows Y ~ N(0, 1) [32, 4096]); the host partial is already answered (ctrl[1] set ahead), so
+    the bounded wait returns at once. `per_graph` calls are captured in one HIP graph; each replay is timed with
+    events, giving `calls` per-call latencies (replay time / per_graph)."""
+    import numpy as np
+    import torch
+    from mi355moe import _lib, workload
+    from mi355moe.hostmem import HostBuffer
+    dev = torch.device("cuda", 0)
+    T, K, E, H = 4, 8, 384, 4096
+    n = T * K
+    ids, w = workload.zipf_routing(T, K, E, seed=2000)
+    slotof = workload.cache_map(ids, E, slots=709, frac_resident=0.4, seed=2000)
+    z = np.random.default_rng(7).normal(0, 1, (T, H)).astype(np.float16)
+    pol = np.array([0.58, 0.03, 0.11, 0.20, 0.35, 384, -1, 0, 0], np.float32)
+    Yh = np.random.default_rng(8).normal(0, 1, (n, H)).astype(np.float32)
+    hb = HostBuffer(128 + T * H * 2 + n * 12)
+    ctrl = hb.array(np.int64, (16,), 0)
+    ctrl[:] = 0
+    ctrl[1] = 1 << 62                      # the host has answered every job
+    t = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+    sel, wd, zd, sl = t(ids.ravel()), t(w.ravel()), t(z.view(np.uint16)), t(slotof)
+    score, pold, Y = torch.zeros(E, dtype=torch.float32, device=dev), t(pol), t(Yh)
+    seqc = torch.zeros(1, dtype=torch.int64, device=dev)
+    so = torch.empty(n, dtype=torch.int64, device=dev)
+    wo = torch.empty(n, dtype=torch.float32, device=dev)
+    dflag = torch.zeros(1, dtype=torch.int64, device=dev)
+    stats = torch.zeros(8, dtype=torch.int64, device=dev)
+    counts = torch.zeros(E, dtype=torch.int32, device=dev)
+    hout = torch.zeros(T * H, dtype=torch.float32, device=dev)
+    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+
+    def call(stream):
+        sp = stream.cuda_stream
+        _lib.call("mm_split", sel.data_ptr(), wd.data_ptr(), zd.data_ptr(), n, T, H, E, sl.data_ptr(), score.data_ptr(),
+                  pold.data_ptr(), hb.data_ptr(0), hb.data_ptr(128), hb.data_ptr(128 + T * H * 2), seqc.data_ptr(), 0,
+                  so.data_ptr(), wo.data_ptr(), dflag.data_ptr(), stats.data_ptr(), counts.data_ptr(), None, None, None,
+                  sp)
+        _lib.call("mm_combine", out.data_ptr(), Y.data_ptr(), so.data_ptr(), wo.data_ptr(), T, K, H, E, 0, sp)
+        _lib.call("mm_combine_host", out.data_ptr(), T * H, dflag.data_ptr(), hb.data_ptr(0), hout.data_ptr(),
+                  stats.data_ptr(), 10 ** 9, sp)
+
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        call(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(per_graph):
+            call(torch.cuda.current_stream())
+    g.replay()
+    torch.cuda.synchronize()
+    reps = max(1, calls // per_graph)
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(reps)]
+    for a, b in evs:
+        a.record()
+        g.replay()
+        b.record()
+    torch.cuda.synchronize()
+    per = np.array(sorted(a.elapsed_time(b) * 1e3 / per_graph for a, b in evs))
+    st = stats.cpu().tolist()
+    res = {"workload": "split + weighted combine + host-partial combine, T=4 x top-8 over 384 experts, 709-slot map",
+           "calls": reps * per_graph, "p50_us": round(float(per[len(per) // 2]), 3),
+           "p90_us": round(float(per[int(len(per) * 0.9)]), 3), "hits_per_call": round(st[0] / max(1, st[3]), 2),
+           "misses_per_call": round(st[1] / max(1, st[3]), 2), "host_experts_per_call": round(st[2] / max(1, st[3]), 2)}
+    # the oracle's split and combine on one host core (bounded sample: 2,000 calls)
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle as O
+    ts = []
+    for _ in range(2000):
+        t0 = time.perf_counter()
+        r = O.split(ids.ravel(), w.ravel(), z, E, slotof, np.zeros(E, np.float32), pol)
+        wm = np.where(r["sel_out"] >= 0, r["w_out"], 0).reshape(T, K).astype(np.float32)
+        O.combine(np.zeros((T, H), np.float32), Yh, wm)
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    res["cpu_baseline"] = {"p50_us": round(ts[len(ts) // 2] * 1e6, 2), "cores": 1, "kind": "port",
+                           "sample": "2,000 calls of the oracle's split and combine (C restatement) on one core"}
+    return res
+
+
 def bench_cache(args):
     """Capacity-limited expert cache: 40 layers whose routed experts live in pinned host memory, a 709-slot HBM
     cache (elastic, replanned every 16 decode steps), decode T=4 steps interleaved with 8,192-token prefill
@@ -455,6 +538,10 @@ def main():
     bytes1 = float(sum((len(np.unique(r[0])) + 1) * BYTES_EXPERT for r in r1))
     log(f"decode T=1: {ms1:.3f} ms per step, {bytes1 / (ms1 * 1e-3) / 1e9:.0f} GB/s")
 
+    log("split/combine latency (10,000 graph-launched calls)")
+    split_res = bench_split()
+    log(f"split/combine: {split_res}")
+
     prefill = None
     if not args.no_prefill:
         del g_gu, g_d, g1
@@ -496,6 +583,7 @@ def main():
         "decode_t1": {"ms_per_step": round(ms1, 4), "tok_s": round(1 / (ms1 * 1e-3), 2),
                       "hbm_gbs": round(bytes1 / (ms1 * 1e-3) / 1e9, 1)},
     }
+    res["split_combine"] = split_res
     if prefill is not None:
         res["prefill"] = prefill
     if cpu is not None:
