@@ -427,13 +427,16 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
         if (tloader) load_trellis(s + FT_PT);
         // one step: the trellis words of step s + 1 and the operands of step s first, then per row block its 4
         // MFMAs, one tile of step s + 1 decoded after every MB / 4 blocks
-        const uint32_t* tw = tword + (size_t)((s + 1) % FT_TS) * (T_SLOT / 4);
+        // slot offset as one scalar, so each read is a per-lane base plus an immediate
+        const uint32_t toff = (uint32_t)__builtin_amdgcn_readfirstlane(((s + 1) % FT_TS) * T_SLOT);
+        const uint8_t* thp = reinterpret_cast<const uint8_t*>(tword + lhi) + toff;
+        const uint8_t* tlp = reinterpret_cast<const uint8_t*>(tword + llo) + toff;
         uint32_t th[4], tl[4];
 #pragma unroll
         for (int u = 0; u < 4; ++u)
         {
-            th[u] = tw[u * 32 + lhi];
-            tl[u] = tw[u * 32 + llo];
+            th[u] = *reinterpret_cast<const uint32_t*>(thp + u * 128);
+            tl[u] = *reinterpret_cast<const uint32_t*>(tlp + u * 128);
         }
         const uint8_t* as = Aring + (size_t)(s % FT_PA) * A_STAGE;
         const uint8_t* bs = bsrc + (size_t)(s & 1) * B_BUF;

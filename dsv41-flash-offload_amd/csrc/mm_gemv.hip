@@ -10,7 +10,7 @@
 //   2. k_partial<0>    gate/up partial sums, one launch that fills the GPU once: the work -- every
 //                      (active expert, matrix, 128 output columns) segment of 256 tile rows -- is cut into
 //                      equal row ranges, one per wave, from the active-expert count on the device. A wave
-//                      streams its rows (8 tiles = 768 contiguous bytes each) from HBM into an 8-deep
+//                      streams its rows (8 tiles = 768 contiguous bytes each) from HBM into a 4-deep
 //                      wave-private LDS ring with buffer-to-LDS loads, decodes each tile in registers and
 //                      multiplies two tile rows at a time on v_mfma_f32_16x16x32_f16 against the inputs of up
 //                      to 16 routes (L2 reads, prefetched with the same depth).
@@ -35,10 +35,10 @@ constexpr int GV_THREADS = 64 * GV_WAVES;
 constexpr int GV_COLS = 128;          // output columns per segment (8 tiles)
 constexpr int GV_MAX_ROWS = 256;      // routes per expert on this path
 constexpr int GV_ROUTE_MAX = 1024;    // in-kernel routing limit (routes per call)
-constexpr int GV_RING = 8;            // tile rows in flight per wave (even: rows go through MFMA in pairs)
+constexpr int GV_RING = 4;            // tile rows in flight per wave (even: rows go through MFMA in pairs)
 static_assert(GV_RING % 2 == 0, "row pairs");
 constexpr int ROW_BYTES = 8 * 96;     // one tile row of a segment
-constexpr int WAVES_PER_CU = 16;      // partial kernels: 4 workgroups of 4 waves per CU (<= 128 VGPRs)
+constexpr int WAVES_PER_CU = 24;      // partial kernels: 6 workgroups of 4 waves per CU (<= 80 VGPRs, 16 KB LDS)
 constexpr int PREP_ROWS = 512;        // input rows per route-prep workgroup
 constexpr int MAX_TOPK = 16;
 
@@ -210,7 +210,7 @@ struct PartArgs
 };
 
 template <int MODE, bool EXACT>
-__global__ __launch_bounds__(GV_THREADS, 4) void k_partial(PartArgs a)
+__global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
 {
     constexpr int NMAT = MODE == 0 ? 2 : 1;
     // A 12-byte buffer-to-LDS load writes lane i's bytes at slot + 16 i (the fourth dword of each lane's 16 is
