@@ -185,12 +185,22 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
     __shared__ int cnt[1024];
     __shared__ int missA[1024];   // misses in ascending id
     __shared__ int miss[1024];    // misses stable-sorted by score
+    __shared__ float mkey[1024];  // score of missA[i]
+    __shared__ int s_slot[1024];  // slotof[e] >= 0
+    __shared__ float s_score[1024];
     __shared__ unsigned char cpu[1024];
     __shared__ int scan_tmp[16];
     __shared__ int s_nh, s_nm, s_best, s_publish, s_npk;
     __shared__ long long s_seq;
     const int t = threadIdx.x, E = a.E;
-    for (int e = t; e < E; e += blockDim.x) { cnt[e] = 0; cpu[e] = 0; }
+    // every global input is loaded up front (one round trip): the slot table and scores into LDS
+    for (int e = t; e < E; e += blockDim.x)
+    {
+        cnt[e] = 0;
+        cpu[e] = 0;
+        s_slot[e] = a.slotof[e] >= 0 ? 1 : 0;
+        s_score[e] = a.score[e];
+    }
     __syncthreads();
     for (int s = t; s < a.n; s += blockDim.x)
     {
@@ -208,7 +218,7 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
     {
         const int e = base + t;
         const bool touched = e < E && cnt[e] > 0;
-        const bool hit = touched && a.slotof[e] >= 0, mis = touched && !hit;
+        const bool hit = touched && s_slot[e] != 0, mis = touched && !hit;
         int th, tm;
         const int ph = block_scan_excl(hit ? 1 : 0, scan_tmp, &th);
         const int pm = block_scan_excl(mis ? 1 : 0, scan_tmp + 0, &tm);
@@ -218,14 +228,16 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
         nm += tm;
     }
     __syncthreads();
-    // stable sort of misses by score: rank = #smaller + #equal earlier
+    // stable sort of misses by score: rank = #smaller + #equal earlier (keys staged in LDS with one load each)
+    for (int i = t; i < nm; i += blockDim.x) mkey[i] = s_score[missA[i]];
+    __syncthreads();
     for (int i = t; i < nm; i += blockDim.x)
     {
-        const float key = a.score[missA[i]];
+        const float key = mkey[i];
         int r = 0;
         for (int m = 0; m < nm; ++m)
         {
-            const float km = a.score[missA[m]];
+            const float km = mkey[m];
             r += (km < key) || (km == key && m < i);
         }
         miss[r] = missA[i];
@@ -294,20 +306,23 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
     }
     if (publish)
     {
+        // the payload (x rows, picks, job words), one system fence per thread, then the sequence word: the host
+        // sees ctrl[0] = seq only after everything it describes (ct/ft_tier_cu_v.cu:85-98)
         const int nx = a.p[8] > 0.5f ? 0 : a.bsz * a.H / 8;
         const int4* src = reinterpret_cast<const int4*>(a.z);
         int4* dst = reinterpret_cast<int4*>(a.hx);
         for (int i = t; i < nx; i += blockDim.x) dst[i] = src[i];
-        __threadfence_system();
-        __syncthreads();
         if (t == 0)
         {
             __hip_atomic_store(&a.ctrl[2], (int64_t)a.li, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             __hip_atomic_store(&a.ctrl[3], (int64_t)a.bsz, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             __hip_atomic_store(&a.ctrl[4], (int64_t)npk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __threadfence_system();
+        }
+        __threadfence_system();
+        __syncthreads();
+        if (t == 0)
+        {
             __hip_atomic_store(&a.ctrl[0], (int64_t)s_seq, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_SYSTEM);
-            __threadfence_system();
             a.dflag[0] = s_seq;
         }
     }
