@@ -383,6 +383,7 @@ def main():
     ap.add_argument("--tokens", type=int, default=4)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
+    ap.add_argument("--no-split", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the measurements, copy 1 GiB device to device 3 times (torch copy kernel of known "
                          "bytes: 1 GiB read + 1 GiB written per launch), to scale HBM byte counters")
@@ -538,9 +539,11 @@ def main():
     bytes1 = float(sum((len(np.unique(r[0])) + 1) * BYTES_EXPERT for r in r1))
     log(f"decode T=1: {ms1:.3f} ms per step, {bytes1 / (ms1 * 1e-3) / 1e9:.0f} GB/s")
 
-    log("split/combine latency (10,000 graph-launched calls)")
-    split_res = bench_split()
-    log(f"split/combine: {split_res}")
+    split_res = None
+    if not args.no_split:
+        log("split/combine latency (10,000 graph-launched calls)")
+        split_res = bench_split()
+        log(f"split/combine: {split_res}")
 
     prefill = None
     if not args.no_prefill:
@@ -583,7 +586,8 @@ def main():
         "decode_t1": {"ms_per_step": round(ms1, 4), "tok_s": round(1 / (ms1 * 1e-3), 2),
                       "hbm_gbs": round(bytes1 / (ms1 * 1e-3) / 1e9, 1)},
     }
-    res["split_combine"] = split_res
+    if split_res is not None:
+        res["split_combine"] = split_res
     if prefill is not None:
         res["prefill"] = prefill
     if cpu is not None:
