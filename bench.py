@@ -33,8 +33,9 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(routes, T, H, I, E, layer_seed, budget_s=15.0):
-    """Time the reference CPU tier (ft_core.h moe_forward, auto mode) on one layer of the step."""
+def cpu_baseline(routes, T, H, I, E, layer_seed, budget_s=10.0):
+    """Time the reference CPU tier (ft_core.h moe_forward, auto mode) on one layer of the step: repeated calls for
+    at least `budget_s` seconds (and at least 300 calls), p50 / p90 of the per-call times."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -73,7 +74,7 @@ def cpu_baseline(routes, T, H, I, E, layer_seed, budget_s=15.0):
         mode = R.ref_moe_forward(0, P(x), T, P(tok), P(exp), P(wt), tok.size, P(out), -1)
     ts = []
     t_end = time.perf_counter() + budget_s
-    while len(ts) < 300 and time.perf_counter() < t_end:
+    while len(ts) < 300 or time.perf_counter() < t_end:
         t0 = time.perf_counter()
         R.ref_moe_forward(0, P(x), T, P(tok), P(exp), P(wt), tok.size, P(out), -1)
         ts.append(time.perf_counter() - t0)
