@@ -72,6 +72,60 @@ __device__ __forceinline__ float xlane(float v, int pattern)
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x201F));
 }
 
+// The 128-point transform of a block held by 16 lanes (lane 4 q + g of the block) with 8 elements each,
+// v[4 t + 2 h + j] = element 32 q + 2 g + j + 8 h + 16 t. sgn = (g & 1, g & 2, q & 1, q & 2 ? -1 : 1).
+struct Lane8Signs
+{
+    float s2, s4, s32, s64;
+};
+__device__ __forceinline__ Lane8Signs lane8_signs(int lane)
+{
+    const int g = lane & 3, q = (lane >> 2) & 3;
+    return { (g & 1) ? -1.0f : 1.0f, (g & 2) ? -1.0f : 1.0f, (q & 1) ? -1.0f : 1.0f, (q & 2) ? -1.0f : 1.0f };
+}
+__device__ __forceinline__ void fwht128_lane8(float (&v)[8], const Lane8Signs& sg)
+{
+    // stride 1 (j)
+#pragma unroll
+    for (int i = 0; i < 8; i += 2)
+    {
+        const float a0 = v[i], a1 = v[i + 1];
+        v[i] = a0 + a1;
+        v[i + 1] = a0 - a1;
+    }
+    // strides 2, 4 (lanes g ^ 1, g ^ 2)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sg.s2, v[i], xlane(v[i], 1));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sg.s4, v[i], xlane(v[i], 2));
+    // strides 8 (h), 16 (t)
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+        if ((i & 2) == 0)
+        {
+            const float a0 = v[i], a1 = v[i + 2];
+            v[i] = a0 + a1;
+            v[i + 2] = a0 - a1;
+        }
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+    {
+        const float a0 = v[i], a1 = v[i + 4];
+        v[i] = a0 + a1;
+        v[i + 4] = a0 - a1;
+    }
+    // strides 32, 64 (lanes q ^ 1, q ^ 2)
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sg.s32, v[i], xlane(v[i], 4));
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(sg.s64, v[i], xlane(v[i], 8));
+}
+// element index of v[i] in its 128-block for the lane (q, g) of the block
+__device__ __forceinline__ int lane8_k(int lane, int i)
+{
+    return 32 * ((lane >> 2) & 3) + 2 * (lane & 3) + (i & 1) + 8 * ((i >> 1) & 1) + 16 * (i >> 2);
+}
+
 template <int XD>
 __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e, int pos, const uint16_t* suh13,
                                                uint16_t* xa, int H)
@@ -79,8 +133,7 @@ __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e,
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane & 3, q = (lane >> 2) & 3, bl = lane >> 4;
     const int m = wave >> 1, nb = H / 128;
-    const float s2 = (g & 1) ? -1.0f : 1.0f, s4 = (g & 2) ? -1.0f : 1.0f;
-    const float s32 = (q & 1) ? -1.0f : 1.0f, s64 = (q & 2) ? -1.0f : 1.0f;
+    const Lane8Signs sg = lane8_signs(lane);
     const uint16_t* su = suh13 + ((size_t)e * 2 + m) * H;
     uint16_t* dst = xa + (size_t)pos * 2 * H + m * 32 + 8 * g;
     for (int b = (wave & 1) * (nb / 2) + bl; b < ((wave & 1) + 1) * (nb / 2); b += 4)
@@ -116,40 +169,7 @@ __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e,
                 v[4 * t + 2 * h] = x0 * h2f((uint16_t)(sd & 0xffffu));
                 v[4 * t + 2 * h + 1] = x1 * h2f((uint16_t)(sd >> 16));
             }
-        // stride 1 (j)
-#pragma unroll
-        for (int i = 0; i < 8; i += 2)
-        {
-            const float a0 = v[i], a1 = v[i + 1];
-            v[i] = a0 + a1;
-            v[i + 1] = a0 - a1;
-        }
-        // strides 2, 4 (lanes g ^ 1, g ^ 2)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(s2, v[i], xlane(v[i], 1));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(s4, v[i], xlane(v[i], 2));
-        // strides 8 (h), 16 (t)
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-            if ((i & 2) == 0)
-            {
-                const float a0 = v[i], a1 = v[i + 2];
-                v[i] = a0 + a1;
-                v[i + 2] = a0 - a1;
-            }
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-        {
-            const float a0 = v[i], a1 = v[i + 4];
-            v[i] = a0 + a1;
-            v[i + 4] = a0 - a1;
-        }
-        // strides 32, 64 (lanes q ^ 1, q ^ 2)
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(s32, v[i], xlane(v[i], 4));
-#pragma unroll
-        for (int i = 0; i < 8; ++i) v[i] = __builtin_fmaf(s64, v[i], xlane(v[i], 8));
+        fwht128_lane8(v, sg);
         uint4 o;
         o.x = (uint32_t)f2h(v[0] * HAD) | ((uint32_t)f2h(v[1] * HAD) << 16);
         o.y = (uint32_t)f2h(v[2] * HAD) | ((uint32_t)f2h(v[3] * HAD) << 16);
@@ -475,7 +495,7 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
     lds_barrier();
 
     // ---- epilogue through a transposed fp16 C tile in LDS (column c at c * CS halves; the output transforms
-    // round y to fp16 first), four rows per wave at a time
+    // round y to fp16 first)
     uint16_t* C = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
     for (int i = 0; i < MB; ++i)
@@ -488,86 +508,124 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
             d[1] = (uint32_t)f2h(acc[i][j][2]) | ((uint32_t)f2h(acc[i][j][3]) << 16);
         }
     __syncthreads();
-    // value of column c for rows r0 + 2 h, r0 + 2 h + 1 (h = 0, 1)
-    auto pair = [&](int c, int r0, int h, float& v0, float& v1) {
-        const uint32_t d = *reinterpret_cast<const uint32_t*>(C + (size_t)c * CS + r0 + 2 * h);
+    // Transforms in the layout of fwht128_lane8: per pass a wave takes 8 rows; lane (rpair, q, g) = (lane >> 4,
+    // (lane >> 2) & 3, lane & 3) holds rows r0 + 2 rpair and r0 + 2 rpair + 1 (one dword of the transposed tile per
+    // column) of the 8 columns lane8_k(lane, i) of each 128-block, so each butterfly stage is in-lane or a DPP /
+    // swizzle exchange within 16 lanes.
+    const Lane8Signs sg = lane8_signs(lane);
+    const int rpair = lane >> 4;
+    int kk[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kk[i] = lane8_k(lane, i);
+    // column c at rows r, r + 1 (r even)
+    auto rows2 = [&](int c, int r, float& v0, float& v1) {
+        const uint32_t d = *reinterpret_cast<const uint32_t*>(C + (size_t)c * CS + r);
         v0 = h2f((uint16_t)(d & 0xffffu));
         v1 = h2f((uint16_t)(d >> 16));
     };
-    for (int r0 = 4 * wave; r0 < rows; r0 += 4 * FT_WAVES)
+    if constexpr (MODE == 0)
     {
-        if constexpr (MODE == 0)
+        const int c0 = nu * 128;
+        const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c0;
+        const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c0;
+        const uint16_t* sd = a.suh2 + (size_t)e * a.I + c0;
+        float sgv[8], suv[8], sdv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
         {
-            const int c0 = nu * 128;
-            float ga[4], gb[4], ua[4], ub[4];
-#pragma unroll
-            for (int h = 0; h < 2; ++h)
-            {
-                pair(lane, r0, h, ga[2 * h], ga[2 * h + 1]);
-                pair(lane + 64, r0, h, gb[2 * h], gb[2 * h + 1]);
-                pair(128 + lane, r0, h, ua[2 * h], ua[2 * h + 1]);
-                pair(128 + lane + 64, r0, h, ub[2 * h], ub[2 * h + 1]);
-            }
-            const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c0;
-            const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c0;
-            const uint16_t* sd = a.suh2 + (size_t)e * a.I + c0;
-            const float sga = h2f(svg[lane]), sgb = h2f(svg[lane + 64]);
-            const float sua = h2f(svu[lane]), sub = h2f(svu[lane + 64]);
-            const float sda = h2f(sd[lane]), sdb = h2f(sd[lane + 64]);
-            float xa[4], xb[4];
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-            {
-                out_block_wave(ga[v], gb[v], sga, sgb);
-                out_block_wave(ua[v], ub[v], sua, sub);
-                xa[v] = r16(act_gu(ga[v], ua[v], a.limit));
-                xb[v] = r16(act_gu(gb[v], ub[v], a.limit));
-                prep_block_wave(xa[v], xb[v], sda, sdb);
-            }
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
-                if (r0 + v < rows)
-                {
-                    uint16_t* dst = a.xd + (size_t)(pos0 + r0 + v) * a.I;
-                    dst[operand_index(c0 + lane)] = f2h(xa[v]);
-                    dst[operand_index(c0 + lane + 64)] = f2h(xb[v]);
-                }
+            sgv[i] = h2f(svg[kk[i]]);
+            suv[i] = h2f(svu[kk[i]]);
+            sdv[i] = h2f(sd[kk[i]]);
         }
-        else
+        // operand order: the lane's 8 elements are positions 32 q + 8 g .. + 7 of the block, v[i] at + i
+        const int od = c0 + 32 * ((lane >> 2) & 3) + 8 * (lane & 3);
+        for (int r0 = 8 * wave; r0 < rows; r0 += 8 * FT_WAVES)
         {
+            const int r = r0 + 2 * rpair;
+            float gv[2][8], uv[2][8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+            {
+                rows2(kk[i], r, gv[0][i], gv[1][i]);
+                rows2(128 + kk[i], r, uv[0][i], uv[1][i]);
+            }
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+            {
+                // the tile holds fp16 values, so the output transform's first rounding is exact
+                fwht128_lane8(gv[h2], sg);
+                fwht128_lane8(uv[h2], sg);
+                float xv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                {
+                    const float gg = r16((gv[h2][i] * HAD) * sgv[i]);
+                    const float uu = r16((uv[h2][i] * HAD) * suv[i]);
+                    xv[i] = r16(act_gu(gg, uu, a.limit)) * sdv[i];
+                }
+                fwht128_lane8(xv, sg);
+                if (r + h2 < rows)
+                {
+                    uint4 o;
+                    o.x = (uint32_t)f2h(xv[0] * HAD) | ((uint32_t)f2h(xv[1] * HAD) << 16);
+                    o.y = (uint32_t)f2h(xv[2] * HAD) | ((uint32_t)f2h(xv[3] * HAD) << 16);
+                    o.z = (uint32_t)f2h(xv[4] * HAD) | ((uint32_t)f2h(xv[5] * HAD) << 16);
+                    o.w = (uint32_t)f2h(xv[6] * HAD) | ((uint32_t)f2h(xv[7] * HAD) << 16);
+                    *reinterpret_cast<uint4*>(a.xd + (size_t)(pos0 + r + h2) * a.I + od) = o;
+                }
+            }
+        }
+    }
+    else
+    {
+        float svv[2][8];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+        {
+            const uint16_t* sv = a.svh2 + (size_t)e * a.H + (2 * nu + hb) * 128;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) svv[hb][i] = h2f(sv[kk[i]]);
+        }
+        for (int r0 = 8 * wave; r0 < rows; r0 += 8 * FT_WAVES)
+        {
+            const int r = r0 + 2 * rpair;
+            // output rows of the lane's two routes (a row past the tile's routes is not stored)
+            const int y0 = r < rows ? a.route_at[pos0 + r] : 0;
+            const int y1 = r + 1 < rows ? a.route_at[pos0 + r + 1] : 0;
 #pragma unroll
             for (int hb = 0; hb < 2; ++hb)
             {
                 const int c0 = (2 * nu + hb) * 128;
-                float ya[4], yb[4];
+                float yv[2][8];
 #pragma unroll
-                for (int h = 0; h < 2; ++h)
+                for (int i = 0; i < 8; ++i) rows2(hb * 128 + kk[i], r, yv[0][i], yv[1][i]);
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
                 {
-                    pair(hb * 128 + lane, r0, h, ya[2 * h], ya[2 * h + 1]);
-                    pair(hb * 128 + lane + 64, r0, h, yb[2 * h], yb[2 * h + 1]);
-                }
-                const uint16_t* sv = a.svh2 + (size_t)e * a.H + c0;
-                const float sva = h2f(sv[lane]), svb = h2f(sv[lane + 64]);
+                    fwht128_lane8(yv[h2], sg);
 #pragma unroll
-                for (int v = 0; v < 4; ++v) out_block_wave(ya[v], yb[v], sva, svb);
-#pragma unroll
-                for (int v = 0; v < 4; ++v)
-                    if (r0 + v < rows)
+                    for (int i = 0; i < 8; ++i) yv[h2][i] = r16((yv[h2][i] * HAD) * svv[hb][i]);
+                    if (r + h2 < rows)
                     {
-                        const size_t yo = (size_t)a.route_at[pos0 + r0 + v] * a.H + c0 + lane;
-                        if constexpr (YH)
+                        const size_t yo = (size_t)(h2 ? y1 : y0) * a.H + c0;
+                        // elements 2 p, 2 p + 1 are adjacent columns kk[2 p], kk[2 p] + 1
+#pragma unroll
+                        for (int p2 = 0; p2 < 4; ++p2)
                         {
-                            // the output transform rounded ya, yb to fp16: the half store is exact
-                            uint16_t* yr = reinterpret_cast<uint16_t*>(a.Y);
-                            yr[yo] = f2h(ya[v]);
-                            yr[yo + 64] = f2h(yb[v]);
-                        }
-                        else
-                        {
-                            a.Y[yo] = ya[v];
-                            a.Y[yo + 64] = yb[v];
+                            if constexpr (YH)
+                            {
+                                // the output transform rounded y to fp16: the half stores are exact
+                                const uint32_t w2 = (uint32_t)f2h(yv[h2][2 * p2]) | ((uint32_t)f2h(yv[h2][2 * p2 + 1]) << 16);
+                                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.Y) + yo + kk[2 * p2]) = w2;
+                            }
+                            else
+                            {
+                                *reinterpret_cast<float2*>(a.Y + yo + kk[2 * p2]) =
+                                    make_float2(yv[h2][2 * p2], yv[h2][2 * p2 + 1]);
+                            }
                         }
                     }
+                }
             }
         }
     }
