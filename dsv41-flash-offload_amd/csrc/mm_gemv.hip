@@ -246,11 +246,12 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
         const int cb = seg % a.ncb, r = seg / a.ncb;
         const int m = r % NMAT, ai = r / NMAT;
         const int tr0 = piece * KT / pps, nrow = (piece + 1) * KT / pps - tr0;
-        const ExpertRec rc = a.rec[ai];
-        const int cnt = min(rc.cnt, GV_MAX_ROWS);
+        // fields read through the pointer: a local copy indexed by the runtime matrix would live in scratch
+        const ExpertRec* rc = a.rec + ai;
+        const int cnt = min(rc->cnt, GV_MAX_ROWS), first = rc->first;
         // per-matrix buffer descriptor in SGPRs. readfirstlane returns int: each half goes through uint32_t
         // before widening, or a low word >= 2^31 would sign-extend into the high word.
-        const uint64_t wp = (uint64_t)rc.w[MODE == 0 ? m : 2];
+        const uint64_t wp = (uint64_t)rc->w[MODE == 0 ? m : 2];
         const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)wp);
         const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(wp >> 32));
         const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
@@ -262,7 +263,7 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
         {
             const int nr = min(16, cnt - r0);
             // this lane's A row: routes past nr repeat a valid one and their outputs are never stored
-            const int pos = rc.first + r0 + min(col, nr - 1);
+            const int pos = first + r0 + min(col, nr - 1);
             const uint32_t xoff = (uint32_t)(((size_t)pos * NMAT + m) * a.K * 2) + (uint32_t)g * 16;
             float4_t acc[8];
 #pragma unroll
@@ -324,7 +325,7 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
                 const int rr = 4 * g + v;
                 if (rr < nr)
                 {
-                    float* dst = a.part + ((size_t)(piece * a.n + rc.first + r0 + rr) * NMAT + m) * a.N + cb * GV_COLS + col;
+                    float* dst = a.part + ((size_t)(piece * a.n + first + r0 + rr) * NMAT + m) * a.N + cb * GV_COLS + col;
 #pragma unroll
                     for (int c = 0; c < 8; ++c) dst[c * 16] = acc[c][v];
                 }
