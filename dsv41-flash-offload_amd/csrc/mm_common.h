@@ -31,21 +31,68 @@ __device__ __forceinline__ uint16_t f2bf(float f)
 }
 __device__ __forceinline__ float bf16_value(float f) { return __uint_as_float((uint32_t)f2bf(f) << 16); }
 
+// Value of lane (lane ^ D) of the wave, D in {1, 2, 4, 8, 16, 32}, through DPP moves (xor 4 = the 8-lane mirror
+// then the reversed quad) and the gfx950 lane-swap instructions, so no exchange goes through the LDS crossbar.
+// Every lane of the wave must be active.
+template <int D>
+__device__ __forceinline__ int xor_lane_i(int v)
+{
+    static_assert(D == 1 || D == 2 || D == 4 || D == 8 || D == 16 || D == 32, "xor distance");
+    if constexpr (D == 1) return __builtin_amdgcn_mov_dpp(v, 0xB1, 0xF, 0xF, false);          // quad_perm 1,0,3,2
+    if constexpr (D == 2) return __builtin_amdgcn_mov_dpp(v, 0x4E, 0xF, 0xF, false);          // quad_perm 2,3,0,1
+    if constexpr (D == 4)                                                                       // half mirror, 3,2,1,0
+        return __builtin_amdgcn_mov_dpp(__builtin_amdgcn_mov_dpp(v, 0x141, 0xF, 0xF, false), 0x1B, 0xF, 0xF, false);
+    if constexpr (D == 8) return __builtin_amdgcn_mov_dpp(v, 0x128, 0xF, 0xF, false);         // row_ror 8
+    const int lane = threadIdx.x & 63;
+    if constexpr (D == 16)
+    {
+        // swapping the odd 16-lane rows of one copy with the even rows of another leaves the partner row in the
+        // first copy for odd rows and in the second for even rows
+        const auto r = __builtin_amdgcn_permlane16_swap((unsigned)v, (unsigned)v, false, false);
+        return (lane & 16) ? (int)r[0] : (int)r[1];
+    }
+    const auto r = __builtin_amdgcn_permlane32_swap((unsigned)v, (unsigned)v, false, false);
+    return (lane & 32) ? (int)r[0] : (int)r[1];
+}
+template <int D>
+__device__ __forceinline__ float xor_lane(float v)
+{
+    return __int_as_float(xor_lane_i<D>(__float_as_int(v)));
+}
+
+// Inclusive prefix sum over the 64 lanes: shifts within each 16-lane row (DPP row_shr with zero fill), then the
+// totals of the rows below, read as scalars. Every lane of the wave must be active.
+__device__ __forceinline__ int wave_incl_scan(int v)
+{
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xF, 0xF, true);    // row_shr 1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xF, 0xF, true);    // row_shr 2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xF, 0xF, true);    // row_shr 4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xF, 0xF, true);    // row_shr 8
+    const int lane = threadIdx.x & 63;
+    const int r0 = __builtin_amdgcn_readlane(v, 15), r1 = __builtin_amdgcn_readlane(v, 31);
+    const int r2 = __builtin_amdgcn_readlane(v, 47);
+    return v + (lane >= 16 ? r0 : 0) + (lane >= 32 ? r1 : 0) + (lane >= 48 ? r2 : 0);
+}
+
 // 128-point fast Walsh-Hadamard transform held by one wave64: lane L owns elements L (a) and L + 64 (b).
 // Stages run with strides 1, 2, ..., 64 and write (lo + hi, lo - hi), exactly the reference butterfly
 // (ft_core.h:89-94), so the fp32 results are bit-identical.
+template <int W>
+__device__ __forceinline__ void fwht_stage(float& a, float& b)
+{
+    const bool up = (threadIdx.x & W) != 0;
+    const float oa = xor_lane<W>(a), ob = xor_lane<W>(b);
+    a = up ? (oa - a) : (a + oa);
+    b = up ? (ob - b) : (b + ob);
+}
 __device__ __forceinline__ void fwht128_wave(float& a, float& b)
 {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int w = 1; w < 64; w <<= 1)
-    {
-        const float oa = __shfl_xor(a, w, 64);
-        const float ob = __shfl_xor(b, w, 64);
-        const bool up = (lane & w) != 0;
-        a = up ? (oa - a) : (a + oa);
-        b = up ? (ob - b) : (b + ob);
-    }
+    fwht_stage<1>(a, b);
+    fwht_stage<2>(a, b);
+    fwht_stage<4>(a, b);
+    fwht_stage<8>(a, b);
+    fwht_stage<16>(a, b);
+    fwht_stage<32>(a, b);
     const float lo = a, hi = b;
     a = lo + hi;
     b = lo - hi;

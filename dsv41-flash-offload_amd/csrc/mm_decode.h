@@ -79,8 +79,12 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 
 __device__ __forceinline__ float wave_sum(float v)
 {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    v += xor_lane<32>(v);
+    v += xor_lane<16>(v);
+    v += xor_lane<8>(v);
+    v += xor_lane<4>(v);
+    v += xor_lane<2>(v);
+    v += xor_lane<1>(v);
     return v;
 }
 
@@ -124,8 +128,12 @@ __device__ __forceinline__ float load_x(const void* x, int dtype, size_t i)
 
 __device__ __forceinline__ int wave_sum_int(int v)
 {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    v += xor_lane_i<32>(v);
+    v += xor_lane_i<16>(v);
+    v += xor_lane_i<8>(v);
+    v += xor_lane_i<4>(v);
+    v += xor_lane_i<2>(v);
+    v += xor_lane_i<1>(v);
     return v;
 }
 

@@ -61,15 +61,15 @@ struct FatArgs
 // {0, 1}) as v[4 t + 2 h + j], exactly the 8 operand-order positions 8 g .. 8 g + 7 of step q, so it stores them
 // with one 16-byte write. The butterflies keep the reference's order and arithmetic (strides 1, 2, 4, ..., 64,
 // (a, b) -> (a + b, a - b), ft_core.h:89-94): strides 1, 8, 16 pair elements within a lane; strides 2 and 4 pair
-// lanes 4 q + g and 4 q + (g ^ 1 or 2) (DPP quad permutations), strides 32 and 64 lanes q ^ 1 and q ^ 2 of the
-// block (swizzles). The lane holding the upper element of a cross-lane pair forms partner - self as
+// lanes 4 q + g and 4 q + (g ^ 1 or 2), strides 32 and 64 lanes q ^ 1 and q ^ 2 of the block (DPP moves, all
+// within the block's 16 lanes). The lane holding the upper element of a cross-lane pair forms partner - self as
 // fma(-1, self, partner), the same single rounding.
 __device__ __forceinline__ float xlane(float v, int pattern)
 {
-    if (pattern == 1) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
-    if (pattern == 2) return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
-    if (pattern == 4) return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x101F));
-    return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x201F));
+    if (pattern == 1) return xor_lane<1>(v);
+    if (pattern == 2) return xor_lane<2>(v);
+    if (pattern == 4) return xor_lane<4>(v);
+    return xor_lane<8>(v);
 }
 
 // The 128-point transform of a block held by 16 lanes (lane 4 q + g of the block) with 8 elements each,
@@ -252,17 +252,7 @@ __global__ __launch_bounds__(FT_PLAN_MAX) void k_fat_plan(const int32_t* counts,
         tb = c / FT_BIG + (r > FT_SMALL ? 1 : 0);
         ts = (r > 0 && r <= FT_SMALL) ? 1 : 0;
     }
-    int ib = tb, is = ts;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1)
-    {
-        const int o1 = __shfl_up(ib, d, 64), o2 = __shfl_up(is, d, 64);
-        if (lane >= d)
-        {
-            ib += o1;
-            is += o2;
-        }
-    }
+    const int ib = wave_incl_scan(tb), is = wave_incl_scan(ts);
     if (lane == 63)
     {
         s_w[0][wave] = ib;
@@ -510,8 +500,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
     __syncthreads();
     // Transforms in the layout of fwht128_lane8: per pass a wave takes 8 rows; lane (rpair, q, g) = (lane >> 4,
     // (lane >> 2) & 3, lane & 3) holds rows r0 + 2 rpair and r0 + 2 rpair + 1 (one dword of the transposed tile per
-    // column) of the 8 columns lane8_k(lane, i) of each 128-block, so each butterfly stage is in-lane or a DPP /
-    // swizzle exchange within 16 lanes.
+    // column) of the 8 columns lane8_k(lane, i) of each 128-block, so each butterfly stage is in-lane or a DPP
+    // exchange within 16 lanes.
     const Lane8Signs sg = lane8_signs(lane);
     const int rpair = lane >> 4;
     int kk[8];
@@ -674,13 +664,7 @@ __global__ __launch_bounds__(FT_PLAN_MAX) void k_fatb_setup(const int32_t* count
     __shared__ int s_w[2][FT_PLAN_MAX / 64];
     const int e = threadIdx.x, lane = e & 63, wave = e >> 6;
     const int c = e < E ? max(counts_in[e], 0) : 0;
-    int ic = c;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1)
-    {
-        const int o = __shfl_up(ic, d, 64);
-        if (lane >= d) ic += o;
-    }
+    const int ic = wave_incl_scan(c);
     if (lane == 63) s_w[0][wave] = ic;
     __syncthreads();
     int base = 0, total = 0;
@@ -691,13 +675,7 @@ __global__ __launch_bounds__(FT_PLAN_MAX) void k_fatb_setup(const int32_t* count
     }
     const long long off = (long long)base + ic - c;
     const bool sel = e < E && c > cap && !(skip && skip[e]) && off + c <= n;
-    int f = sel ? 1 : 0;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1)
-    {
-        const int o = __shfl_up(f, d, 64);
-        if (lane >= d) f += o;
-    }
+    const int f = wave_incl_scan(sel ? 1 : 0);
     if (lane == 63) s_w[1][wave] = f;
     __syncthreads();
     int fb = 0, nf = 0;
@@ -769,13 +747,7 @@ __global__ __launch_bounds__(1024) void k_scan_i32(const int32_t* tcount, int32_
     const int per = (T + 1023) / 1024, i0 = min(tid * per, T), i1 = min(i0 + per, T);
     int sum = 0;
     for (int i = i0; i < i1; ++i) sum += tcount[i];
-    int inc = sum;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1)
-    {
-        const int o = __shfl_up(inc, d, 64);
-        if (lane >= d) inc += o;
-    }
+    const int inc = wave_incl_scan(sum);
     if (lane == 63) s_w[wave] = inc;
     __syncthreads();
     int base = 0, total = 0;

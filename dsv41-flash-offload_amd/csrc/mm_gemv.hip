@@ -111,7 +111,7 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
     same = wave_sum_int(same);
     rank = wave_sum_int(rank);
     nv = wave_sum_int(nv);
-    for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
+    ss = wave_sum(ss);
     if (lane == 0)
     {
         s_cnt[wave][0] = less;

@@ -38,7 +38,7 @@ __device__ __forceinline__ uint64_t peer_mask(int key, bool valid)
     while (todo)
     {
         const int leader = __ffsll((unsigned long long)todo) - 1;
-        const int k0 = __shfl(key, leader, 64);
+        const int k0 = __builtin_amdgcn_readlane(key, leader);
         const uint64_t m = __ballot(valid && key == k0);
         if (valid && key == k0) mine = m;
         todo &= ~m;
@@ -51,13 +51,7 @@ __device__ __forceinline__ uint64_t peer_mask(int key, bool valid)
 __device__ int block_scan_excl(int v, int* scratch, int* total)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    int incl = v;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1)
-    {
-        const int o = __shfl_up(incl, d, 64);
-        if (lane >= d) incl += o;
-    }
+    const int incl = wave_incl_scan(v);
     __syncthreads();
     if (lane == 63) scratch[wave] = incl;
     __syncthreads();
@@ -142,13 +136,16 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
 #pragma unroll
         for (int i = 0; i < 16; ++i)
             if (!(taken & (1u << i)) && (v[i] > bv || (v[i] == bv && lane + 64 * i < be))) { bv = v[i]; be = lane + 64 * i; }
-#pragma unroll
-        for (int d = 32; d >= 1; d >>= 1)
-        {
-            const float ov = __shfl_xor(bv, d, 64);
-            const int oe = __shfl_xor(be, d, 64);
+        // max (value, then lower index) over the wave, distances 32, 16, ..., 1
+        auto pick = [&](float ov, int oe) {
             if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
-        }
+        };
+        pick(xor_lane<32>(bv), xor_lane_i<32>(be));
+        pick(xor_lane<16>(bv), xor_lane_i<16>(be));
+        pick(xor_lane<8>(bv), xor_lane_i<8>(be));
+        pick(xor_lane<4>(bv), xor_lane_i<4>(be));
+        pick(xor_lane<2>(bv), xor_lane_i<2>(be));
+        pick(xor_lane<1>(bv), xor_lane_i<1>(be));
         if ((be & 63) == lane) taken |= 1u << (be >> 6);
         sel_v[r] = bv;
         sel_e[r] = be;
@@ -567,7 +564,12 @@ __global__ __launch_bounds__(256) void k_prepare_input(const float* __restrict__
     {
         float ss = 0.0f;
         for (int h = threadIdx.x; h < H; h += blockDim.x) ss = fmaf(row[h], row[h], ss);
-        for (int d = 32; d >= 1; d >>= 1) ss += __shfl_xor(ss, d, 64);
+        ss += xor_lane<32>(ss);
+        ss += xor_lane<16>(ss);
+        ss += xor_lane<8>(ss);
+        ss += xor_lane<4>(ss);
+        ss += xor_lane<2>(ss);
+        ss += xor_lane<1>(ss);
         if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
         __syncthreads();
         const float tot = (red[0] + red[1]) + (red[2] + red[3]);
