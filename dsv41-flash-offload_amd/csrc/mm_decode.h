@@ -88,15 +88,6 @@ __device__ __forceinline__ float wave_sum(float v)
     return v;
 }
 
-// Sum of p[0 .. count) by one wave: one load per lane (all in flight together), then a fixed reduction tree.
-__device__ __forceinline__ float wave_sum_of(const float* p, int count)
-{
-    const int lane = threadIdx.x & 63;
-    float v = 0.0f;
-    for (int i = lane; i < count; i += 64) v += p[i];
-    return wave_sum(v);
-}
-
 struct PrepArgs
 {
     const void* x;            // [T][H], element type x_dtype
@@ -118,13 +109,6 @@ struct PrepArgs
     float* xsum;              // [n][2][nb] sums of xa over each workgroup's rows
     int n, topk, E, H, nb, x_dtype, rescale;
 };
-
-__device__ __forceinline__ float load_x(const void* x, int dtype, size_t i)
-{
-    if (dtype == MM_DTYPE_F16) return h2f(static_cast<const uint16_t*>(x)[i]);
-    if (dtype == MM_DTYPE_BF16) return __uint_as_float((uint32_t) static_cast<const uint16_t*>(x)[i] << 16);
-    return static_cast<const float*>(x)[i];
-}
 
 __device__ __forceinline__ int wave_sum_int(int v)
 {

@@ -52,9 +52,19 @@ __device__ __forceinline__ int pieces_per_segment(int nwaves, int nseg, int cap)
 
 // ------------------------------------------------------------------------------------------ 1. route prep
 
-// Every load that does not depend on another is issued before the first barrier (the route's id, all ids for
-// the position, the token row for the rescale, this wave's block of it), and the routing counts and the row's
-// sum of squares share one reduction, so the kernel costs about two memory round trips.
+// Every load that does not depend on another is issued before the first barrier, with no branch in between (the
+// route's id, all ids for the position, the token row for the rescale, this wave's block of it; the loads that need
+// the expert follow with clamped indices), and the routing counts and the row's sum of squares share one
+// reduction, so the kernel costs about two memory round trips. XD = the input's element type.
+template <int XD>
+__device__ __forceinline__ float load_x_t(const void* x, size_t i)
+{
+    if constexpr (XD == MM_DTYPE_F16) return h2f(static_cast<const uint16_t*>(x)[i]);
+    if constexpr (XD == MM_DTYPE_BF16) return __uint_as_float((uint32_t) static_cast<const uint16_t*>(x)[i] << 16);
+    return static_cast<const float*>(x)[i];
+}
+
+template <int XD>
 __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
 {
     __shared__ uint32_t s_bm[32];
@@ -71,42 +81,47 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
     const int t = s / a.topk;
     const size_t row = (size_t)t * a.H;
     const int h0 = blk * PREP_ROWS + wave * 128;
-    float va = 0.f, vb = 0.f, ss = 0.f;
-    if (h0 < a.H)
-    {
-        va = load_x(a.x, a.x_dtype, row + h0 + lane);
-        vb = load_x(a.x, a.x_dtype, row + h0 + lane + 64);
-    }
+    const int hc = h0 < a.H ? h0 : 0;           // a block in range for the loads (h0 is wave-uniform)
+    float va = load_x_t<XD>(a.x, row + hc + lane), vb = load_x_t<XD>(a.x, row + hc + lane + 64), ss = 0.f;
+    // the ids for the in-kernel routing (at most GV_ROUTE_MAX = 4 x 256 routes; indices past n reload id n - 1)
+    int64_t rid[GV_ROUTE_MAX / 256];
+#pragma unroll
+    for (int k = 0; k < GV_ROUTE_MAX / 256; ++k) rid[k] = a.ids[min(tid + 256 * k, a.n - 1)];
     if (a.rescale)
         for (int h = tid; h < a.H; h += 256)
         {
-            const float v = load_x(a.x, a.x_dtype, row + h);
+            const float v = load_x_t<XD>(a.x, row + h);
             ss = fmaf(v, v, ss);
         }
     const bool valid = perm ? idx < nvalid_perm : (e64 >= 0 && e64 < a.E);
     const int e = valid ? (int)e64 : -1;
-    float sa = 0.f, sb = 0.f;
-    if (valid && h0 < a.H)
+    const int ec = valid ? e : 0;               // an expert in range for the loads
+    const uint16_t* su = a.suh13 + ((size_t)ec * 2 + m) * a.H;
+    const float sa = h2f(su[hc + lane]), sb = h2f(su[hc + lane + 64]);
+    // the record's matrix addresses, loaded by the thread that may write it
+    int64_t wt0 = 0, wt1 = 0, wt2 = 0;
+    if (tid == 0 && writer && valid)
     {
-        const uint16_t* su = a.suh13 + ((size_t)e * 2 + m) * a.H;
-        sa = h2f(su[h0 + lane]);
-        sb = h2f(su[h0 + lane + 64]);
+        wt0 = a.wtab0[e];
+        wt1 = a.wtab1[e];
+        wt2 = a.wtab2[e];
     }
     if (tid < 32) s_bm[tid] = 0;
     __syncthreads();
     // in-kernel routing: position = routes of lower experts + earlier routes of the same expert
     int less = 0, same = 0, rank = 0, nv = 0;
-    if (!perm)
-        for (int i = tid; i < a.n; i += 256)
-        {
-            const int64_t v = a.ids[i];
-            if (v < 0 || v >= a.E) continue;
-            atomicOr(&s_bm[v >> 5], 1u << (v & 31));
-            nv += 1;
-            less += v < e;
-            same += v == e;
-            rank += (v == e) && (i < s);
-        }
+#pragma unroll
+    for (int k = 0; k < GV_ROUTE_MAX / 256; ++k)
+    {
+        const int64_t v = rid[k];
+        const int i = tid + 256 * k;
+        if (perm || i >= a.n || v < 0 || v >= a.E) continue;
+        atomicOr(&s_bm[v >> 5], 1u << (v & 31));
+        nv += 1;
+        less += v < e;
+        same += v == e;
+        rank += (v == e) && (i < s);
+    }
     less = wave_sum_int(less);
     same = wave_sum_int(same);
     rank = wave_sum_int(rank);
@@ -162,7 +177,7 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
                 }
                 if (ai >= 0)
                 {
-                    ExpertRec r{ e, cnt, pos, 0, { a.wtab0[e], a.wtab1[e], a.wtab2[e] }, 0 };
+                    ExpertRec r{ e, cnt, pos, 0, { wt0, wt1, wt2 }, 0 };
                     a.rec[ai] = r;
                 }
             }
@@ -182,7 +197,7 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
     float bsum = 0.0f;
     if (h0 < a.H)
     {
-        if (!(a.x_dtype == MM_DTYPE_F16 && !a.rescale))
+        if (!(XD == MM_DTYPE_F16 && !a.rescale))
         {
             va = r16(bf16_value(va * scale));
             vb = r16(bf16_value(vb * scale));
@@ -336,6 +351,52 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
 
 // ------------------------------------------------------------------------------------ 3. gate/up epilogue
 
+// For each of NS streams i: a[i] += p[i][q * stride + lane], b[i] += p[i][q * stride + lane + 64] for
+// q = 0 .. np - 1 in ascending q. Eight pieces of every stream are loaded before any is added (pieces past np
+// reload piece np - 1 and are not added), so a short count costs one memory round trip instead of one per piece.
+template <int NS>
+__device__ __forceinline__ void sum_pieces(const float* const (&p)[NS], size_t stride, int np, int lane, float (&a)[NS],
+                                           float (&b)[NS])
+{
+    for (int q0 = 0; q0 < np; q0 += 8)
+    {
+        float va[NS][8], vb[NS][8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+#pragma unroll
+            for (int i = 0; i < NS; ++i)
+            {
+                const float* pk = p[i] + (size_t)min(q0 + k, np - 1) * stride;
+                va[i][k] = pk[lane];
+                vb[i][k] = pk[lane + 64];
+            }
+#pragma unroll
+        for (int k = 0; k < 8; ++k)
+            if (q0 + k < np)
+#pragma unroll
+                for (int i = 0; i < NS; ++i)
+                {
+                    a[i] += va[i][k];
+                    b[i] += vb[i][k];
+                }
+    }
+}
+
+// Sum of p[0 .. count) by one wave, split so its first load shares a round trip with the loads after it:
+// wave_sum_first loads lane's first element (0 past count) without using it; wave_sum_rest adds the lane's
+// elements lane + 64, lane + 128, ... and reduces over the wave in a fixed order.
+__device__ __forceinline__ float wave_sum_first(const float* p, int count, int lane)
+{
+    return p[min(lane, count - 1)];      // count >= 1; lanes past count are zeroed by wave_sum_rest
+}
+__device__ __forceinline__ float wave_sum_rest(const float* p, int count, int lane, float first)
+{
+    asm volatile("" : "+v"(first));      // first used here, not where it was loaded
+    float v = lane < count ? 0.0f + first : 0.0f;
+    for (int i = lane + 64; i < count; i += 64) v += p[i];
+    return wave_sum(v);
+}
+
 struct GuEpiArgs
 {
     const float* part;        // [pieces][n][2][I]
@@ -358,39 +419,46 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int ncb = a.I / GV_COLS;
     const int pos = item / ncb, cb = item % ncb;
-    if (pos >= a.counts[1]) return;
-    const int pps = pieces_per_segment(a.nwaves, a.counts[0] * 2 * ncb, a.cap);
-    const int e = a.e_at[pos];
+    // round trip 1: the counts and the position's expert (read before the range check: only the last
+    // workgroup's spare waves are past n, and they read position n - 1)
+    const int nvalid = a.counts[1], nact = a.counts[0];
+    const int e = a.e_at[min(pos, a.n - 1)];
+    if (pos >= nvalid) return;
+    const int pps = pieces_per_segment(a.nwaves, nact * 2 * ncb, a.cap);
     const int c = cb * GV_COLS;
-    float ga = 0.f, gb = 0.f, ua = 0.f, ub = 0.f;
-#pragma unroll 8
-    for (int q = 0; q < pps; ++q)
-    {
-        const float* pg = a.part + (((size_t)q * a.n + pos) * 2 + 0) * a.I + c;
-        const float* pu = a.part + (((size_t)q * a.n + pos) * 2 + 1) * a.I + c;
-        ga += pg[lane];
-        gb += pg[lane + 64];
-        ua += pu[lane];
-        ub += pu[lane + 64];
-    }
+    // round trip 2: scales, input sums and partial sums
+    const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c;
+    const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c;
+    const uint16_t* sd = a.suh2 + (size_t)e * a.I + c;
+    const float sga = h2f(svg[lane]), sgb = h2f(svg[lane + 64]), sua = h2f(svu[lane]), sub = h2f(svu[lane + 64]);
+    const float sda = h2f(sd[lane]), sdb = h2f(sd[lane + 64]);
+    const float* xsg = a.xsum + ((size_t)pos * 2 + 0) * a.nb;
+    const float* xsu = a.xsum + ((size_t)pos * 2 + 1) * a.nb;
+    float sg = 0.f, su = 0.f;
     if (a.affine)
     {
-        const float sg = wave_sum_of(a.xsum + ((size_t)pos * 2 + 0) * a.nb, a.nb);
-        const float su = wave_sum_of(a.xsum + ((size_t)pos * 2 + 1) * a.nb, a.nb);
+        sg = wave_sum_first(xsg, a.nb, lane);
+        su = wave_sum_first(xsu, a.nb, lane);
+    }
+    const float* const pgu[2] = { a.part + ((size_t)pos * 2 + 0) * a.I + c, a.part + ((size_t)pos * 2 + 1) * a.I + c };
+    float s0[2] = { 0.f, 0.f }, s1[2] = { 0.f, 0.f };
+    sum_pieces<2>(pgu, (size_t)a.n * 2 * a.I, pps, lane, s0, s1);
+    float ga = s0[0], gb = s1[0], ua = s0[1], ub = s1[1];
+    if (a.affine)
+    {
+        sg = wave_sum_rest(xsg, a.nb, lane, sg);
+        su = wave_sum_rest(xsu, a.nb, lane, su);
         const float ki = kinv_f(), kb = kbias_f();
         ga = fmaf(ki, ga, kb * sg);
         gb = fmaf(ki, gb, kb * sg);
         ua = fmaf(ki, ua, kb * su);
         ub = fmaf(ki, ub, kb * su);
     }
-    const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c;
-    const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c;
-    out_block_wave(ga, gb, h2f(svg[lane]), h2f(svg[lane + 64]));
-    out_block_wave(ua, ub, h2f(svu[lane]), h2f(svu[lane + 64]));
+    out_block_wave(ga, gb, sga, sgb);
+    out_block_wave(ua, ub, sua, sub);
     float xa = r16(act_gu(ga, ua, a.limit));
     float xb = r16(act_gu(gb, ub, a.limit));
-    const uint16_t* sd = a.suh2 + (size_t)e * a.I + c;
-    prep_block_wave(xa, xb, h2f(sd[lane]), h2f(sd[lane + 64]));
+    prep_block_wave(xa, xb, sda, sdb);
     uint16_t* dst = a.xd + (size_t)pos * a.I;
     dst[operand_index(c + lane)] = f2h(xa);
     dst[operand_index(c + lane + 64)] = f2h(xb);
@@ -407,6 +475,7 @@ struct DEpiArgs
     const int32_t* counts;
     const int32_t* pos_of;
     const int32_t* route_at;
+    const int32_t* e_at;
     const int64_t* ids;
     const float* w;           // route weights (combine)
     const uint16_t* svh2;     // [E][H]
@@ -417,27 +486,29 @@ struct DEpiArgs
 
 // Down output of one (sorted position, 128-column block of H): row ranges added in order (then the AFFINE
 // fixup), output transform.
-__device__ __forceinline__ void down_block(const DEpiArgs& a, int pos, int c, int64_t e, int lane, float& ya, float& yb)
+// nact = active experts (counts[0]), read by the caller with its other first loads; the scales, input sums and
+// partial sums then share one round trip.
+__device__ __forceinline__ void down_block(const DEpiArgs& a, int nact, int pos, int c, int64_t e, int lane, float& ya,
+                                           float& yb)
 {
-    const int pps = pieces_per_segment(a.nwaves, a.counts[0] * (a.H / GV_COLS), a.cap);
-    ya = 0.f;
-    yb = 0.f;
-#pragma unroll 8
-    for (int q = 0; q < pps; ++q)
-    {
-        const float* pd = a.part + ((size_t)q * a.n + pos) * a.H + c;
-        ya += pd[lane];
-        yb += pd[lane + 64];
-    }
+    const int pps = pieces_per_segment(a.nwaves, nact * (a.H / GV_COLS), a.cap);
+    const uint16_t* sv = a.svh2 + (size_t)e * a.H + c;
+    const float sva = h2f(sv[lane]), svb = h2f(sv[lane + 64]);
+    const float* xs = a.xdsum + (size_t)pos * (a.I / GV_COLS);
+    float sx = a.affine ? wave_sum_first(xs, a.I / GV_COLS, lane) : 0.f;
+    const float* const pd[1] = { a.part + (size_t)pos * a.H + c };
+    float s0[1] = { 0.f }, s1[1] = { 0.f };
+    sum_pieces<1>(pd, (size_t)a.n * a.H, pps, lane, s0, s1);
+    ya = s0[0];
+    yb = s1[0];
     if (a.affine)
     {
-        const float sx = wave_sum_of(a.xdsum + (size_t)pos * (a.I / GV_COLS), a.I / GV_COLS);
+        sx = wave_sum_rest(xs, a.I / GV_COLS, lane, sx);
         const float ki = kinv_f(), kb = kbias_f();
         ya = fmaf(ki, ya, kb * sx);
         yb = fmaf(ki, yb, kb * sx);
     }
-    const uint16_t* sv = a.svh2 + (size_t)e * a.H + c;
-    out_block_wave(ya, yb, h2f(sv[lane]), h2f(sv[lane + 64]));
+    out_block_wave(ya, yb, sva, svb);
 }
 
 // Per-route rows: Y[s] for every routed s.
@@ -447,11 +518,13 @@ __global__ __launch_bounds__(256) void k_down_y(DEpiArgs a)
     const int item = blockIdx.x * 4 + (threadIdx.x >> 6);
     const int ncb = a.H / GV_COLS;
     const int pos = item / ncb, cb = item % ncb;
-    if (pos >= a.counts[1]) return;
-    const int s = a.route_at[pos];
+    const int nvalid = a.counts[1], nact = a.counts[0];
+    const int pc = min(pos, a.n - 1);
+    const int s = a.route_at[pc], e = a.e_at[pc];
+    if (pos >= nvalid) return;
     const int c = cb * GV_COLS;
     float ya, yb;
-    down_block(a, pos, c, a.ids[s], lane, ya, yb);
+    down_block(a, nact, pos, c, e, lane, ya, yb);
     a.Y[(size_t)s * a.H + c + lane] = ya;
     a.Y[(size_t)s * a.H + c + lane + 64] = yb;
 }
@@ -462,29 +535,37 @@ __global__ __launch_bounds__(256) void k_down_y(DEpiArgs a)
 __global__ __launch_bounds__(1024) void k_down_combine(DEpiArgs a)
 {
     __shared__ float ys[MAX_TOPK][GV_COLS];
+    __shared__ float wj[MAX_TOPK];
     __shared__ int ok[MAX_TOPK];
     const int lane = threadIdx.x & 63, j = threadIdx.x >> 6;
     const int ncb = a.H / GV_COLS;
     const int t = blockIdx.x / ncb, c = (blockIdx.x % ncb) * GV_COLS;
     if (j < a.topk)
     {
+        // round trip 1: the route's position, expert and weight and the active-expert count. A pick outside
+        // [0, E) (position -1) is computed on position 0 and expert 0 and left out of the sum, so no branch keeps
+        // the expert's load from being issued with the others.
         const int s = t * a.topk + j;
         const int pos = a.pos_of[s];
-        if (pos >= 0)
+        const int64_t e = a.ids[s];
+        const float wt = a.w[s];
+        const int nact = a.counts[0];
+        float ya, yb;
+        down_block(a, nact, max(pos, 0), c, pos >= 0 ? e : 0, lane, ya, yb);
+        ys[j][lane] = ya;
+        ys[j][lane + 64] = yb;
+        if (lane == 0)
         {
-            float ya, yb;
-            down_block(a, pos, c, a.ids[s], lane, ya, yb);
-            ys[j][lane] = ya;
-            ys[j][lane + 64] = yb;
+            ok[j] = pos >= 0;
+            wj[j] = wt;
         }
-        if (lane == 0) ok[j] = pos >= 0;
     }
     __syncthreads();
     for (int h = threadIdx.x; h < GV_COLS; h += blockDim.x)
     {
         float o = 0.0f;
         for (int jj = 0; jj < a.topk; ++jj)
-            if (ok[jj]) o = fmaf(a.w[t * a.topk + jj], ys[jj][h], o);
+            if (ok[jj]) o = fmaf(wj[jj], ys[jj][h], o);
         a.out[(size_t)t * a.H + c + h] = o;
     }
 }
@@ -511,7 +592,13 @@ int prep_blocks(int H) { return (H + PREP_ROWS - 1) / PREP_ROWS; }
 
 void launch_route_prep(const PrepArgs& p, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_route_prep, dim3(2 * p.n * p.nb), dim3(256), 0, s, p);
+    const dim3 grid(2 * p.n * p.nb), block(256);
+    if (p.x_dtype == MM_DTYPE_F16)
+        hipLaunchKernelGGL(k_route_prep<MM_DTYPE_F16>, grid, block, 0, s, p);
+    else if (p.x_dtype == MM_DTYPE_BF16)
+        hipLaunchKernelGGL(k_route_prep<MM_DTYPE_BF16>, grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL(k_route_prep<MM_DTYPE_F32>, grid, block, 0, s, p);
 }
 
 // Most row ranges per segment a partial launch may use: bounded so the partial sums stay a few MB.
@@ -615,7 +702,7 @@ static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int n, hipStrea
 static DEpiArgs down_args(const mm_layer_t* L, const Ws& w, int n, int topk, const int64_t* ids, const float* wt,
                           float* Y, float* out)
 {
-    return DEpiArgs{ w.part_d, w.xdsum, w.counts, w.pos_of, w.route_at, ids, wt, L->svh2, Y, out, n, L->H, L->I, topk,
+    return DEpiArgs{ w.part_d, w.xdsum, w.counts, w.pos_of, w.route_at, w.e_at, ids, wt, L->svh2, Y, out, n, L->H, L->I, topk,
                      partial_waves(), piece_cap(n), (L->flags & MM_LAYER_EXACT) ? 0 : 1 };
 }
 
