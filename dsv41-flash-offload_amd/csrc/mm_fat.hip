@@ -19,6 +19,7 @@
 // between its v_mfma_f32_16x16x32_f16 over a (BM / 2) x 64 sub-tile (128 accumulators per lane), so one wave's
 // decode runs while the other wave of its SIMD multiplies. The weights are decoded once per tile.
 #include <algorithm>
+#include <type_traits>
 
 #include "mm_decode.h"
 
@@ -132,50 +133,71 @@ __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e,
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane & 3, q = (lane >> 2) & 3, bl = lane >> 4;
-    const int m = wave >> 1, nb = H / 128;
+    const int m = wave >> 1, nbh = H / 256, b0 = (wave & 1) * nbh;
     const Lane8Signs sg = lane8_signs(lane);
     const uint16_t* su = suh13 + ((size_t)e * 2 + m) * H;
     uint16_t* dst = xa + (size_t)pos * 2 * H + m * 32 + 8 * g;
-    for (int b = (wave & 1) * (nb / 2) + bl; b < ((wave & 1) + 1) * (nb / 2); b += 4)
+    // raw words of element pair (t, h): fp16 / bf16 input as one dword, fp32 as two
+    using Raw = typename std::conditional<XD == MM_DTYPE_F32, uint2, uint32_t>::type;
+    // lane group bl takes blocks b0 + bl, + 4, ...: four of them per pass, all loaded before any is used (blocks
+    // past the wave's half reload its last block and are not stored)
+    for (int bb = bl; bb < nbh; bb += 16)
     {
-        const int k0 = b * 128 + 32 * q + 2 * g;
-        float v[8];
+        Raw xr[4][4];
+        uint32_t sr[4][4];
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
+        for (int it = 0; it < 4; ++it)
+        {
+            const int k0 = (b0 + min(bb + 4 * it, nbh - 1)) * 128 + 32 * q + 2 * g;
 #pragma unroll
-            for (int h = 0; h < 2; ++h)
+            for (int th = 0; th < 4; ++th)
             {
-                const int k = k0 + 8 * h + 16 * t;
+                const int k = k0 + 8 * (th & 1) + 16 * (th >> 1);
+                if constexpr (XD == MM_DTYPE_F32)
+                    xr[it][th] = *reinterpret_cast<const uint2*>(static_cast<const float*>(x) + row + k);
+                else
+                    xr[it][th] = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + row + k);
+                sr[it][th] = *reinterpret_cast<const uint32_t*>(su + k);
+            }
+        }
+#pragma unroll
+        for (int it = 0; it < 4; ++it)
+        {
+            const int b = bb + 4 * it;
+            if (b >= nbh) break;
+            float v[8];
+#pragma unroll
+            for (int th = 0; th < 4; ++th)
+            {
+                // th = 2 t + h: elements 8 h + 16 t (+ 0, 1) of the lane's column pair, v[4 t + 2 h + j]
                 float x0, x1;
                 if constexpr (XD == MM_DTYPE_F16)
                 {
-                    const uint32_t d = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + row + k);
-                    x0 = h2f((uint16_t)(d & 0xffffu));
-                    x1 = h2f((uint16_t)(d >> 16));
+                    x0 = h2f((uint16_t)(xr[it][th] & 0xffffu));
+                    x1 = h2f((uint16_t)(xr[it][th] >> 16));
                 }
                 else if constexpr (XD == MM_DTYPE_BF16)
                 {
-                    const uint32_t d = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + row + k);
-                    x0 = r16(__uint_as_float(d << 16));
-                    x1 = r16(__uint_as_float(d & 0xffff0000u));
+                    x0 = r16(__uint_as_float(xr[it][th] << 16));
+                    x1 = r16(__uint_as_float(xr[it][th] & 0xffff0000u));
                 }
                 else
                 {
-                    const float2 f = *reinterpret_cast<const float2*>(static_cast<const float*>(x) + row + k);
-                    x0 = r16(bf16_value(f.x));
-                    x1 = r16(bf16_value(f.y));
+                    x0 = r16(bf16_value(__uint_as_float(xr[it][th].x)));
+                    x1 = r16(bf16_value(__uint_as_float(xr[it][th].y)));
                 }
-                const uint32_t sd = *reinterpret_cast<const uint32_t*>(su + k);
-                v[4 * t + 2 * h] = x0 * h2f((uint16_t)(sd & 0xffffu));
-                v[4 * t + 2 * h + 1] = x1 * h2f((uint16_t)(sd >> 16));
+                const int i = 4 * (th >> 1) + 2 * (th & 1);
+                v[i] = x0 * h2f((uint16_t)(sr[it][th] & 0xffffu));
+                v[i + 1] = x1 * h2f((uint16_t)(sr[it][th] >> 16));
             }
-        fwht128_lane8(v, sg);
-        uint4 o;
-        o.x = (uint32_t)f2h(v[0] * HAD) | ((uint32_t)f2h(v[1] * HAD) << 16);
-        o.y = (uint32_t)f2h(v[2] * HAD) | ((uint32_t)f2h(v[3] * HAD) << 16);
-        o.z = (uint32_t)f2h(v[4] * HAD) | ((uint32_t)f2h(v[5] * HAD) << 16);
-        o.w = (uint32_t)f2h(v[6] * HAD) | ((uint32_t)f2h(v[7] * HAD) << 16);
-        *reinterpret_cast<uint4*>(dst + (size_t)(4 * b + q) * 64) = o;
+            fwht128_lane8(v, sg);
+            uint4 o;
+            o.x = (uint32_t)f2h(v[0] * HAD) | ((uint32_t)f2h(v[1] * HAD) << 16);
+            o.y = (uint32_t)f2h(v[2] * HAD) | ((uint32_t)f2h(v[3] * HAD) << 16);
+            o.z = (uint32_t)f2h(v[4] * HAD) | ((uint32_t)f2h(v[5] * HAD) << 16);
+            o.w = (uint32_t)f2h(v[6] * HAD) | ((uint32_t)f2h(v[7] * HAD) << 16);
+            *reinterpret_cast<uint4*>(dst + (size_t)(4 * (b0 + b) + q) * 64) = o;
+        }
     }
 }
 
