@@ -134,6 +134,11 @@ __device__ __forceinline__ float act_gu(float g, float u, float limit)
 int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
+// The permutation behind mm_permute; e_sorted (optional, [n]) receives the expert bin of each sorted position.
+int permute_launch(const int64_t* ids, const float* w, int n, int topk, int E, int32_t* counts, int32_t* offsets,
+                   int32_t* order, int32_t* token_sorted, float* weight_sorted, int32_t* inv_order, int32_t* active,
+                   int32_t* nactive, int32_t* e_sorted, void* workspace, size_t workspace_bytes, mm_stream_t stream);
+
 }  // namespace mm
 
 #define MM_CHECK_ARG(cond, ...) \

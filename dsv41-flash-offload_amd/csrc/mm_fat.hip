@@ -128,9 +128,12 @@ __device__ __forceinline__ int lane8_k(int lane, int i)
 }
 
 template <int XD>
+// cnt_e (optional): the expert's route count, read with the row and compared only before the stores (rows of
+// experts with cnt_e[0] <= cap are not stored), so it costs no round trip of its own.
 __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e, int pos, const uint16_t* suh13,
-                                               uint16_t* xa, int H)
+                                               uint16_t* xa, int H, const int32_t* cnt_e, int cap)
 {
+    int ce = cnt_e ? cnt_e[0] : cap + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane & 3, q = (lane >> 2) & 3, bl = lane >> 4;
     const int m = wave >> 1, nbh = H / 256, b0 = (wave & 1) * nbh;
@@ -160,6 +163,8 @@ __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e,
                 sr[it][th] = *reinterpret_cast<const uint32_t*>(su + k);
             }
         }
+        asm volatile("" : "+v"(ce));       // the count is first used here, after the row's loads
+        if (ce <= cap) return;
 #pragma unroll
         for (int it = 0; it < 4; ++it)
         {
@@ -202,26 +207,27 @@ __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e,
 }
 
 __device__ __forceinline__ void fat_prep_row(const void* x, int x_dtype, size_t row, int e, int pos,
-                                             const uint16_t* suh13, uint16_t* xa, int H)
+                                             const uint16_t* suh13, uint16_t* xa, int H, const int32_t* cnt_e, int cap)
 {
     if (x_dtype == MM_DTYPE_F16)
-        fat_prep_row_t<MM_DTYPE_F16>(x, row, e, pos, suh13, xa, H);
+        fat_prep_row_t<MM_DTYPE_F16>(x, row, e, pos, suh13, xa, H, cnt_e, cap);
     else if (x_dtype == MM_DTYPE_BF16)
-        fat_prep_row_t<MM_DTYPE_BF16>(x, row, e, pos, suh13, xa, H);
+        fat_prep_row_t<MM_DTYPE_BF16>(x, row, e, pos, suh13, xa, H, cnt_e, cap);
     else
-        fat_prep_row_t<MM_DTYPE_F32>(x, row, e, pos, suh13, xa, H);
+        fat_prep_row_t<MM_DTYPE_F32>(x, row, e, pos, suh13, xa, H, cnt_e, cap);
 }
 
-__global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, const int64_t* ids, const int32_t* counts,
-                                                  const int32_t* offsets, const int32_t* order, const uint16_t* suh13,
-                                                  uint16_t* xa, int topk, int E, int H, int cap)
+__global__ __launch_bounds__(256) void k_fat_prep(const void* x, int x_dtype, const int32_t* e_sorted,
+                                                  const int32_t* counts, const int32_t* offsets, const int32_t* order,
+                                                  const uint16_t* suh13, uint16_t* xa, int topk, int E, int H, int cap)
 {
     const int pos = blockIdx.x;
-    if (pos >= offsets[E]) return;
-    const int s = order[pos];
-    const int e = (int)ids[s];
-    if (counts[e] <= cap) return;
-    fat_prep_row(x, x_dtype, (size_t)(s / topk) * H, e, pos, suh13, xa, H);
+    // round trip 1: the routed count, the route and its expert (pos < n: in range past the routed count too)
+    const int nvalid = offsets[E];
+    const int s = order[pos], e = e_sorted[pos];
+    if (pos >= nvalid || (s | e) < 0) return;        // s, e >= 0: the test only keeps their loads before the branch
+    // round trip 2: the expert's route count with the row's loads; rows of experts at or below cap are not stored
+    fat_prep_row(x, x_dtype, (size_t)(s / topk) * H, e, pos, suh13, xa, H, counts + e, cap);
 }
 
 // Sorted-route form: position pos belongs to the expert e with offsets[e] <= pos < offsets[e + 1] (binary search
@@ -243,7 +249,7 @@ __global__ __launch_bounds__(256) void k_fatb_prep(const void* x, int x_dtype, c
     if (counts[e] <= 0 || pos >= offsets[e] + counts[e]) return;
     const int64_t t = token_sorted[pos];
     if (t < 0 || t >= T) return;
-    fat_prep_row(x, x_dtype, (size_t)t * H, e, pos, suh13, xa, H);
+    fat_prep_row(x, x_dtype, (size_t)t * H, e, pos, suh13, xa, H, nullptr, 0);
 }
 
 // Expert records and the tile lists of the experts with more than cap routes. An expert of c routes gets
@@ -837,6 +843,7 @@ struct FatWs
     uint16_t* xa;         // [n][2][H]
     uint16_t* xd;         // [n][I]
     float* Y;             // [n][H]
+    int32_t* e_sorted;    // [n] expert bin of each sorted position
     size_t bytes;
 };
 
@@ -845,10 +852,11 @@ static FatWs fat_carve(void* base, int n, int E, int H, int I)
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t na = (size_t)(n < E ? n : E);
     const size_t pwsb = mm_permute_workspace(n, E);
-    constexpr int NS = 12;
+    constexpr int NS = 13;
     const size_t sizes[NS] = { al((size_t)(E + 1) * 4), al((size_t)(E + 2) * 4), al((size_t)n * 4), al((size_t)E * 4),
                                al(4), al(pwsb), al(na * sizeof(ExpertRec)), al((na + 1) * 4), al((na + 1) * 4),
-                               al((size_t)n * 2 * H * 2), al((size_t)n * I * 2), al((size_t)n * H * 4) };
+                               al((size_t)n * 2 * H * 2), al((size_t)n * I * 2), al((size_t)n * H * 4),
+                               al((size_t)n * 4) };
     char* p = static_cast<char*>(base);
     char* at[NS];
     size_t off = 0;
@@ -861,7 +869,7 @@ static FatWs fat_carve(void* base, int n, int E, int H, int I)
     w.counts = (int32_t*)at[0]; w.offsets = (int32_t*)at[1]; w.order = (int32_t*)at[2]; w.active = (int32_t*)at[3];
     w.nactive = (int32_t*)at[4]; w.pws = at[5]; w.pws_bytes = pwsb; w.rec = (ExpertRec*)at[6];
     w.off_big = (int32_t*)at[7]; w.off_small = (int32_t*)at[8]; w.xa = (uint16_t*)at[9]; w.xd = (uint16_t*)at[10];
-    w.Y = (float*)at[11];
+    w.Y = (float*)at[11]; w.e_sorted = (int32_t*)at[12];
     w.bytes = off;
     return w;
 }
@@ -923,11 +931,11 @@ static int fat_run(const mm_layer_t* L, const void* x, int x_dtype, int T, int t
                    const FatWs& ws, hipStream_t s, bool yh)
 {
     const int n = T * topk, E = L->E;
-    int rc = mm_permute(ids, nullptr, n, topk, E, ws.counts, ws.offsets, ws.order, nullptr, nullptr, nullptr, ws.active,
-                        ws.nactive, ws.pws, ws.pws_bytes, s);
+    int rc = permute_launch(ids, nullptr, n, topk, E, ws.counts, ws.offsets, ws.order, nullptr, nullptr, nullptr,
+                            ws.active, ws.nactive, ws.e_sorted, ws.pws, ws.pws_bytes, s);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_fat_prep, dim3(n), dim3(256), 0, s, x, x_dtype, ids, ws.counts, ws.offsets, ws.order, L->suh13,
-                       ws.xa, topk, E, L->H, cap);
+    hipLaunchKernelGGL(k_fat_prep, dim3(n), dim3(256), 0, s, x, x_dtype, ws.e_sorted, ws.counts, ws.offsets, ws.order,
+                       L->suh13, ws.xa, topk, E, L->H, cap);
     return fat_gemms(L, n, cap, ws, s, yh);
 }
 

@@ -382,7 +382,8 @@ __device__ __forceinline__ int route_bin(const int64_t* ids, int s, int E)
 
 // Scatter routes [lo, hi) in order; fill[] (LDS) holds the next free sorted position of every bin.
 __device__ void scatter_chunk(const int64_t* ids, const float* w, int lo, int hi, int topk, int E, int* fill,
-                              int32_t* order, int32_t* token_sorted, float* weight_sorted, int32_t* inv_order)
+                              int32_t* order, int32_t* token_sorted, float* weight_sorted, int32_t* inv_order,
+                              int32_t* e_sorted)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     for (int base = lo; base < hi; base += blockDim.x)
@@ -411,6 +412,7 @@ __device__ void scatter_chunk(const int64_t* ids, const float* w, int lo, int hi
             if (token_sorted) token_sorted[pos] = s / topk;
             if (weight_sorted && w) weight_sorted[pos] = w[s];
             if (inv_order) inv_order[s] = pos;
+            if (e_sorted) e_sorted[pos] = e;
         }
         (void)lane;
     }
@@ -434,7 +436,7 @@ __device__ void write_active(const int* cnt, int E, int32_t* active, int32_t* na
 
 __global__ __launch_bounds__(PERM_THREADS) void k_permute_single(const int64_t* __restrict__ ids, const float* __restrict__ w,
     int n, int topk, int E, int32_t* counts, int32_t* offsets, int32_t* order, int32_t* token_sorted,
-    float* weight_sorted, int32_t* inv_order, int32_t* active, int32_t* nactive)
+    float* weight_sorted, int32_t* inv_order, int32_t* active, int32_t* nactive, int32_t* e_sorted)
 {
     __shared__ int cnt[1025 + 1];
     __shared__ int fill[1025 + 1];
@@ -462,7 +464,7 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute_single(const int64_t* 
     if (threadIdx.x == 0) offsets[nb] = run;
     write_active(cnt, E, active, nactive, scan_tmp);
     __syncthreads();
-    scatter_chunk(ids, w, 0, n, topk, E, fill, order, token_sorted, weight_sorted, inv_order);
+    scatter_chunk(ids, w, 0, n, topk, E, fill, order, token_sorted, weight_sorted, inv_order, e_sorted);
 }
 
 // Multi-block path: per-block bin histograms (bin-major), one-block scan, then per-block stable scatter.
@@ -514,14 +516,14 @@ __global__ __launch_bounds__(PERM_THREADS) void k_permute_scan(int32_t* hist, in
 
 __global__ __launch_bounds__(PERM_THREADS) void k_permute_scatter(const int64_t* __restrict__ ids, const float* __restrict__ w,
     int n, int topk, int E, int chunk, const int32_t* __restrict__ hist, int32_t* order, int32_t* token_sorted,
-    float* weight_sorted, int32_t* inv_order)
+    float* weight_sorted, int32_t* inv_order, int32_t* e_sorted)
 {
     __shared__ int fill[1025 + 1];
     const int nb = E + 1, B = gridDim.x, b = blockIdx.x;
     for (int e = threadIdx.x; e < nb; e += blockDim.x) fill[e] = hist[(size_t)e * B + b];
     __syncthreads();
     const int lo = b * chunk, hi = min(n, lo + chunk);
-    scatter_chunk(ids, w, lo, hi, topk, E, fill, order, token_sorted, weight_sorted, inv_order);
+    scatter_chunk(ids, w, lo, hi, topk, E, fill, order, token_sorted, weight_sorted, inv_order, e_sorted);
 }
 
 // ---------------------------------------------------------------------------------------------------------
@@ -623,6 +625,36 @@ __global__ __launch_bounds__(256) void k_synth_layer(const int64_t* __restrict__
     }
 }
 
+// mm_permute's launches; e_sorted (optional, [n]) receives the expert bin of each sorted position.
+int permute_launch(const int64_t* ids, const float* w, int n, int topk, int E, int32_t* counts, int32_t* offsets,
+                   int32_t* order, int32_t* token_sorted, float* weight_sorted, int32_t* inv_order, int32_t* active,
+                   int32_t* nactive, int32_t* e_sorted, void* workspace, size_t workspace_bytes, mm_stream_t stream)
+{
+    MM_CHECK_ARG(E > 0 && E <= 1024, "mm_permute: E must be in [1, 1024] (E=%d)", E);
+    MM_CHECK_ARG(n >= 0 && topk > 0, "mm_permute: bad n/topk");
+    MM_CHECK_ARG(counts && offsets && (n == 0 || (ids && order)), "mm_permute: null pointer");
+    const size_t need = mm_permute_workspace(n, E);
+    MM_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace), "mm_permute: workspace too small (%zu < %zu)",
+                 workspace_bytes, need);
+    const hipStream_t hs = reinterpret_cast<hipStream_t>(stream);
+    if (n <= PERM_SINGLE_MAX)
+    {
+        hipLaunchKernelGGL(k_permute_single, dim3(1), dim3(PERM_THREADS), 0, hs, ids, w, n, topk, E, counts, offsets,
+                           order, token_sorted, weight_sorted, inv_order, active, nactive, e_sorted);
+    }
+    else
+    {
+        const int B = (n + PERM_CHUNK - 1) / PERM_CHUNK;
+        int32_t* hist = (int32_t*)workspace;
+        hipLaunchKernelGGL(k_permute_hist, dim3(B), dim3(PERM_THREADS), 0, hs, ids, n, E, PERM_CHUNK, hist);
+        hipLaunchKernelGGL(k_permute_scan, dim3(1), dim3(PERM_THREADS), 0, hs, hist, B, n, E, counts, offsets, active,
+                           nactive);
+        hipLaunchKernelGGL(k_permute_scatter, dim3(B), dim3(PERM_THREADS), 0, hs, ids, w, n, topk, E, PERM_CHUNK, hist,
+                           order, token_sorted, weight_sorted, inv_order, e_sorted);
+    }
+    return check_launch("mm_permute");
+}
+
 }  // namespace mm
 
 using namespace mm;
@@ -705,28 +737,8 @@ int mm_permute(const int64_t* ids, const float* w, int n, int topk, int E, int32
                int32_t* order, int32_t* token_sorted, float* weight_sorted, int32_t* inv_order, int32_t* active,
                int32_t* nactive, void* workspace, size_t workspace_bytes, mm_stream_t stream)
 {
-    MM_CHECK_ARG(E > 0 && E <= 1024, "mm_permute: E must be in [1, 1024] (E=%d)", E);
-    MM_CHECK_ARG(n >= 0 && topk > 0, "mm_permute: bad n/topk");
-    MM_CHECK_ARG(counts && offsets && (n == 0 || (ids && order)), "mm_permute: null pointer");
-    const size_t need = mm_permute_workspace(n, E);
-    MM_CHECK_ARG(workspace_bytes >= need && (need == 0 || workspace), "mm_permute: workspace too small (%zu < %zu)",
-                 workspace_bytes, need);
-    if (n <= PERM_SINGLE_MAX)
-    {
-        hipLaunchKernelGGL(k_permute_single, dim3(1), dim3(PERM_THREADS), 0, S(stream), ids, w, n, topk, E, counts, offsets,
-                           order, token_sorted, weight_sorted, inv_order, active, nactive);
-    }
-    else
-    {
-        const int B = (n + PERM_CHUNK - 1) / PERM_CHUNK;
-        int32_t* hist = (int32_t*)workspace;
-        hipLaunchKernelGGL(k_permute_hist, dim3(B), dim3(PERM_THREADS), 0, S(stream), ids, n, E, PERM_CHUNK, hist);
-        hipLaunchKernelGGL(k_permute_scan, dim3(1), dim3(PERM_THREADS), 0, S(stream), hist, B, n, E, counts, offsets, active,
-                           nactive);
-        hipLaunchKernelGGL(k_permute_scatter, dim3(B), dim3(PERM_THREADS), 0, S(stream), ids, w, n, topk, E, PERM_CHUNK, hist,
-                           order, token_sorted, weight_sorted, inv_order);
-    }
-    return check_launch("mm_permute");
+    return mm::permute_launch(ids, w, n, topk, E, counts, offsets, order, token_sorted, weight_sorted, inv_order, active,
+                              nactive, nullptr, workspace, workspace_bytes, stream);
 }
 
 int mm_combine(float* out, const float* Y, const int64_t* ids, const float* w, int T, int k, int H, int E, int accumulate,
