@@ -88,10 +88,15 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
 #pragma unroll
     for (int k = 0; k < GV_ROUTE_MAX / 256; ++k) rid[k] = a.ids[min(tid + 256 * k, a.n - 1)];
     if (a.rescale)
-        for (int h = tid; h < a.H; h += 256)
+        // the row's sum of squares, h = tid, tid + 256, ... in order; eight loads in flight before they are used
+        for (int hb = tid; hb < a.H; hb += 256 * 8)
         {
-            const float v = load_x_t<XD>(a.x, row + h);
-            ss = fmaf(v, v, ss);
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = load_x_t<XD>(a.x, row + min(hb + 256 * k, a.H - 1));
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (hb + 256 * k < a.H) ss = fmaf(v[k], v[k], ss);
         }
     const bool valid = perm ? idx < nvalid_perm : (e64 >= 0 && e64 < a.E);
     const int e = valid ? (int)e64 : -1;

@@ -564,8 +564,17 @@ __global__ __launch_bounds__(256) void k_prepare_input(const float* __restrict__
     float scale = 1.0f;
     if (rescale)
     {
+        // h = thread, + blockDim, ... in order; eight loads in flight before they are used
         float ss = 0.0f;
-        for (int h = threadIdx.x; h < H; h += blockDim.x) ss = fmaf(row[h], row[h], ss);
+        for (int hb = threadIdx.x; hb < H; hb += blockDim.x * 8)
+        {
+            float v[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) v[k] = row[min(hb + (int)blockDim.x * k, H - 1)];
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (hb + (int)blockDim.x * k < H) ss = fmaf(v[k], v[k], ss);
+        }
         ss += xor_lane<32>(ss);
         ss += xor_lane<16>(ss);
         ss += xor_lane<8>(ss);
