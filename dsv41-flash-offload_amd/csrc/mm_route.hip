@@ -190,7 +190,8 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
     __shared__ int s_nh, s_nm, s_best, s_publish, s_npk;
     __shared__ long long s_seq;
     const int t = threadIdx.x, E = a.E;
-    // every global input is loaded up front (one round trip): the slot table and scores into LDS
+    // every global input is loaded up front (one round trip): the slot table and scores into LDS, this thread's
+    // routes t + 256 k (the first SPT of them kept in registers), and the policy words and counters thread 0 uses
     for (int e = t; e < E; e += blockDim.x)
     {
         cnt[e] = 0;
@@ -198,16 +199,45 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
         s_slot[e] = a.slotof[e] >= 0 ? 1 : 0;
         s_score[e] = a.score[e];
     }
-    __syncthreads();
-    for (int s = t; s < a.n; s += blockDim.x)
+    constexpr int SPT = 4;
+    int64_t re[SPT];
+    float rw[SPT];
+#pragma unroll
+    for (int k = 0; k < SPT; ++k)
     {
-        const int64_t e = a.sel[s];
-        if (a.w[s] != 0.0f && e >= 0 && e < E)
+        re[k] = -1;
+        rw[k] = 0.0f;
+    }
+    if (a.n > 0)
+#pragma unroll
+        for (int k = 0; k < SPT; ++k)
+        {
+            const int s = min(t + 256 * k, a.n - 1);        // routes past n reload route n - 1 (not used)
+            re[k] = a.sel[s];
+            rw[k] = a.w[s];
+        }
+    float pol[9] = {};
+    int64_t st[4] = {}, sq = 0;
+    if (t == 0)
+    {
+#pragma unroll
+        for (int i = 0; i < 9; ++i) pol[i] = a.p[i];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) st[i] = a.stats[i];
+        sq = a.seqc[0];
+    }
+    __syncthreads();
+    auto count_route = [&](int64_t e, float wt) {
+        if (wt != 0.0f && e >= 0 && e < E)
         {
             atomicAdd(&cnt[e], 1);
             if (a.counts) atomicAdd(&a.counts[e], 1);
         }
-    }
+    };
+#pragma unroll
+    for (int k = 0; k < SPT; ++k)
+        if (t + 256 * k < a.n) count_route(re[k], rw[k]);
+    for (int s = t + 256 * SPT; s < a.n; s += 256) count_route(a.sel[s], a.w[s]);
     __syncthreads();
     // hit list and miss list in ascending expert id
     int nh = 0, nm = 0;
@@ -242,7 +272,7 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
     __syncthreads();
     if (t == 0)
     {
-        const float* p = a.p;
+        const float* p = pol;
         int best = 0;
         const int force = (int)p[6];
         const int maxc = min((int)p[5], nm);
@@ -260,8 +290,12 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
         }
         for (int k = 0; k < best; ++k) cpu[miss[k]] = 1;
         const int publish = best > 0 || p[7] > 0.5f;
-        a.stats[0] += nh; a.stats[1] += nm; a.stats[2] += best; a.stats[3] += 1;
-        s_seq = publish ? ++a.seqc[0] : 0;
+        a.stats[0] = st[0] + nh;
+        a.stats[1] = st[1] + nm;
+        a.stats[2] = st[2] + best;
+        a.stats[3] = st[3] + 1;
+        if (publish) a.seqc[0] = sq + 1;
+        s_seq = publish ? sq + 1 : 0;
         s_best = best;
         s_publish = publish;
         s_nh = nh;
@@ -274,16 +308,10 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
     const int publish = s_publish;
     // CPU picks in ascending route index, then the masked selection
     int npk = 0;
-    for (int base = 0; base < a.n; base += blockDim.x)
-    {
+    auto pick_pass = [&](int base, int64_t e, float wt) {
         const int s = base + t;
-        bool pick = false;
-        int64_t e = -1;
-        if (s < a.n)
-        {
-            e = a.sel[s];
-            pick = e >= 0 && e < E && cpu[e] && a.w[s] != 0.0f;
-        }
+        const bool in = s < a.n;
+        const bool pick = in && e >= 0 && e < E && cpu[e] && wt != 0.0f;
         int tot;
         const int pos = block_scan_excl(pick ? 1 : 0, scan_tmp, &tot);
         if (publish && pick)
@@ -291,15 +319,23 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
             int32_t* hp = a.hpicks + (size_t)(npk + pos) * 3;
             __hip_atomic_store(hp + 0, s / a.topk, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
             __hip_atomic_store(hp + 1, (int32_t)e, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
-            __hip_atomic_store(hp + 2, __float_as_int(a.w[s]), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+            __hip_atomic_store(hp + 2, __float_as_int(wt), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
         }
         npk += tot;
-        if (s < a.n)
+        if (in)
         {
             const bool c = e >= 0 && e < E && cpu[e];
             a.sel_out[s] = c ? -1 : e;
-            a.w_out[s] = c ? 0.0f : a.w[s];
+            a.w_out[s] = c ? 0.0f : wt;
         }
+    };
+#pragma unroll
+    for (int k = 0; k < SPT; ++k)
+        if (256 * k < a.n) pick_pass(256 * k, re[k], rw[k]);
+    for (int base = 256 * SPT; base < a.n; base += 256)
+    {
+        const int s = base + t;
+        pick_pass(base, s < a.n ? a.sel[s] : -1, s < a.n ? a.w[s] : 0.0f);
     }
     if (publish)
     {
