@@ -338,17 +338,41 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
             }
             wait_vmcnt<0>();      // the trailing (empty) loads, so the ring is quiet when it is reused or left
 
-            // D layout: lane (column col, group g) holds routes 4g .. 4g+3 of column col of each tile
-#pragma unroll
-            for (int v = 0; v < 4; ++v)
+            // D layout: lane (column col, group g) holds routes 4g .. 4g+3 of column col of each tile. The sums leave
+            // through the wave's ring, free now, so each route row goes out as one 512-byte run of 16-byte stores:
+            // per pass 8 rows (groups 2p and 2p + 1), row q at dword 128 q.
+            uint32_t* stage = &ring[wave * GV_RING * SLOT];
+            // lane indices recomputed here from an opaque copy, so nothing of this block is held across the loop
+            int sl = lane;
+            asm volatile("" : "+v"(sl));
+            const int sg = sl >> 4, scol = sl & 15;
+            for (int p8 = 0; p8 < nr; p8 += 8)
             {
-                const int rr = 4 * g + v;
-                if (rr < nr)
+                if ((sg >> 1) == (p8 >> 3))
                 {
-                    float* dst = a.part + ((size_t)(piece * a.n + first + r0 + rr) * NMAT + m) * a.N + cb * GV_COLS + col;
 #pragma unroll
-                    for (int c = 0; c < 8; ++c) dst[c * 16] = acc[c][v];
+                    for (int v = 0; v < 4; ++v)
+                    {
+                        const int q = 4 * (sg & 1) + v;
+                        if (p8 + q < nr)
+#pragma unroll
+                            for (int c = 0; c < 8; ++c)
+                                stage[128 * q + 16 * c + scol] = __float_as_uint(acc[c][v]);
+                    }
                 }
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                {
+                    const int q = 2 * h + (sl >> 5), c4 = 4 * (sl & 31);
+                    if (p8 + q < nr)
+                    {
+                        const uint4 v4 = *reinterpret_cast<const uint4*>(&stage[128 * q + c4]);
+                        float* dst = a.part + ((size_t)(piece * a.n + first + r0 + p8 + q) * NMAT + m) * a.N +
+                                     cb * GV_COLS + c4;
+                        *reinterpret_cast<uint4*>(dst) = v4;
+                    }
+                }
+                wait_lgkm0();     // the rows are read before the ring is written again
             }
         }
     }
