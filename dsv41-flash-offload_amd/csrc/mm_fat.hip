@@ -458,57 +458,74 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
 #pragma unroll
     for (int u = 0; u < 4; ++u)
         *reinterpret_cast<half4_t*>(bdst + u * 1024) = decode4<true>(tword[u * 32 + lhi], tword[u * 32 + llo], sh);
-    for (int s = 0; s < S; ++s)
-    {
-        if (tloader) wait_vmcnt<LA + 1>(); else wait_vmcnt<LA>();
-        lds_barrier();
-        if (tloader) load_trellis(s + FT_PT);
-        // one step: the trellis words of step s + 1 and the operands of step s first, then per row block its 4
-        // MFMAs, one tile of step s + 1 decoded after every MB / 4 blocks
-        // slot offset as one scalar, so each read is a per-lane base plus an immediate
-        const uint32_t toff = (uint32_t)__builtin_amdgcn_readfirstlane(((s + 1) % FT_TS) * T_SLOT);
-        const uint8_t* thp = reinterpret_cast<const uint8_t*>(tword + lhi) + toff;
-        const uint8_t* tlp = reinterpret_cast<const uint8_t*>(tword + llo) + toff;
-        uint32_t th[4], tl[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u)
+    // Row blocks of this wave that hold routes of the tile (uniform): a wave whose half of a partial tile ends early
+    // skips the MFMAs and input reads of its empty row blocks (their accumulators stay zero and are never stored);
+    // loads and decode, which serve the whole workgroup, run either way. Full waves take the scheduled variant.
+    const int nvb = max(0, min(MB, (rows - wm * (BM / 2) + 15) / 16));
+    auto main_loop = [&](auto part_tag) {
+        constexpr bool PART = decltype(part_tag)::value;
+        for (int s = 0; s < S; ++s)
         {
-            th[u] = *reinterpret_cast<const uint32_t*>(thp + u * 128);
-            tl[u] = *reinterpret_cast<const uint32_t*>(tlp + u * 128);
-        }
-        const uint8_t* as = Aring + (size_t)(s % FT_PA) * A_STAGE;
-        const uint8_t* bs = bsrc + (size_t)(s & 1) * B_BUF;
-        uint8_t* bd = bdst + (size_t)((s + 1) & 1) * B_BUF;
-        // every operand of the step is read before the step's LDS writes (input loads, decoded tiles): the
-        // compiler keeps LDS accesses that may alias in program order, so reads placed after a write would each
-        // wait a full LDS round trip
-        half8_t B[4], A[MB];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) B[j] = *reinterpret_cast<const half8_t*>(bs + j * 1024);
-#pragma unroll
-        for (int i = 0; i < MB; ++i) A[i] = *reinterpret_cast<const half8_t*>(as + aoff[i]);
-#pragma unroll
-        for (int i = 0; i < MB; ++i)
-        {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], acc[i][j], 0, 0, 0);
-            if (i % (MB / LA) == 0) load_input(s + FT_PA - 1, i / (MB / LA));
-            if (i % (MB / 4) == MB / 4 - 1)
+            if (tloader) wait_vmcnt<LA + 1>(); else wait_vmcnt<LA>();
+            lds_barrier();
+            if (tloader) load_trellis(s + FT_PT);
+            // one step: the trellis words of step s + 1 and the operands of step s first, then per row block its 4
+            // MFMAs, one tile of step s + 1 decoded after every MB / 4 blocks
+            // slot offset as one scalar, so each read is a per-lane base plus an immediate
+            const uint32_t toff = (uint32_t)__builtin_amdgcn_readfirstlane(((s + 1) % FT_TS) * T_SLOT);
+            const uint8_t* thp = reinterpret_cast<const uint8_t*>(tword + lhi) + toff;
+            const uint8_t* tlp = reinterpret_cast<const uint8_t*>(tword + llo) + toff;
+            uint32_t th[4], tl[4];
+    #pragma unroll
+            for (int u = 0; u < 4; ++u)
             {
-                const int u = i / (MB / 4);
-                *reinterpret_cast<half4_t*>(bd + u * 1024) = decode4<true>(th[u], tl[u], sh);
+                th[u] = *reinterpret_cast<const uint32_t*>(thp + u * 128);
+                tl[u] = *reinterpret_cast<const uint32_t*>(tlp + u * 128);
+            }
+            const uint8_t* as = Aring + (size_t)(s % FT_PA) * A_STAGE;
+            const uint8_t* bs = bsrc + (size_t)(s & 1) * B_BUF;
+            uint8_t* bd = bdst + (size_t)((s + 1) & 1) * B_BUF;
+            // every operand of the step is read before the step's LDS writes (input loads, decoded tiles): the
+            // compiler keeps LDS accesses that may alias in program order, so reads placed after a write would each
+            // wait a full LDS round trip
+            half8_t B[4], A[MB];
+    #pragma unroll
+            for (int j = 0; j < 4; ++j) B[j] = *reinterpret_cast<const half8_t*>(bs + j * 1024);
+    #pragma unroll
+            for (int i = 0; i < MB; ++i)
+                if (!PART || i < nvb) A[i] = *reinterpret_cast<const half8_t*>(as + aoff[i]);
+    #pragma unroll
+            for (int i = 0; i < MB; ++i)
+            {
+                if (!PART || i < nvb)
+    #pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], acc[i][j], 0, 0, 0);
+                if (i % (MB / LA) == 0) load_input(s + FT_PA - 1, i / (MB / LA));
+                if (i % (MB / 4) == MB / 4 - 1)
+                {
+                    const int u = i / (MB / 4);
+                    *reinterpret_cast<half4_t*>(bd + u * 1024) = decode4<true>(th[u], tl[u], sh);
+                }
+            }
+            // schedule: the LDS reads first, then one MFMA followed by two VALU instructions (the decode, which needs
+            // about that many per MFMA), so a wave keeps its MFMA pipe busy between its own decode instructions
+            if constexpr (!PART)
+            {
+                __builtin_amdgcn_sched_group_barrier(0x0100, 4 + MB + 8, 0);
+    #pragma unroll
+                for (int k = 0; k < 4 * MB; ++k)
+                {
+                    __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);
+                }
             }
         }
-        // schedule: the LDS reads first, then one MFMA followed by two VALU instructions (the decode, which needs
-        // about that many per MFMA), so a wave keeps its MFMA pipe busy between its own decode instructions
-        __builtin_amdgcn_sched_group_barrier(0x0100, 4 + MB + 8, 0);
-#pragma unroll
-        for (int k = 0; k < 4 * MB; ++k)
-        {
-            __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
-            __builtin_amdgcn_sched_group_barrier(0x0002, 2, 0);
-        }
-    }
+    };
+    if (nvb == MB)
+        main_loop(std::false_type{});
+    else
+        main_loop(std::true_type{});
     wait_vmcnt<0>();
     lds_barrier();
 
