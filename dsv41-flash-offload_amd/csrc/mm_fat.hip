@@ -136,22 +136,22 @@ __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e,
     int ce = cnt_e ? cnt_e[0] : cap + 1;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int g = lane & 3, q = (lane >> 2) & 3, bl = lane >> 4;
-    const int m = wave >> 1, nbh = H / 256, b0 = (wave & 1) * nbh;
+    const int nb = H / 128;
     const Lane8Signs sg = lane8_signs(lane);
-    const uint16_t* su = suh13 + ((size_t)e * 2 + m) * H;
-    uint16_t* dst = xa + (size_t)pos * 2 * H + m * 32 + 8 * g;
+    const uint16_t* su0 = suh13 + (size_t)e * 2 * H;       // gate; up follows
+    uint16_t* dst = xa + (size_t)pos * 2 * H + 8 * g;
     // raw words of element pair (t, h): fp16 / bf16 input as one dword, fp32 as two
     using Raw = typename std::conditional<XD == MM_DTYPE_F32, uint2, uint32_t>::type;
-    // lane group bl takes blocks b0 + bl, + 4, ...: four of them per pass, all loaded before any is used (blocks
-    // past the wave's half reload its last block and are not stored)
-    for (int bb = bl; bb < nbh; bb += 16)
+    // lane group bl of wave w takes blocks w + 4 bl + 16 i of the row, both matrices (the input is read once): two
+    // blocks per pass, all loaded before any is used (blocks past the row reload its last block and are not stored)
+    for (int f0 = wave + 4 * bl; f0 < nb; f0 += 32)
     {
-        Raw xr[4][4];
-        uint32_t sr[4][4];
+        Raw xr[2][4];
+        uint32_t sr[2][2][4];
 #pragma unroll
-        for (int it = 0; it < 4; ++it)
+        for (int it = 0; it < 2; ++it)
         {
-            const int k0 = (b0 + min(bb + 4 * it, nbh - 1)) * 128 + 32 * q + 2 * g;
+            const int k0 = min(f0 + 16 * it, nb - 1) * 128 + 32 * q + 2 * g;
 #pragma unroll
             for (int th = 0; th < 4; ++th)
             {
@@ -160,48 +160,58 @@ __device__ __forceinline__ void fat_prep_row_t(const void* x, size_t row, int e,
                     xr[it][th] = *reinterpret_cast<const uint2*>(static_cast<const float*>(x) + row + k);
                 else
                     xr[it][th] = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(x) + row + k);
-                sr[it][th] = *reinterpret_cast<const uint32_t*>(su + k);
+                sr[it][0][th] = *reinterpret_cast<const uint32_t*>(su0 + k);
+                sr[it][1][th] = *reinterpret_cast<const uint32_t*>(su0 + H + k);
             }
         }
         asm volatile("" : "+v"(ce));       // the count is first used here, after the row's loads
         if (ce <= cap) return;
 #pragma unroll
-        for (int it = 0; it < 4; ++it)
+        for (int it = 0; it < 2; ++it)
         {
-            const int b = bb + 4 * it;
-            if (b >= nbh) break;
-            float v[8];
+            const int b = f0 + 16 * it;
+            if (b >= nb) break;
+            // th = 2 t + h: elements 8 h + 16 t (+ 0, 1) of the lane's column pair go to xv[4 t + 2 h + j]
+            float xv[8];
 #pragma unroll
             for (int th = 0; th < 4; ++th)
             {
-                // th = 2 t + h: elements 8 h + 16 t (+ 0, 1) of the lane's column pair, v[4 t + 2 h + j]
-                float x0, x1;
+                const int i = 4 * (th >> 1) + 2 * (th & 1);
                 if constexpr (XD == MM_DTYPE_F16)
                 {
-                    x0 = h2f((uint16_t)(xr[it][th] & 0xffffu));
-                    x1 = h2f((uint16_t)(xr[it][th] >> 16));
+                    xv[i] = h2f((uint16_t)(xr[it][th] & 0xffffu));
+                    xv[i + 1] = h2f((uint16_t)(xr[it][th] >> 16));
                 }
                 else if constexpr (XD == MM_DTYPE_BF16)
                 {
-                    x0 = r16(__uint_as_float(xr[it][th] << 16));
-                    x1 = r16(__uint_as_float(xr[it][th] & 0xffff0000u));
+                    xv[i] = r16(__uint_as_float(xr[it][th] << 16));
+                    xv[i + 1] = r16(__uint_as_float(xr[it][th] & 0xffff0000u));
                 }
                 else
                 {
-                    x0 = r16(bf16_value(__uint_as_float(xr[it][th].x)));
-                    x1 = r16(bf16_value(__uint_as_float(xr[it][th].y)));
+                    xv[i] = r16(bf16_value(__uint_as_float(xr[it][th].x)));
+                    xv[i + 1] = r16(bf16_value(__uint_as_float(xr[it][th].y)));
                 }
-                const int i = 4 * (th >> 1) + 2 * (th & 1);
-                v[i] = x0 * h2f((uint16_t)(sr[it][th] & 0xffffu));
-                v[i + 1] = x1 * h2f((uint16_t)(sr[it][th] >> 16));
             }
-            fwht128_lane8(v, sg);
-            uint4 o;
-            o.x = (uint32_t)f2h(v[0] * HAD) | ((uint32_t)f2h(v[1] * HAD) << 16);
-            o.y = (uint32_t)f2h(v[2] * HAD) | ((uint32_t)f2h(v[3] * HAD) << 16);
-            o.z = (uint32_t)f2h(v[4] * HAD) | ((uint32_t)f2h(v[5] * HAD) << 16);
-            o.w = (uint32_t)f2h(v[6] * HAD) | ((uint32_t)f2h(v[7] * HAD) << 16);
-            *reinterpret_cast<uint4*>(dst + (size_t)(4 * (b0 + b) + q) * 64) = o;
+#pragma unroll
+            for (int m = 0; m < 2; ++m)
+            {
+                float v[8];
+#pragma unroll
+                for (int th = 0; th < 4; ++th)
+                {
+                    const int i = 4 * (th >> 1) + 2 * (th & 1);
+                    v[i] = xv[i] * h2f((uint16_t)(sr[it][m][th] & 0xffffu));
+                    v[i + 1] = xv[i + 1] * h2f((uint16_t)(sr[it][m][th] >> 16));
+                }
+                fwht128_lane8(v, sg);
+                uint4 o;
+                o.x = (uint32_t)f2h(v[0] * HAD) | ((uint32_t)f2h(v[1] * HAD) << 16);
+                o.y = (uint32_t)f2h(v[2] * HAD) | ((uint32_t)f2h(v[3] * HAD) << 16);
+                o.z = (uint32_t)f2h(v[4] * HAD) | ((uint32_t)f2h(v[5] * HAD) << 16);
+                o.w = (uint32_t)f2h(v[6] * HAD) | ((uint32_t)f2h(v[7] * HAD) << 16);
+                *reinterpret_cast<uint4*>(dst + (size_t)(4 * b + q) * 64 + m * 32) = o;
+            }
         }
     }
 }
