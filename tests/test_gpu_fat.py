@@ -65,6 +65,31 @@ def test_fat_small_shapes_vs_oracle(dev, H, I, E, T, k):
     assert ok, m
 
 
+def test_fat_tile_boundaries(dev):
+    """Experts with 1, 128, 129, 192, 256 and 257 routes: 128-route tiles holding one route, 256-route tiles whose
+    second row half holds 1 or 64 routes (those waves skip their empty row blocks), a full tile, and a full tile
+    followed by a one-route tile."""
+    import torch
+    from mi355moe import moe
+    H, I, seed = 256, 128, 8080
+    counts = [1, 128, 129, 192, 256, 257]
+    E = len(counts)
+    st = make_store(E, H, I, seed, device=dev, exact=True)
+    rng = np.random.default_rng(12)
+    ids = rng.permutation(np.repeat(np.arange(E), counts)).astype(np.int64)[:, None]
+    T = ids.shape[0]
+    w = np.ones((T, 1), np.float32)
+    x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
+    print(f"fat tile boundaries T={T}", flush=True)
+    out = moe.moe_prefill(st, _t(x16, dev), _t(ids, dev), _t(w, dev))
+    torch.cuda.synchronize()
+    ref = OracleLayer(st, seed).forward(x16.astype(np.float32), ids, w)
+    for e in range(E):
+        rows = ids[:, 0] == e
+        ok, m = within_tolerance(out.cpu().numpy()[rows], ref[rows])
+        assert ok, (counts[e], m)
+
+
 def test_grouped_gemm_rows_of_fat_experts_only(dev):
     """Only routes of experts above cap get rows; masked ids (-1, >= E) and small experts are left untouched."""
     import torch

@@ -43,7 +43,8 @@ def test_expert_matches_reference_golden(dev, exact):
 
 
 @pytest.mark.parametrize("exact", [False, True])
-@pytest.mark.parametrize("H,I,E,T,k", [(256, 256, 8, 3, 2), (1024, 384, 16, 5, 4), (2048, 1152, 12, 6, 3)])
+@pytest.mark.parametrize("H,I,E,T,k", [(256, 256, 8, 3, 2), (384, 128, 5, 2, 2), (1024, 384, 16, 5, 4),
+                                         (2048, 1152, 12, 6, 3)])
 def test_small_shapes_vs_oracle(dev, H, I, E, T, k, exact):
     import torch
     from mi355moe import moe
