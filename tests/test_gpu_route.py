@@ -40,11 +40,11 @@ def test_permute_bitexact(dev, n, E, topk):
     assert np.array_equal(r["active"].cpu().numpy()[: act.size], act)
 
 
-def _split_case(seed, pol, score_kind="zero"):
+def _split_case(seed, pol, score_kind="zero", T=4):
     from mi355moe import workload
-    ids, w = workload.zipf_routing(4, 8, 384, seed=seed)
+    ids, w = workload.zipf_routing(T, 8, 384, seed=seed)
     slotof = workload.cache_map(ids, 384, slots=709, frac_resident=0.4, seed=seed)
-    z = np.random.default_rng(seed).normal(0, 1, (4, 4096)).astype(np.float16)
+    z = np.random.default_rng(seed).normal(0, 1, (T, 4096)).astype(np.float16)
     score = np.zeros(384, np.float32) if score_kind == "zero" else np.random.default_rng(seed + 1).permutation(384).astype(np.float32)
     return ids, w, z, slotof, score, np.asarray(pol, np.float32)
 
@@ -53,15 +53,19 @@ POL_DEFAULT = [0.58, 0.03, 0.11, 0.20, 0.35, 384, -1, 0, 0]   # image defaults (
 POL_CHEAP = [0.58, 0.03, 0.01, 0.05, 0.35, 384, -1, 0, 0]     # cheap CPU: several picks
 
 
-@pytest.mark.parametrize("seed,pol,score_kind", [(1, POL_DEFAULT, "zero"), (2, POL_CHEAP, "zero"),
-                                                 (3, POL_CHEAP, "perm"), (4, [0.58, 0.03, 0.11, 0.2, 0.35, 384, 2, 0, 0], "zero"),
-                                                 (5, [0.58, 0.03, 0.11, 0.2, 0.35, 384, 0, 1, 0], "zero")])
-def test_split_bitexact(dev, seed, pol, score_kind):
+@pytest.mark.parametrize("seed,pol,score_kind,T", [(1, POL_DEFAULT, "zero", 4), (2, POL_CHEAP, "zero", 4),
+                                                   (3, POL_CHEAP, "perm", 4),
+                                                   (4, [0.58, 0.03, 0.11, 0.2, 0.35, 384, 2, 0, 0], "zero", 4),
+                                                   (5, [0.58, 0.03, 0.11, 0.2, 0.35, 384, 0, 1, 0], "zero", 4),
+                                                   (6, POL_CHEAP, "perm", 160)])
+def test_split_bitexact(dev, seed, pol, score_kind, T):
+    """Split outputs bit-exact against the oracle; T = 160 (1,280 routes) also covers routes past the first 1,024
+    that the kernel keeps in registers."""
     import torch
     from mi355moe import _lib
     from mi355moe.hostmem import HostBuffer
-    ids, w, z, slotof, score, pol = _split_case(seed, pol, score_kind)
-    n, bsz, H, E = ids.size, 4, 4096, 384
+    ids, w, z, slotof, score, pol = _split_case(seed, pol, score_kind, T)
+    n, bsz, H, E = ids.size, T, 4096, 384
     ref = O.split(ids, w, z, E, slotof, score, pol, seqc=5, li=7)
     hb = HostBuffer(16 * 8 + bsz * H * 2 + n * 3 * 4)
     ctrl = hb.array(np.int64, (16,), 0)
