@@ -504,6 +504,10 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
     #pragma unroll
             for (int i = 0; i < MB; ++i)
                 if (!PART || i < nvb) A[i] = *reinterpret_cast<const half8_t*>(as + aoff[i]);
+            // tile 0 is decoded before the first MFMA: the decode runs while the workgroup's operand reads of the
+            // step are still being served (about 2 % off the layer against decoding it after the MFMAs of row
+            // blocks 0 .. MB / 4 - 1)
+            *reinterpret_cast<half4_t*>(bd) = decode4<true>(th[0], tl[0], sh);
     #pragma unroll
             for (int i = 0; i < MB; ++i)
             {
@@ -512,17 +516,20 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
                     for (int j = 0; j < 4; ++j)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], acc[i][j], 0, 0, 0);
                 if (i % (MB / LA) == 0) load_input(s + FT_PA - 1, i / (MB / LA));
-                if (i % (MB / 4) == MB / 4 - 1)
+                if (i % (MB / 4) == MB / 4 - 1 && i / (MB / 4) < 3)
                 {
-                    const int u = i / (MB / 4);
+                    const int u = i / (MB / 4) + 1;
                     *reinterpret_cast<half4_t*>(bd + u * 1024) = decode4<true>(th[u], tl[u], sh);
                 }
             }
-            // schedule: the LDS reads first, then one MFMA followed by two VALU instructions (the decode, which needs
-            // about that many per MFMA), so a wave keeps its MFMA pipe busy between its own decode instructions
+            // schedule: the LDS reads first, the decode of tile 0 and its store, then one MFMA followed by two VALU
+            // instructions (the rest of the decode, which needs about that many per MFMA), so a wave keeps its MFMA
+            // pipe busy between its own decode instructions
             if constexpr (!PART)
             {
                 __builtin_amdgcn_sched_group_barrier(0x0100, 4 + MB + 8, 0);
+                __builtin_amdgcn_sched_group_barrier(0x0002, 16, 0);
+                __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);
     #pragma unroll
                 for (int k = 0; k < 4 * MB; ++k)
                 {
