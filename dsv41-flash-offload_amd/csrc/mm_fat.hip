@@ -333,8 +333,8 @@ __device__ __forceinline__ int chunk_slot(int q, int r)
 // MB = 16-row blocks per row-wave: tiles of BM = 32 MB routes (256 or 128). 8 waves: wave (wm, wn) = (w >> 2,
 // w & 3) multiplies rows (BM / 2) wm .. + BM / 2 - 1 by column tiles 4 wn .. 4 wn + 3 of 16; every wave loads an
 // eighth of the inputs and waves 0 .. 3 also the trellis (chunk w: tile row w >> 1 of matrix / block w & 1),
-// which runs further ahead; wave w decodes tiles 4 (w & 1) .. + 3 of chunk w >> 1. Rows past the tile's routes
-// read zero inputs.
+// which runs further ahead; wave w decodes column tiles 2 (w & 3), 2 (w & 3) + 1 of sub-block w >> 2 in both tile
+// rows (chunks w >> 2 and 2 + (w >> 2)). Rows past the tile's routes read zero inputs.
 template <int MODE, int MB, bool YH = false>
 __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
 {
@@ -419,17 +419,21 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
         __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, Aring + (size_t)st * A_STAGE + (size_t)li * 1024, 16, voff, 0, 0, 0);
     };
 
-    // ---- decode: wave w owns chunk w >> 1 (tile row t = w >> 2 of matrix / block b = (w >> 1) & 1), tiles
-    // 4 (w & 1) .. + 3; lane (col, g) decodes states i0 .. i0+3 of column col in a tile
+    // ---- decode: lane (col, g) decodes states i0 .. i0+3 of column col in a tile
     const int col = lane & 15, g = lane >> 4;
     const int i0 = 32 * (col & 7) + 8 * g + 4 * (col >> 3);
     const int eb = 3 * i0 + 11;
     const int blo = eb >> 5, bhi = (blo + 23) % 24;
     const int llo = 4 * (blo / 3) + blo % 3, lhi = 4 * (bhi / 3) + bhi % 3;
     const uint32_t sh = 31u - (uint32_t)(eb & 31);
-    const int dq = wave >> 1;
-    const uint32_t* tword = reinterpret_cast<const uint32_t*>(Tring + (size_t)dq * 1024) + (wave & 1) * 4 * 32;
-    uint8_t* bdst = Bdec + ((size_t)((dq & 1) * 8 + (wave & 1) * 4) * 64 + lane) * 16 + (dq >> 1) * 8;
+    // Wave w decodes column tiles 2 (w & 3) and 2 (w & 3) + 1 of sub-block w >> 2 (chunks w >> 2 and 2 + (w >> 2):
+    // tile rows 0 and 1 of the step) and stores each column tile's 8 k-values per lane, tile row 0 in the low 8
+    // bytes and row 1 in the high 8, as one 16-byte write (lane-contiguous: no LDS bank conflicts). Decoded tile k
+    // of the wave (k = 0 .. 3) is tile row k & 1 of column tile 2 (w & 3) + (k >> 1): trellis words at
+    // tword + (k & 1) * 512 + (k >> 1) * 32.
+    const int db = wave >> 2, dc = 2 * (wave & 3);
+    const uint32_t* tword = reinterpret_cast<const uint32_t*>(Tring + (size_t)db * 1024 + (size_t)dc * 128);
+    uint8_t* bdst = Bdec + ((size_t)(db * 8 + dc) * 64 + lane) * 16;
     // ---- MFMA: rows (BM / 2) wm + 16 i + col of input matrix wn >> 1 (gate/up), B tiles 4 wn .. + 3
     const int wm = wave >> 2, wn = wave & 3;
     const uint8_t* bsrc = Bdec + ((size_t)(wn * 4) * 64 + lane) * 16;
@@ -466,8 +470,12 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
     if (tloader) wait_vmcnt<LA + FT_PT - 1>(); else wait_vmcnt<LA>();          // trellis of step 0
     lds_barrier();
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-        *reinterpret_cast<half4_t*>(bdst + u * 1024) = decode4<true>(tword[u * 32 + lhi], tword[u * 32 + llo], sh);
+    for (int v = 0; v < 2; ++v)
+    {
+        const half4_t r0 = decode4<true>(tword[v * 32 + lhi], tword[v * 32 + llo], sh);
+        const half4_t r1 = decode4<true>(tword[512 + v * 32 + lhi], tword[512 + v * 32 + llo], sh);
+        *reinterpret_cast<half8_t*>(bdst + v * 1024) = half8_t{ r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3] };
+    }
     // Row blocks of this wave that hold routes of the tile (uniform): a wave whose half of a partial tile ends early
     // skips the MFMAs and input reads of its empty row blocks (their accumulators stay zero and are never stored);
     // loads and decode, which serve the whole workgroup, run either way. Full waves take the scheduled variant.
@@ -489,8 +497,8 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
     #pragma unroll
             for (int u = 0; u < 4; ++u)
             {
-                th[u] = *reinterpret_cast<const uint32_t*>(thp + u * 128);
-                tl[u] = *reinterpret_cast<const uint32_t*>(tlp + u * 128);
+                th[u] = *reinterpret_cast<const uint32_t*>(thp + (u & 1) * 2048 + (u >> 1) * 128);
+                tl[u] = *reinterpret_cast<const uint32_t*>(tlp + (u & 1) * 2048 + (u >> 1) * 128);
             }
             const uint8_t* as = Aring + (size_t)(s % FT_PA) * A_STAGE;
             const uint8_t* bs = bsrc + (size_t)(s & 1) * B_BUF;
@@ -506,8 +514,9 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
                 if (!PART || i < nvb) A[i] = *reinterpret_cast<const half8_t*>(as + aoff[i]);
             // tile 0 is decoded before the first MFMA: the decode runs while the workgroup's operand reads of the
             // step are still being served (about 2 % off the layer against decoding it after the MFMAs of row
-            // blocks 0 .. MB / 4 - 1)
-            *reinterpret_cast<half4_t*>(bd) = decode4<true>(th[0], tl[0], sh);
+            // blocks 0 .. MB / 4 - 1); tiles 1 .. 3 follow row blocks MB / 4 - 1, MB / 2 - 1, 3 MB / 4 - 1, and
+            // each column tile is stored once both of its tile rows are decoded
+            half4_t d0 = decode4<true>(th[0], tl[0], sh);
     #pragma unroll
             for (int i = 0; i < MB; ++i)
             {
@@ -519,17 +528,21 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
                 if (i % (MB / 4) == MB / 4 - 1 && i / (MB / 4) < 3)
                 {
                     const int u = i / (MB / 4) + 1;
-                    *reinterpret_cast<half4_t*>(bd + u * 1024) = decode4<true>(th[u], tl[u], sh);
+                    const half4_t d = decode4<true>(th[u], tl[u], sh);
+                    if (u & 1)
+                        *reinterpret_cast<half8_t*>(bd + (u >> 1) * 1024) =
+                            half8_t{ d0[0], d0[1], d0[2], d0[3], d[0], d[1], d[2], d[3] };
+                    else
+                        d0 = d;
                 }
             }
-            // schedule: the LDS reads first, the decode of tile 0 and its store, then one MFMA followed by two VALU
+            // schedule: the LDS reads first, the decode of tile 0, then one MFMA followed by two VALU
             // instructions (the rest of the decode, which needs about that many per MFMA), so a wave keeps its MFMA
             // pipe busy between its own decode instructions
             if constexpr (!PART)
             {
                 __builtin_amdgcn_sched_group_barrier(0x0100, 4 + MB + 8, 0);
                 __builtin_amdgcn_sched_group_barrier(0x0002, 16, 0);
-                __builtin_amdgcn_sched_group_barrier(0x0200, 1, 0);
     #pragma unroll
                 for (int k = 0; k < 4 * MB; ++k)
                 {
