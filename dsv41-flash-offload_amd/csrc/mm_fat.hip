@@ -40,7 +40,7 @@ struct FatArgs
     const ExpertRec* rec;         // [max_active] active experts (permutation order)
     const int32_t* nactive;       // [1]
     const int32_t* tile_off;      // [max_active + 1] first tile of each active expert in this launch's list
-    const int32_t* big_off;       // [max_active + 1] 224-route tiles (a 96-route tile follows them)
+    const int32_t* big_off;       // [max_active + 1] 256-route tiles (a 128-route tile follows them)
     const uint16_t* xa;           // mode 0: [n][H/32][gate 32, up 32]; mode 1: [n][I] (operand order)
     const uint16_t* svh13;        // [E][2][I]
     const uint16_t* suh2;         // [E][I]
