@@ -402,7 +402,7 @@ def main():
     args = ap.parse_args()
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
-        print(f"bench.py: this build measures one MI355X (got --gpus {args.gpus}, WORLD_SIZE {world}); the multi-GPU "
+        print(f"bench.py: measures one MI355X only (got --gpus {args.gpus}, WORLD_SIZE {world}); the multi-GPU "
               "expert-parallel design is documented but not built, so N > 1 is not run.", flush=True)
         sys.exit(2)
     if args.workload == "cache":

@@ -4,7 +4,7 @@
  * This file restates, in plain C, the arithmetic of the reference's routed-expert path so that the
  * HIP kernels can be checked against it. It is never linked into, loaded by, or called from the product
  * library: only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use it, and only as
- * the checker.
+ * the expected result that GPU outputs are compared against.
  *
  * Every function names the reference lines it follows (paths relative to the reference checkout).
  * How each function is pinned (golden vectors from the compiled reference, closed forms, brute force):
@@ -373,8 +373,8 @@ MMO_EXPORT void mmo_split(const int64_t* sel, const float* w, const uint16_t* z,
 /* ---------------------------------------------------------------------------------------------
  * Routing prep: map out-of-range ids to the sentinel E, count per expert (E+1 bins), stable order by
  * (expert, flat index), token index = flat index / topk, per-expert exclusive offsets.
- * patches/vllm-exl3-host-dma.patch:204-236,296-312 (argsort stability is unspecified there; this build
- * fixes it to stable).
+ * patches/vllm-exl3-host-dma.patch:204-236,296-312 (argsort stability is unspecified there; the order here
+ * is stable by definition).
  * ------------------------------------------------------------------------------------------- */
 MMO_EXPORT void mmo_permute(const int64_t* ids, const float* w, int n, int topk, int E, int32_t* counts,
                             int32_t* offsets, int32_t* order, int32_t* token_sorted, float* weight_sorted)

@@ -1,7 +1,8 @@
 """CPU ORACLE for the routed-expert MoE path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg may import this module,
-and only as the checker. The product library never routes through it.
+and only as the expected result that GPU outputs are compared against. The product library never routes
+through it.
 
 What each function restates (paths relative to the reference checkout) and how it is pinned:
 
