@@ -108,6 +108,7 @@ struct PrepArgs
     uint16_t* xa;             // [n][2][H] fp16 in operand order
     float* xsum;              // [n][2][nb] sums of xa over each workgroup's rows
     int n, topk, E, H, nb, x_dtype, rescale;
+    int cap;                  // experts with more than cap routes are left out (no record work, no outputs)
 };
 
 __device__ __forceinline__ int wave_sum_int(int v)
@@ -125,5 +126,10 @@ __device__ __forceinline__ int wave_sum_int(int v)
 // routes, from the ids (offsets == nullptr) or from a permutation. nb = input-row blocks per route and matrix.
 int prep_blocks(int H);
 void launch_route_prep(const PrepArgs& p, hipStream_t s);
+
+// The launches of mm_moe_decode on a given workspace (argument checks included); `who` names the caller in errors.
+int moe_decode_launch(const mm_layer_t* L, const void* x, int x_dtype, int rescale, int T, int topk, const int64_t* ids,
+                      const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes,
+                      mm_stream_t stream, const char* who);
 
 }  // namespace mm

@@ -33,7 +33,6 @@ namespace mm {
 constexpr int GV_WAVES = 4;
 constexpr int GV_THREADS = 64 * GV_WAVES;
 constexpr int GV_COLS = 128;          // output columns per segment (8 tiles)
-constexpr int GV_MAX_ROWS = 256;      // routes per expert on this path
 constexpr int GV_ROUTE_MAX = 1024;    // in-kernel routing limit (routes per call)
 constexpr int GV_RING = 4;            // tile rows in flight per wave (even: rows go through MFMA in pairs)
 static_assert(GV_RING % 2 == 0, "row pairs");
@@ -103,6 +102,8 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
     const int ec = valid ? e : 0;               // an expert in range for the loads
     const uint16_t* su = a.suh13 + ((size_t)ec * 2 + m) * a.H;
     const float sa = h2f(su[hc + lane]), sb = h2f(su[hc + lane + 64]);
+    // the expert's route count from the permutation (the in-kernel routing counts it below)
+    const int pcnt = perm ? a.offsets[ec + 1] - a.offsets[ec] : 0;
     // the record's matrix addresses, loaded by the thread that may write it
     int64_t wt0 = 0, wt1 = 0, wt2 = 0;
     if (tid == 0 && writer && valid)
@@ -146,6 +147,9 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
     rank = s_cnt[0][2] + s_cnt[1][2] + s_cnt[2][2] + s_cnt[3][2];
     nv = s_cnt[0][3] + s_cnt[1][3] + s_cnt[2][3] + s_cnt[3][3];
     const int pos = perm ? idx : less + rank;
+    // an expert with more than cap routes belongs to the fat-expert path: its positions stay reserved, but it gets
+    // an empty record and its routes no transformed inputs and no outputs
+    const bool fat = valid && (perm ? pcnt : same) > a.cap;
     if (tid == 0 && (writer || blockIdx.x == 0))
     {
         if (blockIdx.x == 0)
@@ -158,11 +162,11 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
         }
         if (writer)
         {
-            a.pos_of[s] = valid ? pos : -1;
+            a.pos_of[s] = valid && !fat ? pos : -1;
             if (valid)
             {
                 a.route_at[pos] = s;
-                a.e_at[pos] = e;
+                a.e_at[pos] = fat ? -1 : e;
                 // the expert's first route writes its record
                 int ai = -1, cnt = 0;
                 if (!perm && rank == 0)
@@ -182,13 +186,13 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
                 }
                 if (ai >= 0)
                 {
-                    ExpertRec r{ e, cnt, pos, 0, { wt0, wt1, wt2 }, 0 };
+                    ExpertRec r{ e, fat ? 0 : cnt, pos, 0, { wt0, wt1, wt2 }, 0 };
                     a.rec[ai] = r;
                 }
             }
         }
     }
-    if (!valid) return;
+    if (!valid || fat) return;
 
     // the route's expert input: x16 = fp16(bf16(x_t * s_t)) (fp16 input without rescale is taken as is);
     // s_t = 1 / RMS(x_t), the per-wave sums added as mm_prepare_input adds them
@@ -268,7 +272,7 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
         const int tr0 = piece * KT / pps, nrow = (piece + 1) * KT / pps - tr0;
         // fields read through the pointer: a local copy indexed by the runtime matrix would live in scratch
         const ExpertRec* rc = a.rec + ai;
-        const int cnt = min(rc->cnt, GV_MAX_ROWS), first = rc->first;
+        const int cnt = rc->cnt, first = rc->first;
         // per-matrix buffer descriptor in SGPRs. readfirstlane returns int: each half goes through uint32_t
         // before widening, or a low word >= 2^31 would sign-extend into the high word.
         const uint64_t wp = (uint64_t)rc->w[MODE == 0 ? m : 2];
@@ -452,7 +456,7 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     // workgroup's spare waves are past n, and they read position n - 1)
     const int nvalid = a.counts[1], nact = a.counts[0];
     const int e = a.e_at[min(pos, a.n - 1)];
-    if (pos >= nvalid) return;
+    if (pos >= nvalid || e < 0) return;      // past the routes, or a route of an expert above the cap
     const int pps = pieces_per_segment(a.nwaves, nact * 2 * ncb, a.cap);
     const int c = cb * GV_COLS;
     // round trip 2: scales, input sums and partial sums
@@ -550,7 +554,7 @@ __global__ __launch_bounds__(256) void k_down_y(DEpiArgs a)
     const int nvalid = a.counts[1], nact = a.counts[0];
     const int pc = min(pos, a.n - 1);
     const int s = a.route_at[pc], e = a.e_at[pc];
-    if (pos >= nvalid) return;
+    if (pos >= nvalid || e < 0) return;
     const int c = cb * GV_COLS;
     float ya, yb;
     down_block(a, nact, pos, c, e, lane, ya, yb);
@@ -689,7 +693,7 @@ static int check_common(const mm_layer_t* L, const void* x, int x_dtype, int T, 
                  "%s: x_dtype must be MM_DTYPE_F16, MM_DTYPE_BF16 or MM_DTYPE_F32", who);
     MM_CHECK_ARG(T > 0 && n > 0 && topk > 0 && n <= T * topk, "%s: bad T/n/topk", who);
     MM_CHECK_ARG((size_t)n * 2 * (L->H > L->I ? L->H : L->I) * 2 < ((size_t)1 << 31), "%s: too many routes", who);
-    MM_CHECK_ARG(max_rows > 0 && max_rows <= GV_MAX_ROWS, "%s: max_rows must be in [1, %d]", who, GV_MAX_ROWS);
+    MM_CHECK_ARG(max_rows > 0, "%s: max_rows must be at least 1", who);
     const bool perm = offsets != nullptr;
     MM_CHECK_ARG(perm ? (order && active && nactive) : n <= GV_ROUTE_MAX,
                  "%s: more than %d routes need the permutation (offsets, order, active, nactive)", who, GV_ROUTE_MAX);
@@ -700,11 +704,12 @@ static int check_common(const mm_layer_t* L, const void* x, int x_dtype, int T, 
 
 static void launch_prep(const mm_layer_t* L, const Ws& w, const void* x, int x_dtype, int rescale, int n, int topk,
                         const int64_t* ids, const int32_t* offsets, const int32_t* order, const int32_t* active,
-                        const int32_t* nactive, hipStream_t s)
+                        const int32_t* nactive, int cap, hipStream_t s)
 {
     const int nb = prep_blocks(L->H);
     PrepArgs p{ x, ids, offsets, order, active, nactive, L->gate_ptr, L->up_ptr, L->down_ptr, L->suh13,
-                w.rec, w.counts, w.pos_of, w.route_at, w.e_at, w.xa, w.xsum, n, topk, L->E, L->H, nb, x_dtype, rescale };
+                w.rec, w.counts, w.pos_of, w.route_at, w.e_at, w.xa, w.xsum, n, topk, L->E, L->H, nb, x_dtype, rescale,
+                cap };
     launch_route_prep(p, s);
 }
 
@@ -735,6 +740,29 @@ static DEpiArgs down_args(const mm_layer_t* L, const Ws& w, int n, int topk, con
                      partial_waves(), piece_cap(n), (L->flags & MM_LAYER_EXACT) ? 0 : 1 };
 }
 
+// One decode layer (mm_moe_decode) on a caller-provided workspace; `who` names the entry point in errors.
+int moe_decode_launch(const mm_layer_t* L, const void* x, int x_dtype, int rescale, int T, int topk, const int64_t* ids,
+                      const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes,
+                      mm_stream_t stream, const char* who)
+{
+    MM_CHECK_ARG(topk > 0 && topk <= MAX_TOPK, "%s: topk must be in [1, %d]", who, MAX_TOPK);
+    const int n = T * topk;
+    const int rc = check_common(L, x, x_dtype, T, n, topk, ids, nullptr, nullptr, nullptr, nullptr, max_rows, workspace,
+                                workspace_bytes, who);
+    if (rc) return rc;
+    MM_CHECK_ARG(w && out, "%s: null pointer", who);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    const Ws ws = carve(workspace, n, L->E, L->H, L->I);
+    launch_prep(L, ws, x, x_dtype, rescale, n, topk, ids, nullptr, nullptr, nullptr, nullptr, max_rows, s);
+    launch_partial<0>(L, ws, n, s);
+    launch_gu_epilogue(L, ws, n, s);
+    launch_partial<1>(L, ws, n, s);
+    const int threads = 64 * (topk < 2 ? 2 : topk);
+    hipLaunchKernelGGL(k_down_combine, dim3(T * (L->H / GV_COLS)), dim3(threads), 0, s,
+                       down_args(L, ws, n, topk, ids, w, nullptr, out));
+    return check_launch(who);
+}
+
 }  // namespace mm
 
 using namespace mm;
@@ -759,7 +787,7 @@ int mm_expert_gemv(const mm_layer_t* L, const void* x, int x_dtype, int rescale,
     MM_CHECK_ARG(Y || !(phases & 16), "mm_expert_gemv: null Y");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
     const Ws w = carve(workspace, n, L->E, L->H, L->I);
-    if (phases & 1) launch_prep(L, w, x, x_dtype, rescale, n, topk, ids, offsets, order, active, nactive, s);
+    if (phases & 1) launch_prep(L, w, x, x_dtype, rescale, n, topk, ids, offsets, order, active, nactive, max_rows, s);
     if (phases & 2) launch_partial<0>(L, w, n, s);
     if (phases & 4) launch_gu_epilogue(L, w, n, s);
     if (phases & 8) launch_partial<1>(L, w, n, s);
@@ -772,22 +800,8 @@ int mm_expert_gemv(const mm_layer_t* L, const void* x, int x_dtype, int rescale,
 int mm_moe_decode(const mm_layer_t* L, const void* x, int x_dtype, int rescale, int T, int topk, const int64_t* ids,
                   const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes, mm_stream_t stream)
 {
-    MM_CHECK_ARG(topk > 0 && topk <= MAX_TOPK, "mm_moe_decode: topk must be in [1, %d]", MAX_TOPK);
-    const int n = T * topk;
-    const int rc = check_common(L, x, x_dtype, T, n, topk, ids, nullptr, nullptr, nullptr, nullptr, max_rows, workspace,
-                                workspace_bytes, "mm_moe_decode");
-    if (rc) return rc;
-    MM_CHECK_ARG(w && out, "mm_moe_decode: null pointer");
-    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const Ws ws = carve(workspace, n, L->E, L->H, L->I);
-    launch_prep(L, ws, x, x_dtype, rescale, n, topk, ids, nullptr, nullptr, nullptr, nullptr, s);
-    launch_partial<0>(L, ws, n, s);
-    launch_gu_epilogue(L, ws, n, s);
-    launch_partial<1>(L, ws, n, s);
-    const int threads = 64 * (topk < 2 ? 2 : topk);
-    hipLaunchKernelGGL(k_down_combine, dim3(T * (L->H / GV_COLS)), dim3(threads), 0, s,
-                       down_args(L, ws, n, topk, ids, w, nullptr, out));
-    return check_launch("mm_moe_decode");
+    return mm::moe_decode_launch(L, x, x_dtype, rescale, T, topk, ids, w, max_rows, out, workspace, workspace_bytes,
+                                 stream, "mm_moe_decode");
 }
 
 }  // extern "C"

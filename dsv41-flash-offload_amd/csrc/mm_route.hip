@@ -365,40 +365,37 @@ __global__ __launch_bounds__(256) void k_split(SplitArgs a)
 
 // ---------------------------------------------------------------------------------------------------------
 // Host-partial add (ct/ft_tier_cu_v.cu:103-127): bounded wait on the host's done word, then out += hout.
+// The decision is taken once, by the one-lane wait kernel: on a timeout it clears dflag[0], so the add kernel
+// (every workgroup of it) either adds the whole partial or none of it. The reference lets each of its 16
+// workgroups wait and decide on its own, which can add part of a partial that lands near the deadline.
 // ---------------------------------------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_combine_host(float* __restrict__ out, int n, const int64_t* __restrict__ dflag,
-                                                      int64_t* ctrl, const float* hout, int64_t* stats,
-                                                      uint64_t timeout_ticks, double ns_per_tick)
+__global__ __launch_bounds__(64) void k_host_wait(int64_t* __restrict__ dflag, int64_t* ctrl, int64_t* stats,
+                                                  uint64_t timeout_ticks, double ns_per_tick)
 {
-    __shared__ int go;
-    if (threadIdx.x == 0)
+    if (threadIdx.x != 0) return;
+    const int64_t s = dflag[0];
+    if (s == 0) return;
+    const uint64_t t0 = wall_clock64();
+    uint64_t t1 = t0;
+    while (__hip_atomic_load(&ctrl[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < s)
     {
-        const int64_t s = dflag[0];
-        go = s != 0;
-        if (go)
+        t1 = wall_clock64();
+        if (t1 - t0 > timeout_ticks)
         {
-            const uint64_t t0 = wall_clock64();
-            uint64_t t1 = t0;
-            while (__hip_atomic_load(&ctrl[1], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_SYSTEM) < s)
-            {
-                t1 = wall_clock64();
-                if (t1 - t0 > timeout_ticks)
-                {
-                    go = 0;
-                    if (blockIdx.x == 0) atomicAdd((unsigned long long*)&stats[6], 1ull);
-                    break;
-                }
-                __builtin_amdgcn_s_sleep(2);
-            }
-            if (blockIdx.x == 0)
-            {
-                atomicAdd((unsigned long long*)&stats[4], (unsigned long long)((double)(t1 - t0) * ns_per_tick));
-                atomicAdd((unsigned long long*)&stats[5], 1ull);
-            }
+            dflag[0] = 0;                     // the partial is dropped
+            atomicAdd((unsigned long long*)&stats[6], 1ull);
+            break;
         }
+        __builtin_amdgcn_s_sleep(2);
     }
-    __syncthreads();
-    if (!go) return;
+    atomicAdd((unsigned long long*)&stats[4], (unsigned long long)((double)(t1 - t0) * ns_per_tick));
+    atomicAdd((unsigned long long*)&stats[5], 1ull);
+}
+
+__global__ __launch_bounds__(256) void k_host_add(float* __restrict__ out, int n, const int64_t* __restrict__ dflag,
+                                                  const float* hout)
+{
+    if (dflag[0] == 0) return;
     for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x)
         out[i] += __hip_atomic_load(hout + i, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
 }
@@ -756,7 +753,7 @@ int mm_split(const int64_t* sel, const float* w, const void* z_fp16, int n, int 
     return check_launch("mm_split");
 }
 
-int mm_combine_host(float* out, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout, int64_t* stats,
+int mm_combine_host(float* out, int n, int64_t* dflag, const int64_t* ctrl, const float* hout, int64_t* stats,
                     int64_t timeout_ns, mm_stream_t stream)
 {
     MM_CHECK_ARG(out && dflag && ctrl && hout && stats && n >= 0, "mm_combine_host: bad argument");
@@ -766,8 +763,9 @@ int mm_combine_host(float* out, int n, const int64_t* dflag, const int64_t* ctrl
     const double ns_per_tick = 1e6 / (double)khz;
     const uint64_t ticks = timeout_ns <= 0 ? 0 : (uint64_t)((double)timeout_ns / ns_per_tick);
     const int blocks = n <= 16 * 256 * 16 ? 16 : min(256, (n + 256 * 16 - 1) / (256 * 16));
-    hipLaunchKernelGGL(k_combine_host, dim3(blocks), dim3(256), 0, S(stream), out, n, dflag, const_cast<int64_t*>(ctrl), hout,
-                       stats, ticks, ns_per_tick);
+    hipLaunchKernelGGL(k_host_wait, dim3(1), dim3(64), 0, S(stream), dflag,
+                       const_cast<int64_t*>(ctrl), stats, ticks, ns_per_tick);
+    hipLaunchKernelGGL(k_host_add, dim3(blocks), dim3(256), 0, S(stream), out, n, dflag, hout);
     return check_launch("mm_combine_host");
 }
 

@@ -20,6 +20,7 @@ routed expert runs on the GPU from its cache slot or, zero-copy, from its pinned
 import json
 import os
 
+import numpy as np
 import torch
 
 from . import _lib, cache, exl3
@@ -39,12 +40,16 @@ def _init(layer):
     H = layer.H
     maxbsz = int(os.environ.get("DSV41_CT_MAXBSZ", "32"))
     S.update(H=H, I=layer.I, dev=dev, maxbsz=maxbsz, maxpicks=8 * maxbsz)
-    # host mailbox: ctrl int64 [16] | hx fp16 [maxbsz * H] | picks int32 [maxpicks * 3] (ct_vllm.py:62-65)
-    S["mail"] = HostBuffer(128 + maxbsz * H * 2 + S["maxpicks"] * 12)
+    # host mailbox (ct_vllm.py:62-65), pinned and device-mapped: ctrl int64 [16] | hx fp16 [maxbsz * H] |
+    # picks int32 [maxpicks * 3] | hout fp32 [maxbsz * H] (the host worker's partial, read by mm_combine_host)
+    o_hx, o_pk = 128, 128 + maxbsz * H * 2
+    o_out = (o_pk + S["maxpicks"] * 12 + 255) // 256 * 256
+    S["mail"] = HostBuffer(o_out + maxbsz * H * 4)
+    S["mail"].array(np.uint8)[:] = 0
     S["ctrl"] = S["mail"].data_ptr(0)
-    S["hx"] = S["mail"].data_ptr(128)
-    S["picks"] = S["mail"].data_ptr(128 + maxbsz * H * 2)
-    S["hout"] = torch.zeros(maxbsz * H, dtype=torch.float32, device=dev)
+    S["hx"] = S["mail"].data_ptr(o_hx)
+    S["picks"] = S["mail"].data_ptr(o_pk)
+    S["hout"] = S["mail"].data_ptr(o_out)
     S["dflag"] = torch.zeros(1, dtype=torch.int64, device=dev)
     S["seqc"] = torch.zeros(1, dtype=torch.int64, device=dev)
     S["stats"] = torch.zeros(8, dtype=torch.int64, device=dev)
@@ -107,7 +112,7 @@ def _fused(x2d, ids, weights, layer, inners, expert_map, limit):
     out = orig(x2d, so.view(ids.shape), wo.view(weights.shape).to(weights.dtype), layer, inners, expert_map, limit)
     if out.dtype != torch.float32 or not out.is_contiguous():
         raise RuntimeError("mi355moe ct_vllm: expected the fp32 contiguous routed accumulator")
-    _lib.call("mm_combine_host", out.data_ptr(), out.numel(), S["dflag"].data_ptr(), S["ctrl"], S["hout"].data_ptr(),
+    _lib.call("mm_combine_host", out.data_ptr(), out.numel(), S["dflag"].data_ptr(), S["ctrl"], S["hout"],
               S["stats"].data_ptr(), S["timeout_ns"], _lib.stream_ptr())
     return out
 

@@ -31,7 +31,8 @@ def _ienv(name, default):
         return int(default)
 
 
-FAT_EXPERT_THRESHOLD = max(0, _ienv("VLLM_EXL3_FAT_THRESHOLD", 256))
+# default: the reference image's value (docker/entrypoint.sh:69); the plugin's own default is 256
+FAT_EXPERT_THRESHOLD = max(0, _ienv("VLLM_EXL3_FAT_THRESHOLD", 32))
 _EXL3_HOST_DMA_MODE = _ienv("EXL3_HOST_DMA", 0)
 _DMA_B = _ienv("EXL3_HOST_DMA_BATCH", 16)
 _DMA_NS = _ienv("EXL3_HOST_DMA_SLOTS", 3)
@@ -261,16 +262,10 @@ def apply_exl3_fused_moe(x2d, ids, weights, layer, inners=None, expert_map=None,
     if (_EXL3_HOST_DMA_MODE > 0 and layer.host_home is not None and getattr(layer, "_exl3_dma", None) is not None
             and T >= _DMA_MIN_TOKENS and inners is None and not torch.cuda.is_current_stream_capturing()):
         return _dma_prefill(x2d, ids, w16, layer, limit, dev)
-    if T <= FAT_EXPERT_THRESHOLD and n <= moe.GEMV_MAX_ROWS:
-        # no expert can exceed the threshold: decode path, no host sync (graph safe)
-        out = torch.empty((T, layer.H), dtype=torch.float32, device=dev)
-        wsb = _lib.load().mm_gemv_workspace(n, layer.E, layer.H, layer.I)
-        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
-        x = x2d.contiguous()
-        _lib.call("mm_moe_decode", L.mm_layer(), x.data_ptr(), moe.x_dtype_of(x), 0, T, k, ids.data_ptr(),
-                  w16.data_ptr(), max(1, n), out.data_ptr(), ws.data_ptr(), wsb, _lib.stream_ptr())
-        return out
-    return moe.moe_forward(L, x2d, ids, w16, fat_threshold=min(FAT_EXPERT_THRESHOLD, moe.GEMV_MAX_ROWS))
+    # at most FAT_EXPERT_THRESHOLD tokens: every route on the decode path (the reference's fat_possible test);
+    # above it the experts with more than FAT_EXPERT_THRESHOLD routes go to the fat-expert GEMM. Both are decided on
+    # the device, so no call synchronises the host and every call can be captured in a graph.
+    return moe.moe_forward(L, x2d, ids, w16, fat_threshold=FAT_EXPERT_THRESHOLD)
 
 
 class Exl3MoEMethod:

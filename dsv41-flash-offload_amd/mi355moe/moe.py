@@ -6,8 +6,11 @@ import torch
 
 from . import _lib
 
-# Routes per expert served by the decode path (larger groups belong to the fat-expert path).
-GEMV_MAX_ROWS = 256
+# Default fat-expert threshold of moe_forward: experts with more routes than this in a call go to the fat-expert
+# grouped GEMM (the reference image's VLLM_EXL3_FAT_THRESHOLD, docker/entrypoint.sh:69).
+FAT_THRESHOLD = 32
+# Routes per call the decode path routes in-kernel (more go through the permutation).
+GEMV_ROUTE_MAX = 1024
 
 
 def _i(t):
@@ -86,33 +89,46 @@ def _with_shared(ids, w, T, shared_expert):
     return ids.contiguous(), w.contiguous()
 
 
-def moe_forward(store, x, ids, w, shared_expert=None, use_permutation=None, fat_threshold=GEMV_MAX_ROWS, stream=None):
+def decode_routes(store, x, ids, w, cap, out=None, rescale=False, stream=None):
+    """out fp32 [T, H] (+)= sum_j w[t, j] * expert_{ids[t, j]}(x_t) over the routes whose expert has at most `cap`
+    routes in the call (the decode path; experts above the cap contribute nothing). ids int64 [T, k], w fp32
+    [T, k]. No host synchronisation: routing is found in-kernel for up to GEMV_ROUTE_MAX routes (k <= 16), else
+    through the permutation."""
+    T, k = ids.shape
+    n = T * k
+    dev = x.device
+    x = x.contiguous()
+    cap = max(1, int(cap))
+    if n <= GEMV_ROUTE_MAX and k <= 16 and out is None:
+        out = torch.empty((T, store.H), dtype=torch.float32, device=dev)
+        wsb = _lib.load().mm_gemv_workspace(n, store.E, store.H, store.I)
+        ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=dev)
+        _lib.call("mm_moe_decode", store.mm_layer(), _i(x), x_dtype_of(x), 1 if rescale else 0, T, k, _i(ids), _i(w),
+                  cap, _i(out), _i(ws), wsb, _lib.stream_ptr(stream))
+        return out
+    routes = permute(ids, w, k, store.E, stream) if n > GEMV_ROUTE_MAX else None
+    # rows of routes above the cap stay zero and add nothing in the combine
+    Y = expert_gemv(store, x, ids, T, n, k, cap, routes, rescale=rescale, stream=stream)
+    return combine(Y, ids, w, T, k, store.H, store.E, out=out, stream=stream)
+
+
+def moe_forward(store, x, ids, w, shared_expert=None, fat_threshold=FAT_THRESHOLD, stream=None):
     """out fp32 [T, H] = sum_j w[t, j] * expert_{ids[t, j]}(x_t) (+ expert `shared_expert` with weight 1).
 
     Routes with ids outside [0, E) contribute nothing. As the reference's fused-MoE call does
-    (patches/vllm-exl3-host-dma.patch:241-290), experts with more than `fat_threshold` routes (at most
-    GEMV_MAX_ROWS) go to the fat-expert grouped GEMM, added to the decode path's sum; the others run on the
-    decode path, whose routing is found in-kernel for up to 1024 routes, else through permute()."""
+    (patches/vllm-exl3-host-dma.patch:241-290), a call of at most `fat_threshold` tokens runs every route on the
+    decode path; a larger call sends the experts with more than `fat_threshold` routes to the fat-expert grouped
+    GEMM and the rest to the decode path. The split is made on the device (no host synchronisation), so every
+    call can be captured in a HIP graph."""
     T = x.shape[0]
     ids, w = _with_shared(ids, w, T, shared_expert)
     k = ids.shape[1]
     n = T * k
-    fat_threshold = min(int(fat_threshold), GEMV_MAX_ROWS)
-    routes = permute(ids, w, k, store.E, stream)
-    counts = routes["counts"][: store.E]
-    max_rows = int(counts.max().item()) if n else 0
-    if max_rows > fat_threshold:
-        valid = (ids >= 0) & (ids < store.E)
-        fat = valid & (counts.long()[ids.clamp(0, store.E - 1)] > fat_threshold)
-        std_ids = ids.masked_fill(fat, -1)
-        out = moe_forward(store, x, std_ids, w, use_permutation=use_permutation, fat_threshold=fat_threshold,
-                          stream=stream) if bool((valid & ~fat).any().item()) else torch.zeros(
-                              (T, store.H), dtype=torch.float32, device=x.device)
-        return moe_prefill(store, x, ids.masked_fill(~fat, -1), w, cap=fat_threshold, out=out, stream=stream)
-    if use_permutation is None:
-        use_permutation = n > 1024
-    Y = expert_gemv(store, x, ids, T, n, k, max(1, max_rows), routes if use_permutation else None, stream=stream)
-    return combine(Y, ids, w, T, k, store.H, store.E, stream=stream)
+    thr = max(0, int(fat_threshold))
+    if T <= thr:
+        return decode_routes(store, x, ids, w, n, stream=stream)
+    out = decode_routes(store, x, ids, w, max(1, thr), stream=stream)
+    return moe_prefill(store, x, ids, w, cap=thr, out=out, stream=stream)
 
 
 def _prefill_ws(store, n, dev):
@@ -158,12 +174,12 @@ class DecodeRunner:
 
     def __init__(self, E, H, I, T, k, device="cuda", shared=True, max_rows=None):
         self.E, self.H, self.I, self.T, self.k0 = E, H, I, T, k
-        # routes per expert: one per token when every token picks distinct experts
-        self.max_rows = T if max_rows is None else max_rows
         self.shared = shared
         self.Eall = E + (1 if shared else 0)
         self.k = k + (1 if shared else 0)
         self.n = T * self.k
+        # the decode path's cap on routes per expert: every route by default
+        self.max_rows = self.n if max_rows is None else max_rows
         dev = torch.device(device)
         self.ids = torch.zeros((T, self.k), dtype=torch.long, device=dev)
         self.w = torch.zeros((T, self.k), dtype=torch.float32, device=dev)

@@ -71,9 +71,10 @@ int mm_split(const int64_t* sel, const float* w, const void* z_fp16, int n, int 
 
 /* Host-partial add; replaces ft_combine (ct/ft_tier_cu_v.cu:145-153): if dflag[0] != 0, wait (bounded by
  * timeout_ns, measured on the GPU's constant-rate clock) until host-mapped ctrl[1] >= dflag[0], then
- * out[i] += hout[i] for i < n. On timeout the partial is dropped and stats[6]++; stats[4] += wait ns,
- * stats[5]++ as in the reference. */
-int mm_combine_host(float* out, int n, const int64_t* dflag, const int64_t* ctrl, const float* hout, int64_t* stats,
+ * out[i] += hout[i] for i < n (hout host-mapped fp32, written by the host worker). On timeout the whole partial
+ * is dropped, dflag[0] is cleared and stats[6]++; stats[4] += wait ns, stats[5]++ as in the reference. One wait
+ * decides for the whole output (the reference's workgroups each wait and decide on their own). */
+int mm_combine_host(float* out, int n, int64_t* dflag, const int64_t* ctrl, const float* hout, int64_t* stats,
                     int64_t timeout_ns, mm_stream_t stream);
 
 /* Bytes of device workspace mm_permute needs for n routes over E experts. */
@@ -132,8 +133,11 @@ size_t mm_gemv_workspace(int n, int E, int H, int I);
  * The expert input of token t is x[t] (x_dtype MM_DTYPE_*) converted to fp16: fp16 input is used as is, other
  * types go through bf16 (RNE); with rescale != 0 the row is first scaled to unit RMS (any type), as
  * mm_prepare_input does. Routes are found in-kernel from ids when offsets is NULL (n <= 1024); otherwise
- * offsets/order/active/nactive from mm_permute over the same routes are used. max_rows bounds the routes of any
- * one expert (<= 256). phases is a mask of the five launches, run in this order on the same workspace:
+ * offsets/order/active/nactive from mm_permute over the same routes are used. max_rows (>= 1) is the fat-expert
+ * threshold of the call: an expert with more than max_rows routes is left to the fat-expert path (its rows stay
+ * untouched here), so a caller can split a call between both paths without reading the counts on the host;
+ * max_rows >= n computes every route. Any number of routes per expert is supported (the trellis is streamed once
+ * per 16 routes of an expert). phases is a mask of the five launches, run in this order on the same workspace:
  * 1 = route prep and input transform, 2 = gate/up partial sums, 4 = gate/up epilogue (output transforms, SwiGLU,
  * down-input transform), 8 = down partial sums, 16 = down epilogue into Y; 31 = the whole expert MLP. */
 int mm_expert_gemv(const mm_layer_t* layer, const void* x, int x_dtype, int rescale, int T, int n, int topk,
@@ -146,7 +150,8 @@ int mm_expert_gemv(const mm_layer_t* layer, const void* x, int x_dtype, int resc
  * with weights w fp32 [T*topk] (topk <= 16, T*topk <= 1024; ids outside [0, E) contribute nothing) ->
  * out fp32 [T][H] = sum_j w[t,j] * expert_{ids[t,j]}(x_t), summed in ascending j with fp32 fma (equal to
  * mm_combine over mm_expert_gemv's rows). x, x_dtype and rescale as for mm_expert_gemv: a chain of layers
- * passes the previous layer's out with MM_DTYPE_F32. */
+ * passes the previous layer's out with MM_DTYPE_F32. max_rows as for mm_expert_gemv: routes of experts with more
+ * than max_rows routes contribute nothing (mm_moe_prefill with cap = max_rows and accumulate = 1 adds them). */
 int mm_moe_decode(const mm_layer_t* layer, const void* x, int x_dtype, int rescale, int T, int topk,
                   const int64_t* ids, const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes,
                   mm_stream_t stream);

@@ -155,7 +155,7 @@ def test_prefill_full_shape_matches_decode_path(dev):
     xd, idd, wd = _t(x16, dev), _t(ids, dev), _t(w, dev)
     print("prefill full shape T=256", flush=True)
     a = moe.moe_prefill(st, xd, idd, wd, shared_expert=E)
-    b = moe.moe_forward(st, xd, idd, wd, shared_expert=E)
+    b = moe.moe_forward(st, xd, idd, wd, shared_expert=E, fat_threshold=T)
     torch.cuda.synchronize()
     a, b = a.cpu().numpy(), b.cpu().numpy()
     ok, m = within_tolerance(a, b.astype(np.float64))

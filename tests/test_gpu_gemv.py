@@ -157,8 +157,8 @@ def test_layer_input_types_and_rescale(dev):
 
 @pytest.mark.parametrize("T,k,E", [(200, 6, 6), (60, 4, 8)])
 def test_many_routes_per_expert_chunks(dev, T, k, E):
-    """Experts with more routes than one MFMA pass (16): through the permutation (> 1024 routes) and through the
-    in-kernel routing."""
+    """Experts with more routes than one MFMA pass (16), all on the decode path: through the permutation (> 1024
+    routes) and through the in-kernel routing."""
     import torch
     from mi355moe import moe
     H, I = 512, 256
@@ -169,7 +169,7 @@ def test_many_routes_per_expert_chunks(dev, T, k, E):
     w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
     x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
     print(f"many routes T={T} k={k} E={E}", flush=True)
-    out = moe.moe_forward(st, _t(x16, dev), _t(ids, dev), _t(w, dev))
+    out = moe.moe_forward(st, _t(x16, dev), _t(ids, dev), _t(w, dev), fat_threshold=T)
     torch.cuda.synchronize()
     ref = OracleLayer(st, seed).forward(x16.astype(np.float32), ids, w)
     ok, m = within_tolerance(out.cpu().numpy(), ref)
@@ -190,3 +190,61 @@ def test_prepare_input_matches_numpy(dev):
     expect = bf.view(np.float32).astype(np.float16)
     got = x16.cpu().numpy()
     assert np.mean(got != expect) < 1e-3 and np.allclose(got, expect, rtol=1e-2)
+
+
+@pytest.mark.parametrize("T,k", [(300, 3), (400, 3)])
+def test_expert_above_256_routes_on_decode_path(dev, T, k):
+    """One expert holds a route of every token (300 routes through the in-kernel routing of mm_moe_decode, 400
+    through the permutation): every route is computed, none is clamped away."""
+    import torch
+    from mi355moe import moe
+    H, I, E = 256, 128, 16
+    seed = 404 + T
+    st = make_store(E, H, I, seed, device=dev)
+    rng = np.random.default_rng(T)
+    ids = np.stack([np.concatenate([[0], 1 + rng.permutation(E - 1)[: k - 1]]) for _ in range(T)]).astype(np.int64)
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
+    assert np.bincount(ids.ravel(), minlength=E)[0] == T
+    print(f"expert with {T} routes, n={T * k}", flush=True)
+    out = moe.moe_forward(st, _t(x16, dev), _t(ids, dev), _t(w, dev), fat_threshold=T)
+    torch.cuda.synchronize()
+    ref = OracleLayer(st, seed).forward(x16.astype(np.float32), ids, w)
+    ok, m = within_tolerance(out.cpu().numpy(), ref)
+    assert ok, m
+
+
+def test_decode_cap_leaves_fat_experts_out(dev):
+    """mm_expert_gemv with max_rows below an expert's count leaves that expert's rows untouched and computes the
+    others; mm_moe_decode leaves them out of the sum."""
+    import torch
+    from mi355moe import _lib, moe
+    H, I, E, T, k = 256, 128, 10, 40, 3
+    seed = 4242
+    st = make_store(E, H, I, seed, device=dev)
+    rng = np.random.default_rng(5)
+    ids = np.stack([np.concatenate([[0], 1 + rng.permutation(E - 1)[: k - 1]]) for _ in range(T)]).astype(np.int64)
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    cap = 30
+    assert counts[0] > cap and counts[1:].max() <= cap
+    n = T * k
+    print("decode cap", counts.tolist(), flush=True)
+    Y = moe.expert_gemv(st, _t(x16, dev), _t(ids, dev), T, n, k, cap)
+    ref_y = OracleLayer(st, seed).per_route(x16.astype(np.float32), ids)
+    Yc = Y.cpu().numpy()
+    fat = (ids.ravel() == 0)
+    assert np.count_nonzero(Yc[fat]) == 0
+    ok, m = within_tolerance(Yc[~fat], ref_y[~fat])
+    assert ok, m
+    wsb = _lib.load().mm_gemv_workspace(n, E, H, I)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    out = torch.empty((T, H), dtype=torch.float32, device=dev)
+    idd, wd, xd = _t(ids, dev), _t(w, dev), _t(x16, dev)
+    _lib.call("mm_moe_decode", st.mm_layer(), xd.data_ptr(), _lib.DTYPE_F16, 0, T, k, idd.data_ptr(), wd.data_ptr(),
+              cap, out.data_ptr(), ws.data_ptr(), wsb, _lib.stream_ptr())
+    torch.cuda.synchronize()
+    ref = OracleLayer(st, seed).forward(x16.astype(np.float32), np.where(ids == 0, -1, ids), w)
+    ok, m = within_tolerance(out.cpu().numpy(), ref)
+    assert ok, m

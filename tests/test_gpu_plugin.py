@@ -118,3 +118,45 @@ def test_expert_cache_synchronous_copies(dev):
         assert slotof[e] == s and int(st._exl3_ptrs["gate_trellis"][e]) == c.pool.row(s)
         assert np.array_equal(c.pool.t[s].cpu().numpy(), rows[e])
     assert all(slotof[e] == -1 for e in (0, 2, 4, 5, 7))
+
+
+@pytest.mark.parametrize("T", [64, 200, 300])
+def test_fused_moe_captured_in_graph(dev, T):
+    """apply_exl3_fused_moe above the fat threshold (decode path with a cap plus the fat-expert GEMM, split on the
+    device) captures into a HIP graph; every replay, with eager work and synchronisations in between, equals the
+    eager call bit for bit, and the eager call matches the oracle."""
+    import torch
+    from mi355moe import exl3
+    H, I, E, k, seed = 256, 256, 12, 4, 6400 + T
+    st = make_store(E, H, I, seed, device=dev, exact=True)
+    rng = np.random.default_rng(T)
+    p = np.array([0.3, 0.2, 0.1, 0.08, 0.07, 0.06, 0.05, 0.04, 0.04, 0.03, 0.02, 0.01])
+    ids = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(T)]).astype(np.int64)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert T > exl3.FAT_EXPERT_THRESHOLD and (counts > exl3.FAT_EXPERT_THRESHOLD).any()
+    assert ((counts > 0) & (counts <= exl3.FAT_EXPERT_THRESHOLD)).any()
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    x = _t(rng.normal(0, 1, (T, H)).astype(np.float32), dev).to(torch.bfloat16)
+    idd, wd = _t(ids, dev), _t(w, dev)
+    print(f"graph capture T={T} counts={counts.tolist()}", flush=True)
+    eager = exl3.apply_exl3_fused_moe(x, idd, wd, st, None, None, 10.0).clone()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        exl3.apply_exl3_fused_moe(x, idd, wd, st, None, None, 10.0)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        cap_out = exl3.apply_exl3_fused_moe(x, idd, wd, st, None, None, 10.0)
+    for r in range(3):
+        cap_out.fill_(float("nan"))
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(cap_out, eager), f"replay {r}"
+        exl3.apply_exl3_fused_moe(x, idd, wd, st, None, None, 10.0)     # eager work between replays
+        torch.cuda.synchronize()
+    x16 = x.half().cpu().numpy().astype(np.float32)
+    ref = OracleLayer(st, seed).forward(x16, ids, w.astype(np.float16).astype(np.float32))
+    ok, m = within_tolerance(eager.cpu().numpy(), ref)
+    assert ok, m

@@ -144,6 +144,7 @@ def test_combine_host_paths(dev):
     assert torch.equal(out, base)
     st = stats.cpu().numpy()
     assert st[6] == 1 and st[5] == 2 and st[4] >= 2_000_000
+    assert int(dflag.item()) == 0          # the one decision: the whole partial dropped
 
 
 @pytest.mark.parametrize("T,k", [(4, 9), (33, 8)])
