@@ -45,6 +45,7 @@ _SIGS = {
     "mm_expert_gemv": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, i32, i32, vp, vp, vp, vp, vp, i32, vp, vp, sz,
                              i32, vp]),
     "mm_moe_decode": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, i32, vp, vp, i32, vp, vp, sz, vp]),
+    "mm_moe_decode_noalloc": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, i32, vp, vp, i32, vp, vp]),
     "mm_prefill_workspace": (sz, [i32, i32, i32, i32]),
     "mm_grouped_gemm": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, i32, vp, vp, sz, vp]),
     "mm_moe_prefill": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, i32, i32, vp, vp, sz, vp]),

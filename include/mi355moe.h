@@ -156,6 +156,20 @@ int mm_moe_decode(const mm_layer_t* layer, const void* x, int x_dtype, int resca
                   const int64_t* ids, const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes,
                   mm_stream_t stream);
 
+/* Bytes of the library's device scratch array behind mm_moe_decode_noalloc (one array per device, held from the
+ * library's load until the process ends). */
+#define MM_NOALLOC_SCRATCH_BYTES ((size_t)64 << 20)
+
+/* mm_moe_decode without a workspace argument. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, kernels and results (bit for bit) as mm_moe_decode; the workspace is a file-scope device array
+ * of MM_NOALLOC_SCRATCH_BYTES per device, and the call allocates nothing. A call whose workspace
+ * (mm_gemv_workspace(T * topk, E, H, I)) exceeds that size fails with MM_ERR_ARG: at most 62 routes per call at
+ * H 4096 / I 2048 (T = 6 at top-8 plus a shared expert), 52 at H 5120 / I 2304. All calls on one device
+ * share its array: calls that overlap on one device (concurrent streams or threads) race. */
+int mm_moe_decode_noalloc(const mm_layer_t* layer, const void* x, int x_dtype, int rescale, int T, int topk,
+                          const int64_t* ids, const float* w, int max_rows, float* out, mm_stream_t stream);
+
 /* ------------------------------------------------------------------------------ fat experts (prefill) */
 
 /* Bytes of device workspace mm_grouped_gemm / mm_moe_prefill need for n routes over E experts (permutation,

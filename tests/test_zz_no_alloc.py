@@ -1,0 +1,55 @@
+"""mm_moe_decode_noalloc (the decode layer on the library's own device scratch) against mm_moe_decode with a
+caller workspace: bit-identical outputs on two calls in a row, the second with fewer routes, and a clear error for
+a call beyond the scratch size."""
+import numpy as np
+import pytest
+
+from helpers import make_store
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _decode(st, x, ids, w, T, k, dev, noalloc):
+    import torch
+    from mi355moe import _lib
+    out = torch.full((T, st.H), float("nan"), dtype=torch.float32, device=dev)
+    if noalloc:
+        _lib.call("mm_moe_decode_noalloc", st.mm_layer(), x.data_ptr(), _lib.DTYPE_BF16, 1, T, k, ids.data_ptr(),
+                  w.data_ptr(), T * k, out.data_ptr(), _lib.stream_ptr())
+    else:
+        wsb = _lib.load().mm_gemv_workspace(T * k, st.E, st.H, st.I)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        _lib.call("mm_moe_decode", st.mm_layer(), x.data_ptr(), _lib.DTYPE_BF16, 1, T, k, ids.data_ptr(), w.data_ptr(),
+                  T * k, out.data_ptr(), ws.data_ptr(), wsb, _lib.stream_ptr())
+    torch.cuda.synchronize()
+    return out
+
+
+def test_noalloc_decode_equals_workspace_decode(dev):
+    import torch
+    from mi355moe import _lib, workload
+    H, I, E = 4096, 2048, 384
+    st = make_store(E + 1, H, I, 7100, device=dev)
+    for T in (6, 2):                     # the second call has fewer routes than the first
+        ids, w = workload.zipf_routing(T, 8, E, seed=7200 + T)
+        ids = np.concatenate([ids, np.full((T, 1), E)], 1)
+        w = np.concatenate([w, np.ones((T, 1), np.float32)], 1)
+        x = _t(workload.activations(T, H, seed=7300 + T), dev).to(torch.bfloat16)
+        idd, wd = _t(ids, dev), _t(w, dev)
+        print(f"noalloc decode T={T} routes={T * 9}", flush=True)
+        a = _decode(st, x, idd, wd, T, 9, dev, noalloc=True)
+        b = _decode(st, x, idd, wd, T, 9, dev, noalloc=False)
+        assert torch.isfinite(a).all()
+        assert torch.equal(a, b), f"T={T}: max diff {(a - b).abs().max().item()}"
+    # beyond the scratch: a clear error, no device work
+    T = 8
+    ids = np.tile(np.arange(9, dtype=np.int64), (T, 1))
+    with pytest.raises(RuntimeError, match="scratch"):
+        _lib.call("mm_moe_decode_noalloc", st.mm_layer(), x.data_ptr(), _lib.DTYPE_BF16, 1, T, 9,
+                  _t(ids, dev).data_ptr(), _t(np.ones((T, 9), np.float32), dev).data_ptr(), T * 9,
+                  torch.empty((T, H), device=dev).data_ptr(), _lib.stream_ptr())
