@@ -109,6 +109,8 @@ struct PrepArgs
     float* xsum;              // [n][2][nb] sums of xa over each workgroup's rows
     int n, topk, E, H, nb, x_dtype, rescale;
     int cap;                  // experts with more than cap routes are left out (no record work, no outputs)
+    int npos;                 // sorted positions visited (n with in-kernel routing; the permutation's valid
+                              // positions must lie below it)
 };
 
 __device__ __forceinline__ int wave_sum_int(int v)
@@ -128,8 +130,17 @@ int prep_blocks(int H);
 void launch_route_prep(const PrepArgs& p, hipStream_t s);
 
 // The launches of mm_moe_decode on a given workspace (argument checks included); `who` names the caller in errors.
+// accumulate: out += the layer sum instead of out = the layer sum.
 int moe_decode_launch(const mm_layer_t* L, const void* x, int x_dtype, int rescale, int T, int topk, const int64_t* ids,
                       const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes,
-                      mm_stream_t stream, const char* who);
+                      mm_stream_t stream, const char* who, int accumulate = 0);
+
+// Decode workspace of n routes whose sorted positions lie below npos, and the decode path over such a
+// permutation (routes of experts above cap left out) added to / written into out; no argument checks.
+size_t decode_ws_bytes(int n, int npos, int E, int H, int I);
+int decode_perm_launch(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids,
+                       const float* w, const int32_t* offsets, const int32_t* order, const int32_t* active,
+                       const int32_t* nactive, int npos, int cap, float* out, int accumulate, void* workspace,
+                       hipStream_t s);
 
 }  // namespace mm

@@ -922,7 +922,7 @@ static FatWs fat_carve(void* base, int n, int E, int H, int I)
 }
 
 static int fat_check(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids, void* ws,
-                     size_t ws_bytes, const char* who)
+                     size_t ws_bytes, const char* who, bool check_ws = true)
 {
     MM_CHECK_ARG(L && L->gate_ptr && L->up_ptr && L->down_ptr && L->suh13 && L->svh13 && L->suh2 && L->svh2,
                  "%s: incomplete layer", who);
@@ -934,6 +934,7 @@ static int fat_check(const mm_layer_t* L, const void* x, int x_dtype, int T, int
     MM_CHECK_ARG(x_dtype == MM_DTYPE_F16 || x_dtype == MM_DTYPE_BF16 || x_dtype == MM_DTYPE_F32,
                  "%s: x_dtype must be MM_DTYPE_F16, MM_DTYPE_BF16 or MM_DTYPE_F32", who);
     MM_CHECK_ARG(T > 0 && topk > 0 && (size_t)T * topk < ((size_t)1 << 30), "%s: bad T/topk", who);
+    if (!check_ws) return MM_OK;
     const size_t need = fat_carve(nullptr, T * topk, L->E, L->H, L->I).bytes;
     MM_CHECK_ARG(ws && ws_bytes >= need, "%s: workspace too small (%zu < %zu)", who, ws_bytes, need);
     return MM_OK;
@@ -1010,11 +1011,110 @@ static FatbWs fatb_carve(void* base, int n, int T, int E, int H, int I)
     return w;
 }
 
+// ------------------------------------------------------------------------------------ the fused-MoE call
+
+// ids_small[s] = ids[s] when its expert has at most cap routes in the call (counts from the fat pass's
+// permutation), else -1: the routes the decode path takes.
+__global__ __launch_bounds__(256) void k_small_ids(const int64_t* __restrict__ ids, const int32_t* __restrict__ counts,
+                                                   int n, int E, int cap, int64_t* __restrict__ ids_small)
+{
+    for (int s = blockIdx.x * blockDim.x + threadIdx.x; s < n; s += gridDim.x * blockDim.x)
+    {
+        const int64_t e = ids[s];
+        ids_small[s] = (e >= 0 && e < E && counts[e] <= cap) ? e : -1;
+    }
+}
+
+// Workspace of mm_fused_moe: the fat pass over all n routes, the decode path's ids and permutation, then the
+// decode workspace with positions bounded by npos.
+struct FusedWs
+{
+    FatWs fat;
+    int64_t* ids_small;   // [n]
+    int32_t* counts;      // [E + 1]  permutation of ids_small
+    int32_t* offsets;     // [E + 2]
+    int32_t* order;       // [n]
+    int32_t* active;      // [E]
+    int32_t* nactive;     // [1]
+    void* pws;
+    size_t pws_bytes;
+    void* dws;            // decode workspace
+    int npos;
+    bool in_kernel;       // decode routing found in-kernel (n <= 1024, topk <= 16)
+    size_t bytes;
+};
+
+static FusedWs fused_carve(void* base, int T, int topk, int E, int H, int I, int cap)
+{
+    auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
+    const int n = T * topk;
+    FusedWs w;
+    w.fat = fat_carve(base, n, E, H, I);
+    w.in_kernel = n <= 1024 && topk <= 16;
+    // every decode-path expert has at most cap routes, so their positions lie below E x cap
+    w.npos = w.in_kernel ? n : (int)std::min<int64_t>(n, (int64_t)E * std::max(cap, 1));
+    w.pws_bytes = mm_permute_workspace(n, E);
+    const size_t sizes[8] = { al((size_t)n * 8), al((size_t)(E + 1) * 4), al((size_t)(E + 2) * 4), al((size_t)n * 4),
+                              al((size_t)E * 4), al(4), al(w.pws_bytes), decode_ws_bytes(n, w.npos, E, H, I) };
+    char* p = base ? static_cast<char*>(base) + w.fat.bytes : nullptr;
+    char* at[8];
+    size_t off = 0;
+    for (int i = 0; i < 8; ++i)
+    {
+        at[i] = p ? p + off : nullptr;
+        off += sizes[i];
+    }
+    w.ids_small = (int64_t*)at[0]; w.counts = (int32_t*)at[1]; w.offsets = (int32_t*)at[2]; w.order = (int32_t*)at[3];
+    w.active = (int32_t*)at[4]; w.nactive = (int32_t*)at[5]; w.pws = at[6]; w.dws = at[7];
+    w.bytes = w.fat.bytes + off;
+    return w;
+}
+
 }  // namespace mm
 
 using namespace mm;
 
 extern "C" {
+
+size_t mm_fused_moe_workspace(int T, int topk, int E, int H, int I, int cap)
+{
+    if (T <= 0 || topk <= 0 || E <= 0 || H <= 0 || I <= 0 || cap < 0) return 0;
+    return fused_carve(nullptr, T, topk, E, H, I, cap).bytes;
+}
+
+int mm_fused_moe(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids, const float* w,
+                 int cap, float* out, void* workspace, size_t workspace_bytes, mm_stream_t stream)
+{
+    const int rc = fat_check(L, x, x_dtype, T, topk, ids, workspace, 0, "mm_fused_moe", false);
+    if (rc) return rc;
+    MM_CHECK_ARG(w && out && cap >= 1, "mm_fused_moe: null pointer or cap < 1");
+    MM_CHECK_ARG(topk <= 16, "mm_fused_moe: topk must be at most 16");
+    const int n = T * topk, E = L->E;
+    const FusedWs ws = fused_carve(workspace, T, topk, E, L->H, L->I, cap);
+    // the decode path's per-position inputs are addressed with 32-bit buffer offsets
+    MM_CHECK_ARG((size_t)ws.npos * 2 * std::max(L->H, L->I) * 2 < ((size_t)1 << 31),
+                 "mm_fused_moe: too many decode-path positions (%d)", ws.npos);
+    MM_CHECK_ARG(workspace && workspace_bytes >= ws.bytes, "mm_fused_moe: workspace too small (%zu < %zu)",
+                 workspace_bytes, ws.bytes);
+    hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+    // 1. experts above cap on the grouped GEMM: out = their weighted sum (every token written)
+    int r = fat_run(L, x, x_dtype, T, topk, ids, cap, ws.fat, s, true);
+    if (r) return r;
+    const dim3 cgrid((unsigned)((L->H / 4 + 255) / 256), (unsigned)T);
+    hipLaunchKernelGGL(k_fat_combine, cgrid, dim3(256), 0, s, out, reinterpret_cast<const uint16_t*>(ws.fat.Y), ids, w,
+                       ws.fat.counts, T, topk, L->H, E, cap, 0);
+    // 2. the others on the decode path, added per token in ascending route order
+    hipLaunchKernelGGL(k_small_ids, dim3((unsigned)std::min((n + 255) / 256, 1024)), dim3(256), 0, s, ids,
+                       ws.fat.counts, n, E, cap, ws.ids_small);
+    if (ws.in_kernel)
+        return moe_decode_launch(L, x, x_dtype, 0, T, topk, ws.ids_small, w, cap, out, ws.dws,
+                                 decode_ws_bytes(n, n, E, L->H, L->I), stream, "mm_fused_moe", 1);
+    r = permute_launch(ws.ids_small, nullptr, n, topk, E, ws.counts, ws.offsets, ws.order, nullptr, nullptr, nullptr,
+                       ws.active, ws.nactive, nullptr, ws.pws, ws.pws_bytes, s);
+    if (r) return r;
+    return decode_perm_launch(L, x, x_dtype, T, topk, ws.ids_small, w, ws.offsets, ws.order, ws.active, ws.nactive,
+                              ws.npos, cap, out, 1, ws.dws, s);
+}
 
 size_t mm_prefill_workspace(int n, int E, int H, int I)
 {

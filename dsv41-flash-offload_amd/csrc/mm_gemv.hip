@@ -229,8 +229,8 @@ struct PartArgs
     const ExpertRec* rec;
     const int32_t* counts;
     const uint16_t* xa;       // mode 0: [n][2][K]; mode 1: [n][K] (operand order)
-    float* part;              // [pieces][n][nmat][N]
-    int n, K, N, ncb, cap;
+    float* part;              // [pieces][npos][nmat][N]
+    int npos, K, N, ncb, cap; // npos: sorted positions the workspace holds
 };
 
 template <int MODE, bool EXACT>
@@ -253,7 +253,7 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
     const int KT = a.K / 16, NT = a.N / 16;
     const uint32_t row_bytes = (uint32_t)NT * 96;
     const uint32_t wbytes = (uint32_t)KT * row_bytes;                   // one matrix
-    const uint32_t xbytes = (uint32_t)((size_t)a.n * NMAT * a.K * 2);   // the input array
+    const uint32_t xbytes = (uint32_t)((size_t)a.npos * NMAT * a.K * 2);   // the input array
     const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.xa), (short)0,
                                                                           (int)xbytes, 0x00020000);
     // lane constants of the decode
@@ -371,7 +371,7 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
                     if (p8 + q < nr)
                     {
                         const uint4 v4 = *reinterpret_cast<const uint4*>(&stage[128 * q + c4]);
-                        float* dst = a.part + ((size_t)(piece * a.n + first + r0 + p8 + q) * NMAT + m) * a.N +
+                        float* dst = a.part + ((size_t)(piece * a.npos + first + r0 + p8 + q) * NMAT + m) * a.N +
                                      cb * GV_COLS + c4;
                         *reinterpret_cast<uint4*>(dst) = v4;
                     }
@@ -440,7 +440,7 @@ struct GuEpiArgs
     const uint16_t* suh2;     // [E][I]
     uint16_t* xd;             // [n][I] fp16 in operand order
     float* xdsum;             // [n][I / 128] sums of xd over each 128-column block
-    int n, I, nb, nwaves, cap, affine;
+    int npos, I, nb, nwaves, cap, affine;
     float limit;
 };
 
@@ -455,7 +455,7 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     // round trip 1: the counts and the position's expert (read before the range check: only the last
     // workgroup's spare waves are past n, and they read position n - 1)
     const int nvalid = a.counts[1], nact = a.counts[0];
-    const int e = a.e_at[min(pos, a.n - 1)];
+    const int e = a.e_at[min(pos, a.npos - 1)];
     if (pos >= nvalid || e < 0) return;      // past the routes, or a route of an expert above the cap
     const int pps = pieces_per_segment(a.nwaves, nact * 2 * ncb, a.cap);
     const int c = cb * GV_COLS;
@@ -475,7 +475,7 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     }
     const float* const pgu[2] = { a.part + ((size_t)pos * 2 + 0) * a.I + c, a.part + ((size_t)pos * 2 + 1) * a.I + c };
     float s0[2] = { 0.f, 0.f }, s1[2] = { 0.f, 0.f };
-    sum_pieces<2>(pgu, (size_t)a.n * 2 * a.I, pps, lane, s0, s1);
+    sum_pieces<2>(pgu, (size_t)a.npos * 2 * a.I, pps, lane, s0, s1);
     float ga = s0[0], gb = s1[0], ua = s0[1], ub = s1[1];
     if (a.affine)
     {
@@ -514,7 +514,8 @@ struct DEpiArgs
     const uint16_t* svh2;     // [E][H]
     float* Y;                 // [n][H] (per-route rows)
     float* out;               // [T][H] (combine)
-    int n, H, I, topk, nwaves, cap, affine;
+    int npos, H, I, topk, nwaves, cap, affine;
+    int accumulate;           // combine: out += the sum instead of out = the sum
 };
 
 // Down output of one (sorted position, 128-column block of H): row ranges added in order (then the AFFINE
@@ -531,7 +532,7 @@ __device__ __forceinline__ void down_block(const DEpiArgs& a, int nact, int pos,
     float sx = a.affine ? wave_sum_first(xs, a.I / GV_COLS, lane) : 0.f;
     const float* const pd[1] = { a.part + (size_t)pos * a.H + c };
     float s0[1] = { 0.f }, s1[1] = { 0.f };
-    sum_pieces<1>(pd, (size_t)a.n * a.H, pps, lane, s0, s1);
+    sum_pieces<1>(pd, (size_t)a.npos * a.H, pps, lane, s0, s1);
     ya = s0[0];
     yb = s1[0];
     if (a.affine)
@@ -552,7 +553,7 @@ __global__ __launch_bounds__(256) void k_down_y(DEpiArgs a)
     const int ncb = a.H / GV_COLS;
     const int pos = item / ncb, cb = item % ncb;
     const int nvalid = a.counts[1], nact = a.counts[0];
-    const int pc = min(pos, a.n - 1);
+    const int pc = min(pos, a.npos - 1);
     const int s = a.route_at[pc], e = a.e_at[pc];
     if (pos >= nvalid || e < 0) return;
     const int c = cb * GV_COLS;
@@ -596,10 +597,11 @@ __global__ __launch_bounds__(1024) void k_down_combine(DEpiArgs a)
     __syncthreads();
     for (int h = threadIdx.x; h < GV_COLS; h += blockDim.x)
     {
-        float o = 0.0f;
+        float* dst = a.out + (size_t)t * a.H + c + h;
+        float o = a.accumulate ? *dst : 0.0f;
         for (int jj = 0; jj < a.topk; ++jj)
             if (ok[jj]) o = fmaf(wj[jj], ys[jj][h], o);
-        a.out[(size_t)t * a.H + c + h] = o;
+        *dst = o;
     }
 }
 
@@ -625,7 +627,7 @@ int prep_blocks(int H) { return (H + PREP_ROWS - 1) / PREP_ROWS; }
 
 void launch_route_prep(const PrepArgs& p, hipStream_t s)
 {
-    const dim3 grid(2 * p.n * p.nb), block(256);
+    const dim3 grid(2 * p.npos * p.nb), block(256);
     if (p.x_dtype == MM_DTYPE_F16)
         hipLaunchKernelGGL(k_route_prep<MM_DTYPE_F16>, grid, block, 0, s, p);
     else if (p.x_dtype == MM_DTYPE_BF16)
@@ -641,14 +643,16 @@ static int piece_cap(int n)
     return c > 32 ? 32 : (c < 4 ? 4 : c);
 }
 
-static Ws carve(void* base, int n, int E, int H, int I)
+// Workspace of n routes whose sorted positions lie below npos (npos = n unless a caller bounds the positions).
+static Ws carve(void* base, int n, int npos, int E, int H, int I)
 {
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
-    const size_t na = (size_t)(n < E ? n : E), cap = (size_t)piece_cap(n);
-    const size_t sizes[11] = { al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al((size_t)n * 4),
-                               al((size_t)n * 4), al((size_t)n * 2 * H * 2), al((size_t)n * 2 * prep_blocks(H) * 4),
-                               al(cap * n * 2 * I * 4), al((size_t)n * I * 2), al((size_t)n * (I / GV_COLS) * 4),
-                               al(cap * n * H * 4) };
+    const size_t m = (size_t)npos;
+    const size_t na = (size_t)(npos < E ? npos : E), cap = (size_t)piece_cap(npos);
+    const size_t sizes[11] = { al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al(m * 4),
+                               al(m * 4), al(m * 2 * H * 2), al(m * 2 * prep_blocks(H) * 4),
+                               al(cap * m * 2 * I * 4), al(m * I * 2), al(m * (I / GV_COLS) * 4),
+                               al(cap * m * H * 4) };
     char* p = static_cast<char*>(base);
     char* at[11];
     size_t off = 0;
@@ -697,28 +701,35 @@ static int check_common(const mm_layer_t* L, const void* x, int x_dtype, int T, 
     const bool perm = offsets != nullptr;
     MM_CHECK_ARG(perm ? (order && active && nactive) : n <= GV_ROUTE_MAX,
                  "%s: more than %d routes need the permutation (offsets, order, active, nactive)", who, GV_ROUTE_MAX);
-    const size_t need = carve(nullptr, n, L->E, L->H, L->I).bytes;
+    const size_t need = carve(nullptr, n, n, L->E, L->H, L->I).bytes;
     MM_CHECK_ARG(ws && ws_bytes >= need, "%s: workspace too small (%zu < %zu)", who, ws_bytes, need);
     return MM_OK;
 }
 
-static void launch_prep(const mm_layer_t* L, const Ws& w, const void* x, int x_dtype, int rescale, int n, int topk,
-                        const int64_t* ids, const int32_t* offsets, const int32_t* order, const int32_t* active,
-                        const int32_t* nactive, int cap, hipStream_t s)
+__global__ __launch_bounds__(256) void k_fill_pos(int32_t* p, int n)
+{
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n; i += gridDim.x * blockDim.x) p[i] = -1;
+}
+
+static void launch_prep(const mm_layer_t* L, const Ws& w, const void* x, int x_dtype, int rescale, int n, int npos,
+                        int topk, const int64_t* ids, const int32_t* offsets, const int32_t* order,
+                        const int32_t* active, const int32_t* nactive, int cap, hipStream_t s)
 {
     const int nb = prep_blocks(L->H);
+    // positions past npos are not visited: their routes' pos_of must read "no position"
+    if (npos < n) hipLaunchKernelGGL(k_fill_pos, dim3((unsigned)min((n + 255) / 256, 1024)), dim3(256), 0, s, w.pos_of, n);
     PrepArgs p{ x, ids, offsets, order, active, nactive, L->gate_ptr, L->up_ptr, L->down_ptr, L->suh13,
                 w.rec, w.counts, w.pos_of, w.route_at, w.e_at, w.xa, w.xsum, n, topk, L->E, L->H, nb, x_dtype, rescale,
-                cap };
+                cap, npos };
     launch_route_prep(p, s);
 }
 
 template <int MODE>
-static void launch_partial(const mm_layer_t* L, const Ws& w, int n, hipStream_t s)
+static void launch_partial(const mm_layer_t* L, const Ws& w, int npos, hipStream_t s)
 {
     const int K = MODE == 0 ? L->H : L->I, N = MODE == 0 ? L->I : L->H;
-    PartArgs p{ w.rec, w.counts, MODE == 0 ? w.xa : w.xd, MODE == 0 ? w.part_gu : w.part_d, n, K, N, N / GV_COLS,
-                piece_cap(n) };
+    PartArgs p{ w.rec, w.counts, MODE == 0 ? w.xa : w.xd, MODE == 0 ? w.part_gu : w.part_d, npos, K, N, N / GV_COLS,
+                piece_cap(npos) };
     const dim3 grid(partial_waves() / GV_WAVES), block(GV_THREADS);
     if (L->flags & MM_LAYER_EXACT)
         hipLaunchKernelGGL((k_partial<MODE, true>), grid, block, 0, s, p);
@@ -726,24 +737,24 @@ static void launch_partial(const mm_layer_t* L, const Ws& w, int n, hipStream_t 
         hipLaunchKernelGGL((k_partial<MODE, false>), grid, block, 0, s, p);
 }
 
-static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int n, hipStream_t s)
+static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int npos, hipStream_t s)
 {
-    GuEpiArgs g{ w.part_gu, w.xsum, w.counts, w.e_at, L->svh13, L->suh2, w.xd, w.xdsum, n, L->I,
-                 prep_blocks(L->H), partial_waves(), piece_cap(n), (L->flags & MM_LAYER_EXACT) ? 0 : 1, L->limit };
-    hipLaunchKernelGGL(k_gu_epilogue, dim3((n * (L->I / GV_COLS) + 3) / 4), dim3(256), 0, s, g);
+    GuEpiArgs g{ w.part_gu, w.xsum, w.counts, w.e_at, L->svh13, L->suh2, w.xd, w.xdsum, npos, L->I,
+                 prep_blocks(L->H), partial_waves(), piece_cap(npos), (L->flags & MM_LAYER_EXACT) ? 0 : 1, L->limit };
+    hipLaunchKernelGGL(k_gu_epilogue, dim3((npos * (L->I / GV_COLS) + 3) / 4), dim3(256), 0, s, g);
 }
 
-static DEpiArgs down_args(const mm_layer_t* L, const Ws& w, int n, int topk, const int64_t* ids, const float* wt,
-                          float* Y, float* out)
+static DEpiArgs down_args(const mm_layer_t* L, const Ws& w, int npos, int topk, const int64_t* ids, const float* wt,
+                          float* Y, float* out, int accumulate)
 {
-    return DEpiArgs{ w.part_d, w.xdsum, w.counts, w.pos_of, w.route_at, w.e_at, ids, wt, L->svh2, Y, out, n, L->H, L->I, topk,
-                     partial_waves(), piece_cap(n), (L->flags & MM_LAYER_EXACT) ? 0 : 1 };
+    return DEpiArgs{ w.part_d, w.xdsum, w.counts, w.pos_of, w.route_at, w.e_at, ids, wt, L->svh2, Y, out, npos, L->H,
+                     L->I, topk, partial_waves(), piece_cap(npos), (L->flags & MM_LAYER_EXACT) ? 0 : 1, accumulate };
 }
 
 // One decode layer (mm_moe_decode) on a caller-provided workspace; `who` names the entry point in errors.
 int moe_decode_launch(const mm_layer_t* L, const void* x, int x_dtype, int rescale, int T, int topk, const int64_t* ids,
                       const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes,
-                      mm_stream_t stream, const char* who)
+                      mm_stream_t stream, const char* who, int accumulate)
 {
     MM_CHECK_ARG(topk > 0 && topk <= MAX_TOPK, "%s: topk must be in [1, %d]", who, MAX_TOPK);
     const int n = T * topk;
@@ -752,15 +763,36 @@ int moe_decode_launch(const mm_layer_t* L, const void* x, int x_dtype, int resca
     if (rc) return rc;
     MM_CHECK_ARG(w && out, "%s: null pointer", who);
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const Ws ws = carve(workspace, n, L->E, L->H, L->I);
-    launch_prep(L, ws, x, x_dtype, rescale, n, topk, ids, nullptr, nullptr, nullptr, nullptr, max_rows, s);
+    const Ws ws = carve(workspace, n, n, L->E, L->H, L->I);
+    launch_prep(L, ws, x, x_dtype, rescale, n, n, topk, ids, nullptr, nullptr, nullptr, nullptr, max_rows, s);
     launch_partial<0>(L, ws, n, s);
     launch_gu_epilogue(L, ws, n, s);
     launch_partial<1>(L, ws, n, s);
     const int threads = 64 * (topk < 2 ? 2 : topk);
     hipLaunchKernelGGL(k_down_combine, dim3(T * (L->H / GV_COLS)), dim3(threads), 0, s,
-                       down_args(L, ws, n, topk, ids, w, nullptr, out));
+                       down_args(L, ws, n, topk, ids, w, nullptr, out, accumulate));
     return check_launch(who);
+}
+
+size_t decode_ws_bytes(int n, int npos, int E, int H, int I) { return carve(nullptr, n, npos, E, H, I).bytes; }
+
+// The decode path of a call on a permutation whose valid positions lie below npos (every expert <= cap routes
+// there), summed per token into out (out += with accumulate). Arguments are checked by the caller.
+int decode_perm_launch(const mm_layer_t* L, const void* x, int x_dtype, int T, int topk, const int64_t* ids,
+                       const float* w, const int32_t* offsets, const int32_t* order, const int32_t* active,
+                       const int32_t* nactive, int npos, int cap, float* out, int accumulate, void* workspace,
+                       hipStream_t s)
+{
+    const int n = T * topk;
+    const Ws ws = carve(workspace, n, npos, L->E, L->H, L->I);
+    launch_prep(L, ws, x, x_dtype, 0, n, npos, topk, ids, offsets, order, active, nactive, cap, s);
+    launch_partial<0>(L, ws, npos, s);
+    launch_gu_epilogue(L, ws, npos, s);
+    launch_partial<1>(L, ws, npos, s);
+    const int threads = 64 * (topk < 2 ? 2 : topk);
+    hipLaunchKernelGGL(k_down_combine, dim3(T * (L->H / GV_COLS)), dim3(threads), 0, s,
+                       down_args(L, ws, npos, topk, ids, w, nullptr, out, accumulate));
+    return check_launch("decode path");
 }
 
 }  // namespace mm
@@ -772,7 +804,7 @@ extern "C" {
 size_t mm_gemv_workspace(int n, int E, int H, int I)
 {
     if (n <= 0 || E <= 0 || H <= 0 || I <= 0) return 0;
-    return carve(nullptr, n, E, H, I).bytes;
+    return carve(nullptr, n, n, E, H, I).bytes;
 }
 
 int mm_expert_gemv(const mm_layer_t* L, const void* x, int x_dtype, int rescale, int T, int n, int topk,
@@ -786,14 +818,14 @@ int mm_expert_gemv(const mm_layer_t* L, const void* x, int x_dtype, int rescale,
     if (rc) return rc;
     MM_CHECK_ARG(Y || !(phases & 16), "mm_expert_gemv: null Y");
     hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-    const Ws w = carve(workspace, n, L->E, L->H, L->I);
-    if (phases & 1) launch_prep(L, w, x, x_dtype, rescale, n, topk, ids, offsets, order, active, nactive, max_rows, s);
+    const Ws w = carve(workspace, n, n, L->E, L->H, L->I);
+    if (phases & 1) launch_prep(L, w, x, x_dtype, rescale, n, n, topk, ids, offsets, order, active, nactive, max_rows, s);
     if (phases & 2) launch_partial<0>(L, w, n, s);
     if (phases & 4) launch_gu_epilogue(L, w, n, s);
     if (phases & 8) launch_partial<1>(L, w, n, s);
     if (phases & 16)
         hipLaunchKernelGGL(k_down_y, dim3((n * (L->H / GV_COLS) + 3) / 4), dim3(256), 0, s,
-                           down_args(L, w, n, topk, ids, nullptr, Y, nullptr));
+                           down_args(L, w, n, topk, ids, nullptr, Y, nullptr, 0));
     return check_launch("mm_expert_gemv");
 }
 
@@ -801,7 +833,7 @@ int mm_moe_decode(const mm_layer_t* L, const void* x, int x_dtype, int rescale, 
                   const float* w, int max_rows, float* out, void* workspace, size_t workspace_bytes, mm_stream_t stream)
 {
     return mm::moe_decode_launch(L, x, x_dtype, rescale, T, topk, ids, w, max_rows, out, workspace, workspace_bytes,
-                                 stream, "mm_moe_decode");
+                                 stream, "mm_moe_decode", 0);
 }
 
 }  // extern "C"

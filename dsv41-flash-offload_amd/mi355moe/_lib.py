@@ -49,6 +49,8 @@ _SIGS = {
     "mm_prefill_workspace": (sz, [i32, i32, i32, i32]),
     "mm_grouped_gemm": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, i32, vp, vp, sz, vp]),
     "mm_moe_prefill": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, i32, i32, vp, vp, sz, vp]),
+    "mm_fused_moe_workspace": (sz, [i32, i32, i32, i32, i32, i32]),
+    "mm_fused_moe": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, i32, vp, vp, sz, vp]),
     "mm_fat_batched_workspace": (sz, [i32, i32, i32, i32, i32]),
     "mm_fat_batched": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, vp, vp, i32, vp, vp, sz, vp]),
     "mm_slot_point": (i32, [vp, vp, vp, vp, i32, vp, i32, vp]),

@@ -127,8 +127,24 @@ def moe_forward(store, x, ids, w, shared_expert=None, fat_threshold=FAT_THRESHOL
     thr = max(0, int(fat_threshold))
     if T <= thr:
         return decode_routes(store, x, ids, w, n, stream=stream)
-    out = decode_routes(store, x, ids, w, max(1, thr), stream=stream)
-    return moe_prefill(store, x, ids, w, cap=thr, out=out, stream=stream)
+    if thr == 0 or k > 16:
+        return moe_prefill(store, x, ids, w, cap=thr, stream=stream)
+    return fused_moe(store, x, ids, w, thr, stream=stream)
+
+
+def fused_moe(store, x, ids, w, cap, stream=None):
+    """mm_fused_moe: out fp32 [T, H] over ids [T, k] / w [T, k], experts with more than `cap` routes on the
+    grouped GEMM and the others on the decode path, split on the device."""
+    T, k = ids.shape
+    x = x.contiguous()
+    ids = ids.contiguous().long()
+    w = w.contiguous().float()
+    wsb = _lib.load().mm_fused_moe_workspace(T, k, store.E, store.H, store.I, int(cap))
+    ws = torch.empty(max(wsb, 1), dtype=torch.uint8, device=x.device)
+    out = torch.empty((T, store.H), dtype=torch.float32, device=x.device)
+    _lib.call("mm_fused_moe", store.mm_layer(), _i(x), x_dtype_of(x), T, k, _i(ids), _i(w), int(cap), _i(out), _i(ws),
+              wsb, _lib.stream_ptr(stream))
+    return out
 
 
 def _prefill_ws(store, n, dev):

@@ -194,6 +194,18 @@ int mm_moe_prefill(const mm_layer_t* layer, const void* x, int x_dtype, int T, i
                    const float* w, int cap, int accumulate, float* out, void* workspace, size_t workspace_bytes,
                    mm_stream_t stream);
 
+/* The fused-MoE call of a prefill-sized batch (patches/vllm-exl3-host-dma.patch:241-449: experts with more than
+ * the fat threshold routes through the fat-expert GEMM, patch:286-291,450-460, the others through the fused
+ * group kernel), with the split made on the device: out fp32 [T][H] = sum_j w[t,j] * expert_{ids[t,j]}(x_t) over
+ * the valid routes, where experts with more than cap routes run on the grouped GEMM (fp16-rounded weights, as the
+ * reference's reconstruct) and the others on the decode path (the layer's codebook evaluation), each token's
+ * decode-path routes added in ascending j onto its fat-expert sum. No host synchronisation: the call can be
+ * captured. ids int64 [T*topk], w fp32 [T*topk], topk <= 16, cap >= 1; x as for mm_moe_prefill. Workspace:
+ * mm_fused_moe_workspace(T, topk, E, H, I, cap) bytes. */
+size_t mm_fused_moe_workspace(int T, int topk, int E, int H, int I, int cap);
+int mm_fused_moe(const mm_layer_t* layer, const void* x, int x_dtype, int T, int topk, const int64_t* ids,
+                 const float* w, int cap, float* out, void* workspace, size_t workspace_bytes, mm_stream_t stream);
+
 /* ----------------------------------------------------------------------------------------- utility */
 
 /* Fat-expert path on routes already sorted by expert, with the argument meaning of the reference's

@@ -8,7 +8,8 @@ sequence of explicit passes over every (layer, expert) pair, without the product
                                          residency order), free slots popped from the end of the list, eviction
                                          only when the newcomer's score exceeds HYST x the victim's
   release()      ct/ct_vllm.py:394-416   the resident set kept in residency order, every slot given back
-  rewarm(N)      ct/ct_vllm.py:419-436   kept set re-admitted in descending score onto a fresh slot list
+  rewarm(N)      ct/ct_vllm.py:419-436   kept set re-admitted in descending score (ties in residency order) onto
+                                         a fresh slot list
 
 Ties in score (which the reference leaves to torch.topk and to set iteration order) are broken here toward the
 lower flat index (layer * E + expert); the tests use tie-free scores. The planner is pinned by invariants that do
@@ -79,7 +80,9 @@ class ECOracle:
     def rewarm(self, N):
         self.N = N
         self.free = list(range(N))
-        keep = sorted(self.keep, key=lambda i: (-self.score[i], i))[:N]
+        # descending score; equal scores keep their residency order (the reference's stable sort of the kept
+        # list, ct/ct_vllm.py:421)
+        keep = sorted(self.keep, key=lambda i: -self.score[i])[:N]
         admitted = []
         for i in keep:
             s = self.free[-1]

@@ -19,6 +19,7 @@ What each function restates (paths relative to the reference checkout) and how i
   split            ct/ft_tier_cu_v.cu:16-101             pinned: brute-force argmin over k + set invariants
   permute          patch:204-236,296-312                 pinned: numpy stable argsort + bincount
   combine          ct/ft_tier_cu_v.cu:103-127            pinned: closed form (numpy einsum in float64)
+  prepare_input    build's decode-chain step (no ref.)   pinned: bf16 RNE against hand-computed tie cases + numpy
   synth_u16        build's synthetic generator           pinned: golden checksum + GPU fill agreement
   ec (ec_oracle)   ct/ct_vllm.py:243-427                 pinned: invariants (see tests/test_ec.py)
 """
@@ -246,6 +247,27 @@ def combine(out, Y, w, hout=None):
 
 
 # ---------------------------------------------------------------------------------------------- metrics
+def bf16_rne(x):
+    """float32 -> nearest bfloat16 value (ties to even), as float32."""
+    u = _c(x, np.float32).view(np.uint32).astype(np.uint64)
+    u = ((u + 0x7FFF + ((u >> 16) & 1)) & 0xFFFF0000).astype(np.uint32)
+    return u.view(np.float32)
+
+
+def prepare_input(x, rescale=True):
+    """The decode-chain workload's step between layers (a definition of this build's benchmark, not of the
+    reference): each row scaled to unit RMS (scale 1 / sqrt(mean(x^2)) in float64, applied in fp32), rounded to
+    bf16 (RNE), then to fp16. Returns the fp16 values as float32 [T, H]."""
+    x = np.asarray(x, np.float64)
+    if rescale:
+        ms = np.mean(x * x, axis=1, keepdims=True)
+        s = np.where(ms > 0, 1.0 / np.sqrt(np.where(ms > 0, ms, 1.0)), 1.0)
+        y = x.astype(np.float32) * s.astype(np.float32)
+    else:
+        y = x.astype(np.float32)
+    return bf16_rne(y).astype(np.float16).astype(np.float32)
+
+
 def tolerance_metrics(a, b):
     """(max|a-b| / RMS(b), sum|a-b| / sum|b|) in float64 over the whole output."""
     a = np.asarray(a, np.float64)

@@ -15,18 +15,24 @@ def make_store(E, H, I, layer_seed, device="cuda", limit=10.0, exact=False):
 class OracleLayer:
     """Oracle of one layer whose experts come from the synthetic generator (trellis) and the store's scales."""
 
-    def __init__(self, store, layer_seed):
+    def __init__(self, store, layer_seed, cache=True):
+        """layer_seed: the synthetic trellis stream of the layer's experts (the scales come from `store`).
+        cache=False decodes each expert afresh and keeps nothing (100 MB per expert at 4096/2048)."""
         self.store, self.seed = store, layer_seed
         self.H, self.I = store.H, store.I
+        self.keep = cache
         self._cache = {}
 
     def expert(self, e):
-        if e not in self._cache:
-            tr = O.synth_expert_trellis(self.seed, e, self.H, self.I)
-            s = self.store.scales_numpy(e)
-            self._cache[e] = O.DenseExpert(*tr, s["w13_suh"][0], s["w13_svh"][0], s["w13_suh"][1], s["w13_svh"][1],
-                                           s["w2_suh"], s["w2_svh"], self.H, self.I)
-        return self._cache[e]
+        if e in self._cache:
+            return self._cache[e]
+        tr = O.synth_expert_trellis(self.seed, e, self.H, self.I)
+        s = self.store.scales_numpy(e)
+        d = O.DenseExpert(*tr, s["w13_suh"][0], s["w13_svh"][0], s["w13_suh"][1], s["w13_svh"][1], s["w2_suh"],
+                          s["w2_svh"], self.H, self.I)
+        if self.keep:
+            self._cache[e] = d
+        return d
 
     def forward(self, x16, ids, w, limit=10.0):
         """float64 out [T, H] = sum_j w * expert(x) over valid routes (x16: fp16-valued fp32 [T, H])."""

@@ -195,3 +195,32 @@ def test_prefill_16k_tokens_deterministic_and_sampled(dev):
     ok, m = within_tolerance(a.cpu().numpy()[rows], ref)
     print("16k sampled", m, flush=True)
     assert ok, m
+
+
+@pytest.mark.parametrize("T,k,E,cap", [(600, 4, 40, 32), (90, 6, 24, 20)])
+def test_fused_moe_device_split_vs_oracle(dev, T, k, E, cap):
+    """mm_fused_moe: experts above cap on the grouped GEMM, the rest on the decode path, split on the device --
+    through the decode path's permutation (2,400 routes, positions bounded by E x cap) and its in-kernel routing
+    (540 routes)."""
+    import torch
+    from mi355moe import moe
+    H, I = 512, 256
+    seed = 7700 + T
+    st = make_store(E, H, I, seed, device=dev)
+    rng = np.random.default_rng(T)
+    p = np.concatenate([np.full(E // 4, 3.0), np.ones(E - E // 4)])
+    p /= p.sum()
+    ids = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(T)]).astype(np.int64)
+    ids[::11, 1] = -1
+    counts = np.bincount(ids[ids >= 0], minlength=E)
+    assert (counts > cap).any() and ((counts > 0) & (counts <= cap)).any()
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
+    print(f"fused device split T={T} k={k} counts={counts.tolist()}", flush=True)
+    out = moe.fused_moe(st, _t(x16, dev), _t(ids, dev), _t(w, dev), cap)
+    again = moe.fused_moe(st, _t(x16, dev), _t(ids, dev), _t(w, dev), cap)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again)
+    ref = OracleLayer(st, seed).forward(x16.astype(np.float32), ids, w)
+    ok, m = within_tolerance(out.cpu().numpy(), ref)
+    assert ok, m

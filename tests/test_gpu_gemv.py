@@ -189,7 +189,14 @@ def test_prepare_input_matches_numpy(dev):
     bf = (scaled.view(np.uint32) + 0x7FFF + ((scaled.view(np.uint32) >> 16) & 1)) & 0xFFFF0000
     expect = bf.view(np.float32).astype(np.float16)
     got = x16.cpu().numpy()
-    assert np.mean(got != expect) < 1e-3 and np.allclose(got, expect, rtol=1e-2)
+    # the scale is 1 / sqrt(mean(x^2)) in fp32 on the GPU and in float64 here; the two can differ in the last bit, so
+    # a value within an fp32 ulp of a bf16 rounding tie may round to the neighbouring bf16 value (about 2^-16 of
+    # the elements): at most a handful, each one bf16 ulp away
+    bad = np.nonzero(got != expect)[0] if got.ndim == 1 else np.argwhere(got != expect)
+    assert len(bad) <= 4, len(bad)
+    for idx in map(tuple, np.atleast_2d(bad)):
+        e = float(expect[idx])
+        assert abs(float(got[idx]) - e) <= abs(e) * 2.0 ** -7, (idx, float(got[idx]), e)
 
 
 @pytest.mark.parametrize("T,k", [(300, 3), (400, 3)])

@@ -1,0 +1,217 @@
+"""Parity of the workloads the benchmark runs, at their full shapes: the 16k-token prefill layer on its skewed
+routing through both prefill entries, a chain of full-shape decode layers with the unit-RMS step between them,
+and the served DSV41 expert shape (H 5120, I 2304, top-6) on the decode and the fat-expert paths."""
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import OracleLayer, make_store, within_tolerance
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(a, dev):
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(a)).to(dev)
+
+
+def _tiles(c):
+    """Route tiles of an expert with c routes on the fat path: c // 256 tiles of 256, then a remainder above 128
+    in one more 256-route tile, else a 128-route tile. Returns [(first route, routes)]."""
+    out, r0 = [], 0
+    for _ in range(c // 256):
+        out.append((r0, 256))
+        r0 += 256
+    if c - r0 > 0:
+        out.append((r0, c - r0))
+    return out
+
+
+def test_prefill_16k_skewed_routing_both_entries(dev):
+    """The benchmark's 16k-token prefill routing (64 hot experts take 60 % of 131,072 routes, the others about
+    164 each), with one expert thinned to 20 routes so the decode path serves it at the image's threshold (32).
+    mm_moe_prefill (cap 32: fat experts only) and apply_exl3_fused_moe (threshold 32: fat GEMM + capped decode
+    path) are compared with the oracle on 16 sampled tokens: routes in the last tile of hot experts, routes in
+    129-255-route tiles, routes of the thinned expert and random ones."""
+    import torch
+    from mi355moe import exl3, moe, workload
+    H, I, E, T, K, cap = 4096, 2048, 384, 16384, 8, 32
+    seed = 1000
+    st = make_store(E + 1, H, I, seed, device=dev)
+    ids, w = workload.skewed_routing(T, K, E, seed=2000)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    thin = int(np.argmin(counts))
+    rows_thin = np.nonzero((ids == thin).any(1))[0]
+    rng = np.random.default_rng(11)
+    for t in rows_thin[20:]:                      # move its routes past the 20th to other cold experts
+        j = int(np.nonzero(ids[t] == thin)[0][0])
+        while True:
+            r = int(rng.integers(0, E))
+            if r != thin and r not in ids[t]:
+                break
+        ids[t, j] = r
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert counts[thin] == 20 and (np.delete(counts, thin) > cap).all()
+    # sampled tokens
+    order = np.argsort(ids.ravel(), kind="stable")
+    offs = np.concatenate([[0], np.cumsum(counts)])
+    tok_of = lambda e, r: int(order[offs[e] + r] // K)
+    hot = np.argsort(-counts)[:64]
+    pick = []
+    big_rem = [e for e in hot if 128 < counts[e] % 256]
+    small_rem = [e for e in hot if 0 < counts[e] % 256 <= 128]
+    for e in big_rem[:2] + small_rem[:1]:
+        pick.append(tok_of(e, counts[e] - 1))                  # last route of a hot expert (its last tile)
+    for e in big_rem[:1]:
+        first, n_t = _tiles(counts[e])[-1]
+        pick.append(tok_of(e, first + n_t // 2))               # middle of a 129-255-route tile
+    cold = [e for e in range(E) if 128 < counts[e] < 256]
+    for e in cold[:3]:
+        pick += [tok_of(e, 0), tok_of(e, counts[e] - 1)]      # first and last route of a 129-255-route tile
+    pick += [tok_of(thin, 0), tok_of(thin, 19)]                # the thinned expert (decode path)
+    rows = list(dict.fromkeys(pick))
+    while len(rows) < 16:
+        v = int(rng.integers(0, T))
+        if v not in rows:
+            rows.append(v)
+    rows = sorted(rows)
+    x = _t(workload.activations(T, H, seed=7), dev).to(torch.bfloat16)
+    idd, wd = _t(ids, dev), _t(w, dev)
+    print(f"16k skewed: {len(rows)} sampled tokens, thinned expert {thin}", flush=True)
+    a = moe.moe_prefill(st, x, idd, wd, cap=cap)
+    saved = exl3.FAT_EXPERT_THRESHOLD
+    try:
+        exl3.FAT_EXPERT_THRESHOLD = cap
+        b = exl3.apply_exl3_fused_moe(x, idd, wd, st, None, None, 10.0)
+    finally:
+        exl3.FAT_EXPERT_THRESHOLD = saved
+    torch.cuda.synchronize()
+    a, b = a.cpu().numpy()[rows], b.cpu().numpy()[rows]
+    x16 = x.half().cpu().numpy()[rows].astype(np.float32)
+    sub = ids[rows]
+    Y = OracleLayer(st, seed, cache=False).per_route(x16, sub).reshape(len(rows), K, H).astype(np.float64)
+    w16 = w[rows].astype(np.float16).astype(np.float64)
+    ref_b = np.einsum("tk,tkh->th", w16, Y)
+    ref_a = np.einsum("tk,tkh->th", np.where(sub == thin, 0.0, w[rows].astype(np.float64)), Y)
+    ok_a, m_a = within_tolerance(a, ref_a)
+    ok_b, m_b = within_tolerance(b, ref_b)
+    print(f"mm_moe_prefill cap 32 {m_a}, apply_exl3_fused_moe {m_b}", flush=True)
+    assert ok_a, m_a
+    assert ok_b, m_b
+
+
+def test_decode_chain_three_layers(dev):
+    """Three full-shape decode layers (H 4096, I 2048, 384 routed experts top-8 + shared, Zipf routing per layer)
+    chained as the benchmark chains them: each layer rescales its fp32 input to unit RMS and rounds it through bf16
+    to fp16 inside its route-prep kernel.
+
+    - The chain step: the fp16 input a layer builds from the previous layer's output equals the oracle's step
+      (prepare_input) on that output, up to a last-bit difference of the fp32 scale (at most a few elements, one
+      bf16 ulp each), and running the layer on that prepared input gives the chained output bit for bit.
+    - Every layer (the benchmark's AFFINE codebook evaluation, and EXACT weights) matches the oracle on its own
+      input.
+    A whole GPU chain is not compared with an independent oracle chain: the layer's fp16 rounding points amplify
+    any input difference (in the oracle alone, a 3e-6 relative perturbation of the first input grows to 4e-4,
+    1.2e-3 and 2.5e-3 mean relative error over three layers), so the comparison would measure that sensitivity,
+    not the kernels."""
+    import torch
+    from mi355moe import _lib, workload
+    from mi355moe.moe import DecodeRunner
+    H, I, E, T, K, L = 4096, 2048, 384, 4, 8, 3
+    stores = [make_store(E + 1, H, I, 1000 + l, device=dev) for l in range(L)]
+    routes = [workload.zipf_routing(T, K, E, seed=2000 + l) for l in range(L)]
+    ids = [np.concatenate([r[0], np.full((T, 1), E)], 1) for r in routes]
+    wts = [np.concatenate([r[1], np.ones((T, 1), np.float32)], 1) for r in routes]
+    runners = []
+    for l in range(L):
+        R = DecodeRunner(E, H, I, T, K, device=dev)
+        R.set_routes(_t(routes[l][0], dev), _t(routes[l][1], dev))
+        runners.append(R)
+    x0 = workload.activations(T, H, seed=7)
+    oracles = [OracleLayer(stores[l], 1000 + l) for l in range(L)]
+    for mode in ("AFFINE", "EXACT"):
+        for st in stores:
+            st.exact, st._c = mode == "EXACT", None
+        print(f"decode chain of 3 layers, {mode}", flush=True)
+        src, outs = _t(x0, dev), []
+        for l in range(L):
+            src = runners[l].layer(stores[l], x=src, out=torch.empty((T, H), dtype=torch.float32, device=dev),
+                                   rescale=True)
+            outs.append(src)
+        prev = _t(x0, dev)
+        for l in range(L):
+            x16 = torch.empty((T, H), dtype=torch.float16, device=dev)
+            _lib.call("mm_prepare_input", prev.data_ptr(), T, H, 1, None, x16.data_ptr(), _lib.stream_ptr())
+            again = runners[l].layer(stores[l], x=x16, out=torch.empty((T, H), dtype=torch.float32, device=dev))
+            torch.cuda.synchronize()
+            assert torch.equal(again, outs[l]), f"{mode} layer {l}: the chained step differs from mm_prepare_input"
+            p_in = prev.cpu().numpy()
+            want = O.prepare_input(p_in.astype(np.float64), rescale=True)
+            got = x16.cpu().numpy().astype(np.float32)
+            bad = np.argwhere(got != want)
+            assert len(bad) <= 4, (mode, l, len(bad))
+            for idx in map(tuple, bad):
+                assert abs(got[idx] - want[idx]) <= abs(want[idx]) * 2.0 ** -7
+            ref = oracles[l].forward(got, ids[l], wts[l])
+            ok, m = within_tolerance(outs[l].cpu().numpy(), ref)
+            print(f"{mode} layer {l} on its own input: {m}, chain-step mismatches {len(bad)}", flush=True)
+            assert ok, (mode, l, m)
+            prev = outs[l]
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_dsv41_shape_decode(dev, T):
+    """The served DSV41 expert shape: H 5120, I 2304, top-6 over 384 routed experts + 1 shared, on the decode
+    path (AFFINE codebook evaluation, as the benchmark runs it)."""
+    import torch
+    from mi355moe import moe, workload
+    H, I, E, K = 5120, 2304, 384, 6
+    seed = 5100 + T
+    st = make_store(E + 1, H, I, seed, device=dev)
+    ids, w = workload.zipf_routing(T, K, E, seed=5200 + T)
+    x = _t(workload.activations(T, H, seed=5300 + T), dev).to(torch.bfloat16)
+    print(f"DSV41 shape decode T={T}", flush=True)
+    out = moe.moe_forward(st, x, _t(ids, dev), _t(w, dev), shared_expert=E)
+    torch.cuda.synchronize()
+    ids_ext = np.concatenate([ids, np.full((T, 1), E)], 1)
+    w_ext = np.concatenate([w, np.ones((T, 1), np.float32)], 1)
+    ref = OracleLayer(st, seed, cache=False).forward(x.half().cpu().numpy().astype(np.float32), ids_ext, w_ext)
+    ok, m = within_tolerance(out.cpu().numpy(), ref)
+    print(f"DSV41 decode T={T}: {m}", flush=True)
+    assert ok, m
+
+
+def test_dsv41_shape_prefill(dev):
+    """DSV41 shape on the fat-expert path: 2048 tokens top-6 with skewed routing (hot experts about 115 routes,
+    cold about 15): mm_moe_prefill with cap 0 (every expert on the grouped GEMM) and apply_exl3_fused_moe at the
+    image's threshold (hot experts on the GEMM, cold ones on the decode path), 6 sampled tokens against the
+    oracle."""
+    import torch
+    from mi355moe import exl3, moe, workload
+    H, I, E, T, K = 5120, 2304, 384, 2048, 6
+    seed = 5400
+    st = make_store(E + 1, H, I, seed, device=dev)
+    ids, w = workload.skewed_routing(T, K, E, seed=5401)
+    x = _t(workload.activations(T, H, seed=5402), dev).to(torch.bfloat16)
+    idd, wd = _t(ids, dev), _t(w, dev)
+    counts = np.bincount(ids.ravel(), minlength=E)
+    assert (counts > 32).any() and ((counts > 0) & (counts <= 32)).any()
+    print("DSV41 shape prefill 2048 tokens", flush=True)
+    a = moe.moe_prefill(st, x, idd, wd, cap=0)
+    saved = exl3.FAT_EXPERT_THRESHOLD
+    try:
+        exl3.FAT_EXPERT_THRESHOLD = 32
+        b = exl3.apply_exl3_fused_moe(x, idd, wd, st, None, None, 10.0)
+    finally:
+        exl3.FAT_EXPERT_THRESHOLD = saved
+    torch.cuda.synchronize()
+    rows = [0, 511, 1024, 1500, 2000, 2047]
+    x16 = x.half().cpu().numpy()[rows].astype(np.float32)
+    Y = OracleLayer(st, seed, cache=False).per_route(x16, ids[rows]).reshape(len(rows), K, H).astype(np.float64)
+    ref_a = np.einsum("tk,tkh->th", w[rows].astype(np.float64), Y)
+    ref_b = np.einsum("tk,tkh->th", w[rows].astype(np.float16).astype(np.float64), Y)
+    ok_a, m_a = within_tolerance(a.cpu().numpy()[rows], ref_a)
+    ok_b, m_b = within_tolerance(b.cpu().numpy()[rows], ref_b)
+    print(f"DSV41 prefill cap 0 {m_a}, fused {m_b}", flush=True)
+    assert ok_a, m_a
+    assert ok_b, m_b

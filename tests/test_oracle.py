@@ -290,3 +290,17 @@ def test_router_matches_library_topk_softmax():
     assert np.array_equal(ids, top.indices.numpy())
     assert np.allclose(w, torch.softmax(top.values, dim=1).numpy(), rtol=1e-6, atol=1e-7)
     assert np.allclose(logits, lt.float().numpy(), rtol=1e-5, atol=1e-6)
+
+
+def test_bf16_rne_ties_and_prepare_input():
+    """bf16 rounding of the decode-chain step: hand-computed ties round to even, values past a tie round away;
+    prepare_input gives unit-RMS rows that are bf16 values representable in fp16."""
+    u = 2.0 ** -8
+    x = np.array([1 + u, 1 + 3 * u, 1 + u + 2 ** -20, -(1 + u), 3.0, 1 + 2 ** -7], np.float32)
+    want = np.array([1.0, 1 + 2 ** -6, 1 + 2 ** -7, -1.0, 3.0, 1 + 2 ** -7], np.float32)
+    assert np.array_equal(O.bf16_rne(x), want)
+    rng = np.random.default_rng(3)
+    a = rng.normal(0, 5, (3, 4096))
+    y = O.prepare_input(a)
+    assert np.allclose(np.sqrt(np.mean(y.astype(np.float64) ** 2, 1)), 1.0, atol=5e-3)
+    assert np.array_equal(O.bf16_rne(y), y) and np.array_equal(y.astype(np.float16).astype(np.float32), y)
