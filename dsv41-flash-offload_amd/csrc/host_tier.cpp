@@ -1,0 +1,691 @@
+// Host expert tier: routed experts computed on the host cores, straight from their pinned home copies, for the
+// picks the decode split sends to the host (the reference's CPU tier, kernels/cpu_avx2/ft_tier_ext.cpp:36-231 and
+// ft_core.h:573-727, rebuilt for AVX-512 hosts). Three parts:
+//
+//   Pool      N threads pinned to the given CPUs (the caller is thread 0); a phase is a list of work units taken
+//             from an atomic counter. Idle threads spin on a generation word, then nap.
+//   kernel    the EXL3 3-bpw expert MLP for a group of tokens: input transform, gate/up GEMV, SwiGLU, down-input
+//             transform, down GEMV, output transforms, weighted sum per token.
+//   worker    a thread that serves the mailbox the GPU split kernel publishes (ctrl words, fp16 x rows, picks) and
+//             answers with an fp32 partial in host-mapped memory and the done word.
+//
+// Trellis decode, 16 weights per AVX-512 operation: a 16x16 tile is 24 dwords (held in two zmm registers); the
+// 16 weights of tile row r, columns 0..15, are the trellis states i(r, c) = 32 (c & 7) + 8 ((r & 7) >> 1) + (r & 1)
+// + 2 (r >> 3) + 4 (c >> 3) (the inverse of the stream order PERM, ft_core.h:48-61). State i is the 16-bit window
+// ending at stream bit 3 i + 2 (mod 768, MSB first over the tile's little-endian dwords, ft_core.h:63-73): two
+// lane permutes fetch the two dwords holding it, one double shift (VBMI2) extracts it. The code is
+// 1024 + bytesum(state * 0x83DCD12D) (ft_core.h:75-83): one 32-bit multiply, one byte dot product against ones
+// (VNNI) that adds the four bytes onto the constant. EXACT rounds KINV * code + KBIAS to fp16 per weight (the
+// reference's EXACT expert and the GPU's fp16 weights); AFFINE (the default) accumulates sum_k x_k (code_k - 1534)
+// per column and forms KINV * S + (KBIAS + 1534 KINV) * sum_k x_k once per output (ft_core.h:267-293's AFFINE
+// evaluation; the codes are centred so the fp32 sum carries less of the common offset).
+#include <immintrin.h>
+#include <pthread.h>
+#include <sched.h>
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+#include <time.h>
+#include <unistd.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <thread>
+#include <vector>
+
+#include "host_tier.h"
+
+namespace tier {
+
+using mm::set_error;
+
+constexpr uint32_t MUL1 = 0x83DCD12Du;
+constexpr float HAD = 0.088388347648f;           // 1/sqrt(128), the reference's literal (ft_core.h:29)
+constexpr int TILE_BYTES = 96;
+constexpr int MAX_MT = 3;                        // tokens per pass of the GEMV (accumulators in registers)
+constexpr int CENTER = 1534;                     // AFFINE: codes 1024 + bytesum (1024 .. 2044) centred on 1534
+
+static inline float h2f(uint16_t h) { return _cvtsh_ss(h); }
+static inline uint16_t f2h(float f) { return _cvtss_sh(f, _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC); }
+static inline float r16(float f) { return h2f(f2h(f)); }
+static inline float kinv() { return h2f(0x1eee); }
+static inline float kbias() { return h2f(0xc931); }
+
+static double now_s()
+{
+    timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+// ------------------------------------------------------------------------------------------------ pool
+
+class Pool
+{
+public:
+    typedef void (*Fn)(void* ctx, int unit);
+
+    void start(const std::vector<int>& cpus, int n)
+    {
+        n_ = n < 1 ? 1 : n;
+        cpus_ = cpus;
+        quit_.store(false);
+        // the generation the threads start from is read here, before any run() or stop() can move it
+        const uint64_t g0 = gen_.load(std::memory_order_acquire);
+        for (int w = 1; w < n_; ++w) th_.emplace_back([this, w, g0] { loop(w, g0); });
+    }
+    void stop()
+    {
+        quit_.store(true);
+        gen_.fetch_add(1, std::memory_order_release);
+        for (auto& t : th_) t.join();
+        th_.clear();
+    }
+    int size() const { return n_; }
+    int cpu_of(int w) const { return cpus_.empty() ? -1 : cpus_[(size_t)w % cpus_.size()]; }
+
+    // Runs fn(ctx, u) for u in [0, units) on every thread (the caller included); returns when all are done.
+    void run(Fn fn, void* ctx, int units)
+    {
+        if (units <= 0) return;
+        fn_ = fn;
+        ctx_ = ctx;
+        units_ = units;
+        next_.store(0, std::memory_order_relaxed);
+        done_.store(0, std::memory_order_relaxed);
+        gen_.fetch_add(1, std::memory_order_release);
+        work();
+        while (done_.load(std::memory_order_acquire) < n_ - 1) _mm_pause();
+    }
+
+    static void pin(int cpu)
+    {
+        if (cpu < 0) return;
+        cpu_set_t s;
+        CPU_ZERO(&s);
+        CPU_SET(cpu, &s);
+        pthread_setaffinity_np(pthread_self(), sizeof(s), &s);
+    }
+
+private:
+    void work()
+    {
+        for (;;)
+        {
+            const int u = next_.fetch_add(1, std::memory_order_relaxed);
+            if (u >= units_) break;
+            fn_(ctx_, u);
+        }
+    }
+    void loop(int w, uint64_t seen)
+    {
+        pin(cpu_of(w));
+        for (;;)
+        {
+            long spins = 0;
+            uint64_t g;
+            while ((g = gen_.load(std::memory_order_acquire)) == seen)
+            {
+                if (++spins < 200000) _mm_pause();
+                else usleep(20);
+            }
+            seen = g;
+            if (quit_.load()) return;
+            work();
+            done_.fetch_add(1, std::memory_order_acq_rel);
+        }
+    }
+
+    int n_ = 1;
+    std::vector<int> cpus_;
+    std::vector<std::thread> th_;
+    std::atomic<uint64_t> gen_{ 0 };
+    std::atomic<int> next_{ 0 }, done_{ 0 };
+    std::atomic<bool> quit_{ false };
+    Fn fn_ = nullptr;
+    void* ctx_ = nullptr;
+    int units_ = 0;
+};
+
+// ------------------------------------------------------------------------------------------------ model
+
+struct Mat
+{
+    const uint8_t* tr = nullptr;     // tiles [K/16][N/16][96 B]
+    const uint16_t* suh = nullptr;   // fp16 [K]
+    const uint16_t* svh = nullptr;   // fp16 [N]
+    int K = 0, N = 0;
+};
+struct Expert { Mat g, u, d; };
+struct Layer { int E = 0; std::vector<Expert> ex; };
+
+// Per tile row r (16) and lane c (16): the dword holding the state's last bit, the one before it (circularly)
+// and the right shift that leaves the 16-bit state in the low half of the pair.
+struct Tables
+{
+    alignas(64) int32_t lo[16][16];
+    alignas(64) int32_t hi[16][16];
+    alignas(64) int32_t sh[16][16];
+    Tables()
+    {
+        for (int r = 0; r < 16; ++r)
+            for (int c = 0; c < 16; ++c)
+            {
+                const int i = 32 * (c & 7) + 8 * ((r & 7) >> 1) + (r & 1) + 2 * (r >> 3) + 4 * (c >> 3);
+                const int last = (3 * i + 2) % 768;
+                lo[r][c] = last >> 5;
+                hi[r][c] = ((last >> 5) + 23) % 24;
+                sh[r][c] = 31 - (last & 31);
+            }
+    }
+};
+// Built on first use (this file is compiled for AVX-512; nothing of it runs before the CPU check).
+static const Tables& tab()
+{
+    static const Tables t;
+    return t;
+}
+
+// ------------------------------------------------------------------------------------------------ transforms
+
+// 128-point Walsh-Hadamard transform with the reference's butterfly (strides 1 .. 64, (a + b, a - b),
+// ft_core.h:89-94), so every fp32 result is the reference's.
+static void fwht128(float* v)
+{
+    for (int h = 1; h < 128; h <<= 1)
+        for (int i = 0; i < 128; i += 2 * h)
+            for (int j = i; j < i + h; ++j)
+            {
+                const float a = v[j], b = v[j + h];
+                v[j] = a + b;
+                v[j + h] = a - b;
+            }
+}
+
+// xt = r16(FWHT(x * suh) * HAD) per 128-block (ft_core.h:96-102); returns the sum of xt.
+static float prep_input(const float* x, const uint16_t* suh, int K, float* xt)
+{
+    float s = 0.0f;
+    for (int b = 0; b < K; b += 128)
+    {
+        float v[128];
+        for (int i = 0; i < 128; ++i) v[i] = x[b + i] * h2f(suh[b + i]);
+        fwht128(v);
+        for (int i = 0; i < 128; ++i)
+        {
+            xt[b + i] = r16(v[i] * HAD);
+            s += xt[b + i];
+        }
+    }
+    return s;
+}
+
+// y = r16(FWHT(r16(y)) * HAD * svh) on one 128-block in place (ft_core.h:104-110).
+static void out_block(float* y, const uint16_t* svh)
+{
+    for (int i = 0; i < 128; ++i) y[i] = r16(y[i]);
+    fwht128(y);
+    for (int i = 0; i < 128; ++i) y[i] = r16((y[i] * HAD) * h2f(svh[i]));
+}
+
+static inline float act_gu(float g, float u, float limit)
+{
+    float x = g / (1.0f + std::exp(-g));
+    if (limit != 0.0f)
+    {
+        u = std::fmin(std::fmax(u, -limit), limit);
+        x = std::fmin(x, limit);
+    }
+    return x * u;
+}
+
+// ------------------------------------------------------------------------------------------------ GEMV
+
+// y[t][0..127] (raw sums, before the output transform) of column block cb of matrix m for MT tokens whose
+// transformed inputs are xt[t][0..K) and sums xs[t]. EXACT: fp16-rounded weights; else the centred AFFINE codes.
+template <int MT, bool EXACT>
+static void gemv_block(const Mat& m, int cb, const float* const* xt, const float* xs, float* const* y)
+{
+    const int NT = m.N / 16, KT = m.K / 16;
+    const __m512i vmask = _mm512_set1_epi32(0xffff), vmul = _mm512_set1_epi32((int)MUL1);
+    const __m512i vones = _mm512_set1_epi8(1);
+    const __m512i vbase = _mm512_set1_epi32(EXACT ? 1024 : 1024 - CENTER);
+    const __m512 vkinv = _mm512_set1_ps(kinv()), vkbias = _mm512_set1_ps(kbias());
+    __m512 acc[MT][8];
+    for (int t = 0; t < MT; ++t)
+        for (int j = 0; j < 8; ++j) acc[t][j] = _mm512_setzero_ps();
+    const uint8_t* base = m.tr + (size_t)cb * 8 * TILE_BYTES;
+    const Tables& TAB = tab();
+    for (int tk = 0; tk < KT; ++tk)
+    {
+        const uint8_t* row = base + (size_t)tk * NT * TILE_BYTES;
+        if (tk + 4 < KT)
+        {
+            const uint8_t* pf = row + (size_t)4 * NT * TILE_BYTES;
+            for (int o = 0; o < 8 * TILE_BYTES; o += 64) _mm_prefetch((const char*)(pf + o), _MM_HINT_T0);
+        }
+        for (int j = 0; j < 8; ++j)
+        {
+            const uint8_t* tile = row + j * TILE_BYTES;
+            const __m512i wa = _mm512_loadu_si512(tile);
+            const __m512i wb = _mm512_castsi256_si512(_mm256_loadu_si256((const __m256i*)(tile + 64)));
+            for (int r = 0; r < 16; ++r)
+            {
+                const __m512i lo = _mm512_permutex2var_epi32(wa, _mm512_load_si512(TAB.lo[r]), wb);
+                const __m512i hi = _mm512_permutex2var_epi32(wa, _mm512_load_si512(TAB.hi[r]), wb);
+                const __m512i st = _mm512_and_si512(_mm512_shrdv_epi32(lo, hi, _mm512_load_si512(TAB.sh[r])), vmask);
+                const __m512i p = _mm512_mullo_epi32(st, vmul);
+                const __m512i code = _mm512_dpbusd_epi32(vbase, p, vones);
+                __m512 w = _mm512_cvtepi32_ps(code);
+                if constexpr (EXACT)
+                    w = _mm512_cvtph_ps(_mm512_cvtps_ph(_mm512_fmadd_ps(w, vkinv, vkbias),
+                                                        _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+                const int k = tk * 16 + r;
+                for (int t = 0; t < MT; ++t) acc[t][j] = _mm512_fmadd_ps(_mm512_set1_ps(xt[t][k]), w, acc[t][j]);
+            }
+        }
+    }
+    for (int t = 0; t < MT; ++t)
+    {
+        if constexpr (EXACT)
+        {
+            for (int j = 0; j < 8; ++j) _mm512_storeu_ps(y[t] + 16 * j, acc[t][j]);
+        }
+        else
+        {
+            const __m512 off = _mm512_set1_ps((float)((double)kbias() + CENTER * (double)kinv()) * xs[t]);
+            for (int j = 0; j < 8; ++j) _mm512_storeu_ps(y[t] + 16 * j, _mm512_fmadd_ps(vkinv, acc[t][j], off));
+        }
+    }
+}
+
+template <bool EXACT>
+static void gemv_tokens(const Mat& m, int cb, int nt, const float* const* xt, const float* xs, float* const* y)
+{
+    for (int t0 = 0; t0 < nt; t0 += MAX_MT)
+    {
+        const int mt = nt - t0 < MAX_MT ? nt - t0 : MAX_MT;
+        if (mt == 3) gemv_block<3, EXACT>(m, cb, xt + t0, xs + t0, y + t0);
+        else if (mt == 2) gemv_block<2, EXACT>(m, cb, xt + t0, xs + t0, y + t0);
+        else gemv_block<1, EXACT>(m, cb, xt + t0, xs + t0, y + t0);
+    }
+}
+
+// ------------------------------------------------------------------------------------------------ a job
+
+// The picks of one call grouped by expert: expert g's tokens are tok[first[g] .. first[g + 1]) (pick order).
+struct Job
+{
+    const Layer* L = nullptr;
+    int H = 0, I = 0, T = 0, mode = 0;
+    float limit = 0.0f;
+    const float* x = nullptr;               // [T][H] fp32
+    std::vector<int> gexp, first, tok;      // experts, token groups
+    std::vector<float> wt;                  // weight of each group entry
+    std::vector<int> pick_of;               // group entry of pick p (the combine's order)
+    std::vector<int> tok_pick_start, tok_picks;   // picks of token t in pick order
+    // per group entry (expert e, token t): transformed inputs and intermediate rows
+    std::vector<float> xt, xs, gu, xd, xds, yd;
+    float* out = nullptr;                   // [T][H]
+};
+
+static void ph_input(void* c, int u)          // u = group entry
+{
+    Job& J = *static_cast<Job*>(c);
+    const int g = (int)(std::upper_bound(J.first.begin(), J.first.end(), u) - J.first.begin()) - 1;
+    const Expert& E = J.L->ex[J.gexp[g]];
+    const float* x = J.x + (size_t)J.tok[u] * J.H;
+    float* xt = J.xt.data() + (size_t)u * 2 * J.H;
+    J.xs[2 * u + 0] = prep_input(x, E.g.suh, J.H, xt);
+    J.xs[2 * u + 1] = prep_input(x, E.u.suh, J.H, xt + J.H);
+}
+
+static void ph_gateup(void* c, int u)         // u = (group, matrix, column block of I)
+{
+    Job& J = *static_cast<Job*>(c);
+    const int ncb = J.I / 128;
+    const int cb = u % ncb, mm = (u / ncb) % 2, g = u / (2 * ncb);
+    const Expert& E = J.L->ex[J.gexp[g]];
+    const Mat& M = mm == 0 ? E.g : E.u;
+    const int f = J.first[g], nt = J.first[g + 1] - f;
+    std::vector<const float*> xt(nt);
+    std::vector<float*> y(nt);
+    std::vector<float> xs(nt);
+    for (int t = 0; t < nt; ++t)
+    {
+        xt[t] = J.xt.data() + (size_t)(f + t) * 2 * J.H + (size_t)mm * J.H;
+        xs[t] = J.xs[2 * (f + t) + mm];
+        y[t] = J.gu.data() + (size_t)(f + t) * 2 * J.I + (size_t)mm * J.I + cb * 128;
+    }
+    if (J.mode == 1) gemv_tokens<true>(M, cb, nt, xt.data(), xs.data(), y.data());
+    else gemv_tokens<false>(M, cb, nt, xt.data(), xs.data(), y.data());
+    for (int t = 0; t < nt; ++t) out_block(y[t], M.svh + cb * 128);
+}
+
+static void ph_act(void* c, int u)            // u = group entry: SwiGLU, then the down input transform
+{
+    Job& J = *static_cast<Job*>(c);
+    const int g = (int)(std::upper_bound(J.first.begin(), J.first.end(), u) - J.first.begin()) - 1;
+    const Expert& E = J.L->ex[J.gexp[g]];
+    const float* gg = J.gu.data() + (size_t)u * 2 * J.I;
+    const float* uu = gg + J.I;
+    std::vector<float> a(J.I);
+    for (int i = 0; i < J.I; ++i) a[i] = r16(act_gu(gg[i], uu[i], J.limit));
+    J.xds[u] = prep_input(a.data(), E.d.suh, J.I, J.xd.data() + (size_t)u * J.I);
+}
+
+static void ph_down(void* c, int u)           // u = (group, column block of H)
+{
+    Job& J = *static_cast<Job*>(c);
+    const int ncb = J.H / 128;
+    const int cb = u % ncb, g = u / ncb;
+    const Mat& M = J.L->ex[J.gexp[g]].d;
+    const int f = J.first[g], nt = J.first[g + 1] - f;
+    std::vector<const float*> xt(nt);
+    std::vector<float*> y(nt);
+    std::vector<float> xs(nt);
+    for (int t = 0; t < nt; ++t)
+    {
+        xt[t] = J.xd.data() + (size_t)(f + t) * J.I;
+        xs[t] = J.xds[f + t];
+        y[t] = J.yd.data() + (size_t)(f + t) * J.H + cb * 128;
+    }
+    if (J.mode == 1) gemv_tokens<true>(M, cb, nt, xt.data(), xs.data(), y.data());
+    else gemv_tokens<false>(M, cb, nt, xt.data(), xs.data(), y.data());
+    for (int t = 0; t < nt; ++t) out_block(y[t], M.svh + cb * 128);
+}
+
+static void ph_combine(void* c, int u)        // u = (token, 512-column chunk): out = sum of w * y in pick order
+{
+    Job& J = *static_cast<Job*>(c);
+    const int nch = J.H / 512 > 0 ? J.H / 512 : 1;
+    const int t = u / nch, ch = u % nch;
+    const int h0 = ch * (J.H / nch), h1 = ch == nch - 1 ? J.H : h0 + J.H / nch;
+    float* o = J.out + (size_t)t * J.H;
+    for (int h = h0; h < h1; ++h) o[h] = 0.0f;
+    for (int q = J.tok_pick_start[t]; q < J.tok_pick_start[t + 1]; ++q)
+    {
+        const int ge = J.pick_of[J.tok_picks[q]];
+        const float w = J.wt[ge];
+        const float* y = J.yd.data() + (size_t)ge * J.H;
+        for (int h = h0; h < h1; ++h) o[h] = std::fma(w, y[h], o[h]);
+    }
+}
+
+// Runs the picks (token, expert, weight) of one layer: out [T][H] (every token row written).
+static void run_picks(Pool& pool, const Layer& L, int H, int I, const float* x, int T, const int32_t* pt,
+                      const int32_t* pe, const float* pw, int np, int mode, float limit, float* out, Job& J)
+{
+    J.L = &L;
+    J.H = H;
+    J.I = I;
+    J.T = T;
+    J.mode = mode;
+    J.limit = limit;
+    J.x = x;
+    J.out = out;
+    // group the picks by expert (ascending id), tokens in pick order
+    std::vector<int> cnt(L.E, 0);
+    for (int p = 0; p < np; ++p) cnt[pe[p]]++;
+    J.gexp.clear();
+    J.first.assign(1, 0);
+    std::vector<int> slot(L.E, -1);
+    for (int e = 0; e < L.E; ++e)
+        if (cnt[e])
+        {
+            slot[e] = (int)J.gexp.size();
+            J.gexp.push_back(e);
+            J.first.push_back(J.first.back() + cnt[e]);
+        }
+    const int ng = (int)J.gexp.size();
+    J.tok.assign(np, 0);
+    J.wt.assign(np, 0.0f);
+    J.pick_of.assign(np, 0);
+    std::vector<int> fill(J.first.begin(), J.first.end() - 1);
+    for (int p = 0; p < np; ++p)
+    {
+        const int ge = fill[slot[pe[p]]]++;
+        J.tok[ge] = pt[p];
+        J.wt[ge] = pw[p];
+        J.pick_of[p] = ge;
+    }
+    J.tok_pick_start.assign(T + 1, 0);
+    for (int p = 0; p < np; ++p) J.tok_pick_start[pt[p] + 1]++;
+    for (int t = 0; t < T; ++t) J.tok_pick_start[t + 1] += J.tok_pick_start[t];
+    J.tok_picks.assign(np, 0);
+    std::vector<int> tf(J.tok_pick_start.begin(), J.tok_pick_start.end() - 1);
+    for (int p = 0; p < np; ++p) J.tok_picks[tf[pt[p]]++] = p;
+    J.xt.resize((size_t)np * 2 * H);
+    J.xs.resize((size_t)np * 2);
+    J.gu.resize((size_t)np * 2 * I);
+    J.xd.resize((size_t)np * I);
+    J.xds.resize((size_t)np);
+    J.yd.resize((size_t)np * H);
+    if (np)
+    {
+        pool.run(ph_input, &J, np);
+        pool.run(ph_gateup, &J, ng * 2 * (I / 128));
+        pool.run(ph_act, &J, np);
+        pool.run(ph_down, &J, ng * (H / 128));
+    }
+    pool.run(ph_combine, &J, T * (H / 512 > 0 ? H / 512 : 1));
+}
+
+// ------------------------------------------------------------------------------------------------ the tier
+
+struct Tier
+{
+    Pool pool;
+    std::vector<int> cpus;
+    std::vector<Layer> layers;
+    int64_t* ctrl = nullptr;
+    const uint16_t* hx = nullptr;
+    const int32_t* picks = nullptr;
+    float* hout = nullptr;
+    int mode = -1, H = 0, I = 0;
+    float limit = 0.0f;
+    std::thread th;
+    std::atomic<bool> quit{ false }, running{ false };
+    std::atomic<int64_t> jobs{ 0 }, experts{ 0 }, tokens{ 0 }, empty{ 0 }, busy_ns{ 0 };
+    std::vector<float> xf;
+    std::vector<int32_t> pt, pe;
+    std::vector<float> pw;
+    Job job;
+};
+
+static Tier* g_tier = nullptr;
+
+// mode: 0 AFFINE, 1 EXACT, -1 auto (AFFINE)
+static int eff_mode(int m) { return m == 1 ? 1 : 0; }
+
+static void run_job(Tier& Tr, int li, int bsz, int np)
+{
+    const int H = Tr.H;
+    Tr.xf.resize((size_t)(bsz > 0 ? bsz : 1) * H);
+    for (size_t i = 0; i < (size_t)bsz * H; ++i) Tr.xf[i] = h2f(Tr.hx[i]);
+    Tr.pt.resize(np);
+    Tr.pe.resize(np);
+    Tr.pw.resize(np);
+    for (int p = 0; p < np; ++p)
+    {
+        Tr.pt[p] = Tr.picks[3 * p];
+        Tr.pe[p] = Tr.picks[3 * p + 1];
+        memcpy(&Tr.pw[p], &Tr.picks[3 * p + 2], 4);
+    }
+    run_picks(Tr.pool, Tr.layers[li], H, Tr.I, Tr.xf.data(), bsz, Tr.pt.data(), Tr.pe.data(), Tr.pw.data(), np,
+              eff_mode(Tr.mode), Tr.limit, Tr.hout, Tr.job);
+    if (np == 0) Tr.empty++;
+    Tr.experts += np;
+    Tr.tokens += bsz;
+}
+
+// `last` is the job sequence when the tier started: read by the starting thread, so a job published right after
+// mm_tier_start returns is not mistaken for an old one.
+static void worker_main(Tier* Tr, int cpu0, int64_t last)
+{
+    Pool::pin(cpu0);
+    long idle = 0;
+    while (!Tr->quit.load(std::memory_order_relaxed))
+    {
+        const int64_t s = __atomic_load_n(Tr->ctrl, __ATOMIC_ACQUIRE);
+        if (s == last)
+        {
+            if (++idle < 400000) _mm_pause();
+            else usleep(20);
+            continue;
+        }
+        idle = 0;
+        const double t0 = now_s();
+        const int li = (int)__atomic_load_n(Tr->ctrl + 2, __ATOMIC_RELAXED);
+        const int bsz = (int)__atomic_load_n(Tr->ctrl + 3, __ATOMIC_RELAXED);
+        const int np = (int)__atomic_load_n(Tr->ctrl + 4, __ATOMIC_RELAXED);
+        if (li >= 0 && li < (int)Tr->layers.size() && Tr->layers[li].E > 0 && bsz >= 0 && np >= 0) run_job(*Tr, li, bsz, np);
+        Tr->busy_ns += (int64_t)((now_s() - t0) * 1e9);
+        Tr->jobs++;
+        last = s;
+        __atomic_store_n(Tr->ctrl + 1, s, __ATOMIC_RELEASE);
+    }
+}
+
+}  // namespace tier
+
+namespace tier {
+
+int impl_init(int threads, const int* cpus, int ncpus, int64_t* ctrl, const void* hx, const int32_t* picks,
+              float* hout, int mode, int H, int I, int nlayers)
+{
+    if (g_tier) return set_error(MM_ERR_ARG, "mm_tier_init: the tier is already initialised");
+    if (threads < 1 || H <= 0 || I <= 0 || H % 512 || I % 128 || nlayers <= 0 || (ncpus > 0 && !cpus))
+        return set_error(MM_ERR_ARG, "mm_tier_init: need threads >= 1, H a multiple of 512, I of 128, nlayers > 0");
+    Tier* T = new Tier();
+    if (ncpus > 0) T->cpus.assign(cpus, cpus + ncpus);
+    T->ctrl = ctrl;
+    T->hx = static_cast<const uint16_t*>(hx);
+    T->picks = picks;
+    T->hout = hout;
+    T->mode = mode;
+    T->H = H;
+    T->I = I;
+    T->layers.resize(nlayers);
+    T->pool.start(T->cpus, threads);
+    g_tier = T;
+    return MM_OK;
+}
+
+int impl_add_layer(int li, int E, const int64_t* ptrs, const void* suh_g, const void* svh_g, const void* suh_u,
+                      const void* svh_u, const void* suh_d, const void* svh_d)
+{
+    Tier* T = g_tier;
+    if (!T) return set_error(MM_ERR_ARG, "mm_tier_add_layer: mm_tier_init first");
+    if (li < 0 || li >= (int)T->layers.size() || E <= 0 || !ptrs || !suh_g || !svh_g || !suh_u || !svh_u || !suh_d || !svh_d)
+        return set_error(MM_ERR_ARG, "mm_tier_add_layer: bad layer index, expert count or null pointer");
+    if (T->running.load()) return set_error(MM_ERR_ARG, "mm_tier_add_layer: the worker is running");
+    const int H = T->H, I = T->I;
+    auto u16 = [](const void* p, size_t off) { return static_cast<const uint16_t*>(p) + off; };
+    Layer& L = T->layers[li];
+    L.E = E;
+    L.ex.assign(E, Expert());
+    for (int e = 0; e < E; ++e)
+    {
+        Expert& X = L.ex[e];
+        X.g = { reinterpret_cast<const uint8_t*>(ptrs[3 * e]), u16(suh_g, (size_t)e * H), u16(svh_g, (size_t)e * I), H, I };
+        X.u = { reinterpret_cast<const uint8_t*>(ptrs[3 * e + 1]), u16(suh_u, (size_t)e * H), u16(svh_u, (size_t)e * I), H, I };
+        X.d = { reinterpret_cast<const uint8_t*>(ptrs[3 * e + 2]), u16(suh_d, (size_t)e * I), u16(svh_d, (size_t)e * H), I, H };
+    }
+    return MM_OK;
+}
+
+int impl_set_limit(float limit)
+{
+    if (!g_tier) return set_error(MM_ERR_ARG, "mm_tier_set_limit: mm_tier_init first");
+    g_tier->limit = limit;
+    return MM_OK;
+}
+
+int impl_set_mode(int mode)
+{
+    if (!g_tier) return set_error(MM_ERR_ARG, "mm_tier_set_mode: mm_tier_init first");
+    g_tier->mode = mode;
+    return MM_OK;
+}
+
+int impl_start(int cpu0)
+{
+    Tier* T = g_tier;
+    if (!T || T->running.load()) return set_error(MM_ERR_ARG, "mm_tier_start: not initialised or already running");
+    if (!T->ctrl || !T->hx || !T->picks || !T->hout)
+        return set_error(MM_ERR_ARG, "mm_tier_start: the mailbox (ctrl, hx, picks, hout) was not given to mm_tier_init");
+    T->quit.store(false);
+    T->running.store(true);
+    T->th = std::thread(worker_main, T, cpu0, __atomic_load_n(T->ctrl, __ATOMIC_ACQUIRE));
+    return MM_OK;
+}
+
+int impl_stop()
+{
+    Tier* T = g_tier;
+    if (!T) return MM_OK;
+    if (T->running.load())
+    {
+        T->quit.store(true);
+        if (T->th.joinable()) T->th.join();
+        T->running.store(false);
+    }
+    return MM_OK;
+}
+
+int impl_shutdown()
+{
+    Tier* T = g_tier;
+    if (!T) return MM_OK;
+    impl_stop();
+    T->pool.stop();
+    delete T;
+    g_tier = nullptr;
+    return MM_OK;
+}
+
+int impl_forward(int li, const float* x, int m, const int32_t* sel, const float* w, int k, float* out, int mode)
+{
+    Tier* T = g_tier;
+    if (!T) return set_error(MM_ERR_ARG, "mm_tier_forward: mm_tier_init first");
+    if (T->running.load()) return set_error(MM_ERR_ARG, "mm_tier_forward: the worker is running");
+    if (li < 0 || li >= (int)T->layers.size() || T->layers[li].E <= 0 || m < 0 || k <= 0 || !x || !sel || !w || !out)
+        return set_error(MM_ERR_ARG, "mm_tier_forward: bad layer or argument");
+    const int E = T->layers[li].E;
+    std::vector<int32_t> pt, pe;
+    std::vector<float> pw;
+    for (int t = 0; t < m; ++t)
+        for (int j = 0; j < k; ++j)
+        {
+            const int e = sel[(size_t)t * k + j];
+            if (e < 0 || e >= E) continue;
+            pt.push_back(t);
+            pe.push_back(e);
+            pw.push_back(w[(size_t)t * k + j]);
+        }
+    run_picks(T->pool, T->layers[li], T->H, T->I, x, m, pt.data(), pe.data(), pw.data(), (int)pt.size(),
+              eff_mode(mode >= 0 ? mode : T->mode), T->limit, out, T->job);
+    return MM_OK;
+}
+
+int impl_stats(int64_t* out)
+{
+    Tier* T = g_tier;
+    if (!out) return set_error(MM_ERR_ARG, "mm_tier_stats: null pointer");
+    if (!T)
+    {
+        for (int i = 0; i < 5; ++i) out[i] = 0;
+        return MM_OK;
+    }
+    out[0] = T->jobs.load();
+    out[1] = T->experts.load();
+    out[2] = T->tokens.load();
+    out[3] = T->empty.load();
+    out[4] = T->busy_ns.load();
+    return MM_OK;
+}
+
+}  // namespace tier

@@ -14,8 +14,14 @@
   before_step(ntok)           the engine-step hook's part before a step (ct_vllm.py:459-475): release the cache
                               before prefill-sized steps; the hook calls ec_step after every step
 
-No host worker computes misses here: the split's policy sends no picks to the host (force_n = 0), so every
-routed expert runs on the GPU from its cache slot or, zero-copy, from its pinned host home.
+  calibrate(), set_policy(...)  the split's cost-model constants measured on this machine (per-expert time of a
+                              zero-copy miss on the GPU and of an expert on the host tier), or set by hand
+
+With DSV41_CPU_TIER=1 the host tier (mi355moe.tier, the library's mm_tier_*) serves the picks the split sends
+to the host: the split's cost model (ct/ft_tier_cu_v.cu:35-62) chooses how many of the call's misses the host
+cores compute from their pinned home rows while the GPU reads the rest zero-copy over PCIe and computes its
+share; the combine then adds the host partial (bounded wait, DSV41_CT_TIMEOUT_S). Without it the policy's
+force_n is 0 and every routed expert runs on the GPU.
 """
 import json
 import os
@@ -24,9 +30,10 @@ import numpy as np
 import torch
 
 from . import _lib, cache, exl3
+from . import tier as _tier
 from .hostmem import HostBuffer
 
-S = {"layers": [], "started": False, "init": False}
+S = {"layers": [], "started": False, "init": False, "selftest": None, "cpu_tier": False}
 EC = {"cache": None}
 _ORIG = {}
 
@@ -53,14 +60,21 @@ def _init(layer):
     S["dflag"] = torch.zeros(1, dtype=torch.int64, device=dev)
     S["seqc"] = torch.zeros(1, dtype=torch.int64, device=dev)
     S["stats"] = torch.zeros(8, dtype=torch.int64, device=dev)
-    # cost-model policy (ct_vllm.py:69-71), with no host worker: force_n = 0 sends nothing to the host
+    # cost-model policy (ct_vllm.py:69-71): without the host tier force_n = 0 sends nothing to the host
+    S["cpu_tier"] = os.environ.get("DSV41_CPU_TIER", "0") == "1"
+    force = _f("DSV41_CT_FORCE_N", -1) if S["cpu_tier"] else 0.0
     S["pol"] = torch.tensor([_f("DSV41_CT_TZC", 0.58), _f("DSV41_CT_THIT", 0.03), _f("DSV41_CT_A", 0.11),
-                             _f("DSV41_CT_B", 0.16), _f("DSV41_CT_TOK", 0.2), _f("DSV41_CT_MAXN", 64), 0.0, 0.0, 0.0],
+                             _f("DSV41_CT_B", 0.16), _f("DSV41_CT_TOK", 0.2), _f("DSV41_CT_MAXN", 64), force, 0.0, 0.0],
                             dtype=torch.float32, device=dev)
     S["timeout_ns"] = int(_f("DSV41_CT_TIMEOUT_S", 2) * 1e9)
     S["sel"] = torch.empty(S["maxpicks"], dtype=torch.long, device=dev)
     S["w"] = torch.empty(S["maxpicks"], dtype=torch.float32, device=dev)
     S["nlayers"] = int(os.environ.get("DSV41_CT_LAYERS", "40"))
+    if S["cpu_tier"]:
+        _tier.init(H, layer.I, S["nlayers"], mailbox={"ctrl": S["ctrl"], "hx": S["hx"], "picks": S["picks"],
+                                                        "hout": S["hout"]})
+        S["limit"] = _f("DSV41_CT_LIMIT", 10.0)
+        _tier.set_limit(S["limit"] if S["limit"] > 0 else 0.0)
     S["init"] = True
 
 
@@ -80,15 +94,96 @@ def register(layer, nlayers=None):
     layer._ct = {"li": li, "E": layer.E, "slotof": layer.slotof,
                  "score": torch.zeros(layer.E, dtype=torch.float32, device=dev), "counts": layer.counts,
                  "home": layer.home}
+    if S["cpu_tier"]:
+        _tier.add_layer(li, layer)          # home rows read in place, host copies of the scales (ct_vllm.py:97-110)
     S["layers"].append(layer)
     if len(S["layers"]) == S["nlayers"]:
         start()
+
+
+def selftest(layers=None):
+    """The host tier against the GPU path on the same cold experts (ct_vllm.py:123-140): x ~ N(0, 0.35^2) fp16, six
+    random host-resident experts with weight 0.25, 1 and 3 tokens, up to three layers; returns the largest relative
+    L2 difference of the weighted sums."""
+    res = []
+    g = torch.Generator(device="cpu").manual_seed(0)
+    layers = S["layers"] if layers is None else layers
+    orig = _ORIG.get("fused", exl3.apply_exl3_fused_moe)
+    for layer in layers[:: max(1, len(layers) // 3)][:3]:
+        cold = [e for e in range(layer.E) if int(layer.slotof[e]) < 0]
+        for mt in (1, 3):
+            x = (torch.randn(mt, S["H"], generator=g) * 0.35).half()
+            exps = [cold[int(i)] for i in torch.randperm(len(cold), generator=g)[:6]]
+            sel = torch.tensor([exps] * mt, dtype=torch.int32)
+            w = torch.full((mt, 6), 0.25, dtype=torch.float32)
+            cpu = torch.from_numpy(_tier.forward(layer._ct["li"], x.float().numpy(), sel.numpy(), w.numpy()))
+            gpu = orig(x.to(S["dev"]), sel.long().to(S["dev"]), w.to(S["dev"]), layer, None, None,
+                       S["limit"] if S["limit"] > 0 else None).float().cpu()
+            res.append(float((cpu - gpu).norm() / gpu.norm().clamp_min(1e-12)))
+    return {"max_rel_vs_gpu": round(max(res), 6), "n": len(res)}
+
+
+def set_policy(tzc=None, thit=None, a=None, b=None, tok=None, maxn=None, force_n=None):
+    """Set cost-model constants of the split's policy vector (ms per zero-copy miss, per resident hit, per host job,
+    per host expert, extra-token factor, most host experts per call, forced host count or -1)."""
+    p = S["pol"].cpu()
+    for j, v in enumerate((tzc, thit, a, b, tok, maxn, force_n)):
+        if v is not None:
+            p[j] = float(v)
+    S["pol"].copy_(p)
+
+
+def calibrate(layer=None, experts=8):
+    """Measure the policy's constants on this machine for one tier layer: a zero-copy miss (the GPU path on
+    `experts` host-resident experts, one token), an HBM hit (the same experts from HBM copies is not needed: a hit
+    streams the expert at HBM rate, taken as 1/400 of the miss), and the host tier on one and on `experts`
+    experts (job overhead and per-expert time). Returns the constants set."""
+    import time
+    layer = S["layers"][0] if layer is None else layer
+    orig = _ORIG.get("fused", exl3.apply_exl3_fused_moe)
+    cold = [e for e in range(layer.E) if int(layer.slotof[e]) < 0][:experts]
+    x = (torch.randn(1, S["H"]) * 0.35).half()
+    xd = x.to(S["dev"])
+
+    def gpu_t(ids):
+        idd = torch.tensor([ids], dtype=torch.long, device=S["dev"])
+        wd = torch.full((1, len(ids)), 1.0 / len(ids), device=S["dev"])
+        orig(xd, idd, wd, layer, None, None, 10.0)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(5):
+            orig(xd, idd, wd, layer, None, None, 10.0)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) / 5 * 1e3
+
+    def cpu_t(ids):
+        sel = np.array([ids], np.int32)
+        ww = np.full((1, len(ids)), 1.0 / len(ids), np.float32)
+        _tier.forward(layer._ct["li"], x.float().numpy(), sel, ww)
+        t0 = time.perf_counter()
+        for _ in range(5):
+            _tier.forward(layer._ct["li"], x.float().numpy(), sel, ww)
+        return (time.perf_counter() - t0) / 5 * 1e3
+
+    zc = gpu_t(cold) / len(cold)
+    c1, cn = cpu_t(cold[:1]), cpu_t(cold)
+    b = max((cn - c1) / max(1, len(cold) - 1), 1e-3)
+    a = max(c1 - b, 0.0)
+    set_policy(tzc=zc, thit=zc / 400.0, a=a, b=b)
+    return {"tzc": zc, "thit": zc / 400.0, "a": a, "b": b}
 
 
 def start(**ec_args):
     if S["started"]:
         return
     EC["cache"] = cache.ExpertCache(S["layers"], **ec_args)
+    if S["cpu_tier"]:
+        if os.environ.get("DSV41_CT_SELFTEST", "1") == "1":
+            try:
+                S["selftest"] = selftest()
+            except Exception as exc:    # the diagnostic never blocks serving (ct_vllm.py:146-152)
+                S["selftest"] = {"error": repr(exc)}
+        _tier.start()
     S["started"] = True
 
 
@@ -153,8 +248,10 @@ def summary():
         return None
     st = S["stats"].tolist()
     calls = max(1, st[3])
+    h = _tier.stats() if S["cpu_tier"] else {"jobs": 0, "busy_ns": 0}
     return {"calls": st[3], "hits": st[0], "misses": st[1], "cpu_experts": st[2], "cpu_per_call": round(st[2] / calls, 3),
-            "gpu_wait_ms": round(st[4] / 1e6 / max(1, st[5]), 4), "timeouts": st[6],
+            "gpu_wait_ms": round(st[4] / 1e6 / max(1, st[5]), 4), "timeouts": st[6], "host_jobs": h["jobs"],
+            "host_busy_ms": round(h["busy_ns"] / 1e6 / max(1, h["jobs"]), 4), "selftest": S["selftest"],
             "hit_rate": round(st[0] / max(1, st[0] + st[1]), 4), "ec": ec_summary()}
 
 
@@ -192,9 +289,11 @@ def uninstall(X):
 
 
 def reset():
-    """Forget every registered layer and the cache (tests, benchmarks)."""
+    """Forget every registered layer, the cache and the host tier (tests, benchmarks)."""
+    if S.get("cpu_tier") and _tier.running():
+        _tier.shutdown()
     S.clear()
-    S.update({"layers": [], "started": False, "init": False})
+    S.update({"layers": [], "started": False, "init": False, "selftest": None, "cpu_tier": False})
     EC["cache"] = None
 
 

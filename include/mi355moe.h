@@ -253,6 +253,45 @@ uint64_t mm_expert_seed(uint64_t layer_seed, uint64_t expert);
  * s_t = 1/sqrt(mean(x_t^2)) if rescale else 1. Also writes bf16 [T][H] if x_bf16 != NULL. */
 int mm_prepare_input(const float* x, int T, int H, int rescale, void* x_bf16, void* x_fp16, mm_stream_t stream);
 
+/* ----------------------------------------------------------------------------------------- host tier */
+
+/* Host expert tier (replaces the reference's CPU tier extension, kernels/cpu_avx2/ft_tier_ext.cpp:36-231, and its
+ * expert kernel, kernels/cpu_avx2/ft_core.h:573-727): experts computed on the host cores straight from their
+ * pinned home rows, serving the mailbox mm_split publishes. One tier per process. Needs an AVX-512 host
+ * (F, BW, VL, VBMI2, VNNI) with F16C and FMA; every entry fails with MM_ERR_UNSUP / MM_ERR_ARG otherwise.
+ *
+ * mm_tier_init (tier_init, ft_tier_ext.cpp:36-56): `threads` workers pinned to cpus[0 .. ncpus) (the serving thread
+ * is worker 0 and runs on cpus[0]); the mailbox is the split's: ctrl int64 [16] (ctrl[0] job sequence, written by
+ * the GPU last; ctrl[1] done sequence, written here last; ctrl[2] layer, ctrl[3] tokens, ctrl[4] picks), hx fp16
+ * [tokens][H], picks int32 [picks][3] = (token, expert, weight fp32 bits), hout fp32 [tokens][H] (all host
+ * memory the GPU maps, e.g. mm_host_alloc); they may be NULL when only mm_tier_forward is used. mode: 1 EXACT
+ * (fp16-rounded weights), 0 AFFINE, -1 automatic (AFFINE; the reference's automatic choice of its int16 path is
+ * not built). H a multiple of 512, I of 128. */
+int mm_tier_init(int threads, const int* cpus, int ncpus, int64_t* ctrl, const void* hx, const int32_t* picks,
+                 float* hout, int mode, int H, int I, int nlayers);
+/* Layer li (tier_add_layer, ft_tier_ext.cpp:60-101): ptrs int64 [E][3] host addresses of each expert's gate, up and
+ * down trellis (tiles [K/16][N/16][96 B], as the GPU reads them); scales fp16 in host memory, per expert:
+ * suh_g [E][H], svh_g [E][I], suh_u [E][H], svh_u [E][I], suh_d [E][I], svh_d [E][H]. The memory stays the
+ * caller's and must outlive the tier. */
+int mm_tier_add_layer(int li, int E, const int64_t* ptrs, const void* suh_g, const void* svh_g, const void* suh_u,
+                      const void* svh_u, const void* suh_d, const void* svh_d);
+/* SwiGLU clamp (tier_set_limit; 0 = off) and mode (tier_set_mode). */
+int mm_tier_set_limit(float limit);
+int mm_tier_set_mode(int mode);
+/* Start / stop the serving thread (tier_start, tier_stop, ft_tier_ext.cpp:161-175): it waits for ctrl[0] to move,
+ * computes sum over the picks of token t of w * expert(x_t) into hout rows 0 .. tokens-1 (every row written),
+ * then stores ctrl[1] = ctrl[0] with release ordering. mm_tier_shutdown also stops the workers and frees the
+ * tier (mm_tier_init may then be called again). */
+int mm_tier_start(int cpu0);
+int mm_tier_stop(void);
+int mm_tier_shutdown(void);
+/* Synchronous forward (tier_forward, ft_tier_ext.cpp:177-191), refused while the serving thread runs: x fp32
+ * [m][H] (fp16-valued), sel int32 [m][k] (entries outside [0, E) skipped), w fp32 [m][k] -> out fp32 [m][H];
+ * mode as for mm_tier_init (-1: the tier's mode). */
+int mm_tier_forward(int li, const float* x, int m, const int32_t* sel, const float* w, int k, float* out, int mode);
+/* out int64 [5]: jobs served, picks computed, tokens, jobs without picks, busy nanoseconds (tier_stats). */
+int mm_tier_stats(int64_t* out);
+
 #ifdef __cplusplus
 }
 #endif
