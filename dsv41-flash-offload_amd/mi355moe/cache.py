@@ -47,6 +47,11 @@ def point(layer, items, stream=None):
     _lib.call("mm_slot_point", p["gate_trellis"].data_ptr(), p["up_trellis"].data_ptr(), p["down_trellis"].data_ptr(),
               layer.slotof.data_ptr(), int(layer.E), d.data_ptr(), len(items), _lib.stream_ptr(s))
     d.record_stream(s)
+    mirror = getattr(layer, "slot_host", None)
+    if mirror is not None:
+        for it in items:                              # in order: the last item of an expert wins, as on the device
+            if 0 <= int(it[0]) < layer.E:
+                mirror[int(it[0])] = int(it[4])
 
 
 def stage_copy(copies, stream=None):

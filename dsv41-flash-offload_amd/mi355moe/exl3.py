@@ -38,7 +38,11 @@ _DMA_B = _ienv("EXL3_HOST_DMA_BATCH", 16)
 _DMA_NS = _ienv("EXL3_HOST_DMA_SLOTS", 3)
 _DMA_MIN_TOKENS = _ienv("EXL3_HOST_DMA_MIN_TOKENS", 65)
 
+# cross-layer prefetch (runtime/patch_dma_prefetch.py:17-36): after a layer's last staged batch, the next layer's
+# first NS batches are queued on the copy engine, each behind the last reader of its slot
+_DMA_PREFETCH = os.environ.get("EXL3_DMA_STOCK_PREFETCH", "1") == "1"
 _DMA_STATE = {}         # device index -> {"slots": SlotPool [NS * B rows], "copy": Stream, "free": [Event | None] * NS}
+_DMA_LAST = {}          # device index -> the last layer registered for staging (links each layer to the next)
 _WS = {}                # device index -> reusable workspace tensor of the staged path
 _DMA_TIMING = None      # a list to collect (start event, end event, bytes) of every staged copy, or None
 
@@ -134,11 +138,24 @@ def _dma_register(layer, dev=None):
     st = _DMA_STATE.get(key)
     if st is None:
         st = _DMA_STATE[key] = {"slots": cache.SlotPool(_DMA_NS * _DMA_B, layer.H, layer.I, dev), "copy": None,
-                                "free": [None] * _DMA_NS, "shape": (layer.H, layer.I)}
+                                "free": [None] * _DMA_NS, "shape": (layer.H, layer.I), "owner": [None] * _DMA_NS}
     if st["shape"] != (layer.H, layer.I):
         return False
-    layer._exl3_dma = {"tables": None, "copied": 0, "bytes": 0, "batches": 0}
+    layer._exl3_dma = {"tables": None, "copied": 0, "bytes": 0, "batches": 0, "pre": {}, "next": None,
+                       "prefetched": 0}
+    prev = _DMA_LAST.get(key)
+    if prev is not None and getattr(prev, "_exl3_dma", None) is not None:
+        prev._exl3_dma["next"] = layer
+    _DMA_LAST[key] = layer
     return True
+
+
+def _dma_batches(layer):
+    """Staging batches of a layer: its host-resident experts that are not in an HBM slot (ascending id, from the
+    host mirror of the slot table), B per batch. Known before the layer's routing, as the reference's are (every
+    cold expert of the host plan, patch:31-52), so the previous layer can queue the first copies."""
+    cold = [e for e in range(layer.E) if layer.slot_host[e] < 0]
+    return [cold[i:i + _DMA_B] for i in range(0, len(cold), _DMA_B)]
 
 
 def _dma_tables(layer):
@@ -161,6 +178,7 @@ def _dma_issue(layer, sl, experts, dev):
         cs.wait_event(st["free"][sl])
     pool = st["slots"]
     rb = pool.rows.row_bytes
+    st["owner"][sl] = (id(layer), tuple(experts))       # what the slot holds once the copy has run
     cl = [(pool.row(sl * _DMA_B + r), layer.host_home.row(e), rb) for r, e in enumerate(experts)]
     D = layer._exl3_dma
     timing = _DMA_TIMING
@@ -178,28 +196,28 @@ def _dma_issue(layer, sl, experts, dev):
 
 def _dma_prefill(x2d, ids, w16, layer, limit, dev):
     """Prefill with host-resident experts: the experts in HBM (slot or home) in one grouped-GEMM pass on the
-    layer's tables, then the routed experts that live in host memory in batches of B through NS staging slots:
-    the copy of batch j + NS overlaps the compute of batch j (patch_dma_stock.py:41-52 with the busy-expert
-    GEMM of runtime/dma_gemm.py)."""
+    layer's tables, then the host-resident experts in batches of B through NS staging slots: the copy of batch
+    j + NS overlaps the compute of batch j (patch_dma_stock.py:41-52 with the busy-expert GEMM of
+    runtime/dma_gemm.py). Unrouted experts of a batch are copied and skipped. The first NS batches may already be
+    in flight, queued by the previous layer; after the last batch the next layer's first NS batches are queued.
+    No host synchronisation."""
     T, E = x2d.shape[0], layer.E
     k = ids.shape[1]
     n = T * k
     key = dev.index if dev.index is not None else 0
     st = _DMA_STATE[key]
+    D = layer._exl3_dma
     main = torch.cuda.current_stream(dev)
     routes = moe.permute(ids, w16, k, E)
-    counts_h = routes["counts"][:E].cpu().numpy()
-    slot_h = layer.slotof.cpu().numpy()
     out = torch.zeros((T, layer.H), dtype=torch.float32, device=dev)
     tok = routes["token_sorted"][:n].to(torch.int64)
     wsd = routes["weight_sorted"][:n].to(torch.float16)
     counts_d = routes["counts"][:E]
     ws, need = _fat_ws(dev, n, T, E, layer.H, layer.I)
-    cold = [e for e in range(E) if counts_h[e] > 0 and slot_h[e] < 0]
-    cold_set = set(cold)
-    batches = [cold[i:i + _DMA_B] for i in range(0, len(cold), _DMA_B)]
+    batches = _dma_batches(layer)
+    staged_e = {e for b in batches for e in b}
     masks = np.ones((len(batches) + 1, E), np.uint8)
-    masks[0, [e for e in range(E) if e not in cold_set]] = 0          # row 0: the HBM-resident experts
+    masks[0, [e for e in range(E) if e not in staged_e]] = 0          # row 0: the HBM-resident experts
     items = np.zeros((max(len(batches), 1), _DMA_B, 5), np.int64)
     items[:, :, 0] = -1
     pool = st["slots"]
@@ -220,8 +238,16 @@ def _dma_prefill(x2d, ids, w16, layer, limit, dev):
                   counts_d.data_ptr(), masks_d[mask_row].data_ptr(), 0, out.data_ptr(), ws.data_ptr(), need,
                   _lib.stream_ptr(main))
 
-    events = {j: _dma_issue(layer, j % _DMA_NS, batches[j], dev) for j in range(min(_DMA_NS, len(batches)))}
-    if len(cold) < int((counts_h > 0).sum()):
+    pre, D["pre"] = D.get("pre") or {}, {}
+    events = {}
+    for j in range(min(_DMA_NS, len(batches))):
+        p = pre.get(j)
+        if p is not None and p[0] == batches[j] and st["owner"][j % _DMA_NS] == (id(layer), tuple(batches[j])):
+            events[j] = p[1]                    # copied while the previous layer finished, slot not reused since
+            D["prefetched"] += 1
+        else:
+            events[j] = _dma_issue(layer, j % _DMA_NS, batches[j], dev)
+    if len(staged_e) < E:
         run(L, 0)
     if batches:
         tabs = _dma_tables(layer)
@@ -237,7 +263,12 @@ def _dma_prefill(x2d, ids, w16, layer, limit, dev):
             st["free"][j % _DMA_NS] = done
             if j + _DMA_NS < len(batches):
                 events[j + _DMA_NS] = _dma_issue(layer, (j + _DMA_NS) % _DMA_NS, batches[j + _DMA_NS], dev)
-        layer._exl3_dma["batches"] += len(batches)
+        D["batches"] += len(batches)
+    nxt = D.get("next")
+    if _DMA_PREFETCH and nxt is not None and getattr(nxt, "_exl3_dma", None) is not None:
+        nb = _dma_batches(nxt)
+        nxt._exl3_dma["pre"] = {j: (nb[j], _dma_issue(nxt, j % _DMA_NS, nb[j], dev))
+                                for j in range(min(_DMA_NS, len(nb)))}
     return out
 
 

@@ -56,6 +56,8 @@ class ExpertStore:
             self.slotof = torch.arange(E, dtype=torch.int32, device=dev)   # every expert HBM-resident
         else:
             self.slotof = torch.full((E,), -1, dtype=torch.int32, device=dev)
+        # host mirror of slotof, kept by cache.point, so host code can plan staging without reading the device
+        self.slot_host = self.slotof.cpu().numpy().copy()
         self.counts = torch.zeros(E, dtype=torch.int32, device=dev)
         self._c = None
 

@@ -244,6 +244,7 @@ def test_staged_prefill_matches_hbm_layer(dev):
     try:
         exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS = 1, 3, 2, 64
         exl3._DMA_STATE.clear()
+        exl3._DMA_LAST.clear()
         exl3.Exl3MoEMethod().process_weights_after_loading(hs)
         c = ExpertCache([hs], slots=5, every=1, admit=5, warmup=0, async_copy=False, margin_mb=0, elastic=False)
         cnt = np.zeros((1, E))
@@ -269,6 +270,7 @@ def test_staged_prefill_matches_hbm_layer(dev):
     finally:
         exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS = saved[:4]
         exl3._DMA_STATE.clear()
+        exl3._DMA_LAST.clear()
         exl3._DMA_STATE.update(saved[4])
 
 
@@ -308,3 +310,43 @@ def test_plugin_entry_and_tier_split(dev, monkeypatch):
     finally:
         ct_vllm.uninstall(exl3)
         ct_vllm.reset()
+
+
+def test_cross_layer_prefetch_outputs_identical(dev):
+    """Staged prefill through three host-resident layers: with the cross-layer prefetch the second and third
+    layers start on batches the previous layer queued, and every layer's output is bit-identical to the run
+    without it."""
+    import torch
+    from mi355moe import exl3
+    H, I, E, T, k = 512, 256, 24, 200, 4
+    saved = (exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS, exl3._DMA_PREFETCH,
+             dict(exl3._DMA_STATE), dict(exl3._DMA_LAST))
+    try:
+        exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS = 1, 4, 2, 64
+        exl3._DMA_STATE.clear()
+        exl3._DMA_LAST.clear()
+        layers = [_host_store(E, H, I, 1700 + l, dev, exact=False) for l in range(3)]
+        for st in layers:
+            exl3.Exl3MoEMethod().process_weights_after_loading(st)
+        rng = np.random.default_rng(17)
+        ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
+        wts = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+        x = _t(rng.normal(0, 1, (T, H)).astype(np.float32), dev).to(torch.bfloat16)
+        outs = {}
+        for pf in (False, True):
+            exl3._DMA_PREFETCH = pf
+            for st in layers:
+                st._exl3_dma["prefetched"] = 0
+            print(f"three staged layers, prefetch {pf}", flush=True)
+            outs[pf] = [exl3.apply_exl3_fused_moe(x, _t(ids, dev), _t(wts, dev), st, None, None, 10.0) for st in layers]
+            torch.cuda.synchronize()
+            pre = [st._exl3_dma["prefetched"] for st in layers]
+            assert pre == ([0, 2, 2] if pf else [0, 0, 0]), pre
+        for a, b in zip(outs[False], outs[True]):
+            assert torch.equal(a, b)
+    finally:
+        (exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS, exl3._DMA_PREFETCH) = saved[:5]
+        exl3._DMA_STATE.clear()
+        exl3._DMA_STATE.update(saved[5])
+        exl3._DMA_LAST.clear()
+        exl3._DMA_LAST.update(saved[6])

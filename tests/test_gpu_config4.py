@@ -65,6 +65,7 @@ def test_capacity_limited_cache_at_benchmark_shape(dev, monkeypatch):
     exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS = 1, 8, 8, 513
     exl3.FAT_EXPERT_THRESHOLD = 32
     exl3._DMA_STATE.clear()
+    exl3._DMA_LAST.clear()
     ct_vllm.reset()
     try:
         rows = cache.ExpertRows(H, I)
