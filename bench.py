@@ -1,21 +1,35 @@
 #!/usr/bin/env python3
-"""Benchmark: a decode step through 40 routed-expert MoE layers on one MI355X.
+"""Benchmark: a decode step through 40 routed-expert MoE layers on one MI355X, and the legs around it.
 
-Workload (one "step"): T = 4 tokens through 40 MoE layers of H 4096 / I 2048, 384 routed experts (top-8) plus
-1 shared expert per layer, all EXL3 3.0 bpw and resident in HBM (40 x 385 experts, 146 GB). Routing per layer
-is Zipf(1.1) over a seeded permutation (seed 2000 + layer); weights are seeded synthetic (1000 + layer); the
-input is bf16 N(0, 1) and each layer's output is rescaled to unit RMS (bf16) before the next layer. Each layer
-runs routing prep, the fused decode expert kernels (trellis decode + GEMV + SwiGLU + Hadamard transforms) and
-the fixed-order combine; the 40-layer step is replayed as one HIP graph.
+Workload of `value` (one "step"): T = 4 tokens through 40 MoE layers of H 4096 / I 2048, 384 routed experts
+(top-8) plus 1 shared expert per layer, all EXL3 3.0 bpw and resident in HBM (40 x 385 experts, 146 GB). Routing
+per layer is Zipf(1.1) over a seeded permutation (seed 2000 + layer); weights are seeded synthetic (1000 + layer);
+the input is bf16 N(0, 1) and each layer's output is rescaled to unit RMS (bf16) before the next layer. Each layer
+runs routing prep, the fused decode expert kernels (trellis decode + GEMV + SwiGLU + Hadamard transforms) and the
+fixed-order combine; the 40-layer step is replayed as one HIP graph.
 
 Prints one JSON line. `value` is MoE tok/s = T / step time. `roofline` is measured live on the dominant kernel
-(the gate/up decode GEMV) with HIP events on its stream; `cpu_baseline` times the reference's own CPU expert tier
-(compiled from its sources into oracle/_ref) on this host for one layer of the same step.
+(the gate/up decode GEMV) with HIP events on its stream. The other objects of the line:
+  decode_t1       the same 40-layer step at T = 1
+  split_combine   split + combine latency of one decode call (T = 4, 709-slot map), graph-launched
+  prefill         the 16,384-token prefill layer (skewed routing) on the fat-expert grouped GEMM: MFMA utilisation
+  peaks           HBM copy / read rates and a dense fp16 / bf16 GEMM (hipBLASLt) measured in the same run
+  dsv41           the served DSV41 expert shape (H 5120, I 2304, top-6) as a secondary point: the 40-layer decode
+                  step (204 GB of experts) and the 16k prefill layer
+  cache           the capacity-limited configuration: experts in pinned host memory, a 709-slot HBM cache, decode
+                  T = 4 with 8,192-token prefill chunks staged through 8 slots x 8 experts
+  cpu_baseline    the reference's own CPU expert tier (kernels/cpu_avx2/ft_core.h, compiled from its sources into
+                  oracle/_ref) on this host's cores: one layer of the step and the decode layer at T = 1, auto and
+                  EXACT modes, on every physical core of the GPU's NUMA node and on 22 threads, 50 warm-up + 300
+                  timed jobs each (p50 / p90)
 """
 import argparse
 import ctypes
+import gc
+import glob
 import json
 import os
+import subprocess
 import sys
 import time
 
@@ -24,83 +38,335 @@ sys.path.insert(0, os.path.join(ROOT, "dsv41-flash-offload_amd"))
 
 METRIC = "MoE tok/s (decode T=1/4, prefill 16k) + HBM GB/s & MFMA util vs peak"
 HBM_PEAK_GBS = 8000.0
-BYTES_TRELLIS = 3145728             # one 4096 x 2048 matrix at 3 bpw
-BYTES_GU_PARTIAL = 2 * BYTES_TRELLIS + 2 * 4096 * 2                 # gate/up partial kernel: trellis + suh13
-BYTES_EXPERT = 3 * BYTES_TRELLIS + (2 * 4096 + 2 * 2048 + 2048 + 4096) * 2   # all trellis + scales: 9,474,048
+MFMA_PEAK_TFLOPS = 2500.0           # dense fp16 / bf16
+CPU_JOB_SHAPES = ((1, 3), (1, 6), (2, 6), (4, 6), (4, 10))   # (tokens, experts) of the reference's tier jobs
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(routes, T, H, I, E, layer_seed, budget_s=10.0):
-    """Time the reference CPU tier (ft_core.h moe_forward, auto mode) on one layer of the step: repeated calls for
-    at least `budget_s` seconds (and at least 300 calls), p50 / p90 of the per-call times."""
+def trellis_bytes(K, N):
+    return (K // 16) * (N // 16) * 96
+
+
+def expert_bytes(H, I):
+    """Trellis of gate, up and down plus the fp16 scales of one expert (9,474,048 B at 4096 / 2048)."""
+    return 2 * trellis_bytes(H, I) + trellis_bytes(I, H) + (2 * H + 2 * I + I + H) * 2
+
+
+# ------------------------------------------------------------------------------------------ CPU baseline
+
+def _cpulist(s):
+    out = []
+    for part in s.strip().split(","):
+        if part:
+            a, _, b = part.partition("-")
+            out += list(range(int(a), int(b or a) + 1))
+    return out
+
+
+def host_topology():
+    """lscpu-style counts from sysfs: sockets, physical cores, threads per core, NUMA nodes, the NUMA node of the
+    GPU (its PCI device's numa_node; -1 on a single-node host means node 0) and the CPUs this process may use."""
+    allowed = sorted(os.sched_getaffinity(0))
+    core_of = {}
+    for c in allowed:
+        base = f"/sys/devices/system/cpu/cpu{c}/topology/"
+        try:
+            with open(base + "physical_package_id") as f:
+                pkg = int(f.read())
+            with open(base + "core_id") as f:
+                core = int(f.read())
+        except OSError:
+            pkg, core = 0, c
+        core_of[c] = (pkg, core)
+    nodes = {}
+    for d in sorted(glob.glob("/sys/devices/system/node/node[0-9]*")):
+        with open(os.path.join(d, "cpulist")) as f:
+            nodes[int(d.rsplit("node", 1)[1])] = _cpulist(f.read())
+    gpu_node = -1
+    for d in sorted(glob.glob("/sys/class/drm/card[0-9]*/device/numa_node")):
+        try:
+            with open(d) as f:
+                gpu_node = int(f.read())
+            break
+        except (OSError, ValueError):
+            pass
+    node = gpu_node if gpu_node in nodes else (min(nodes) if nodes else 0)
+    node_cpus = [c for c in nodes.get(node, allowed) if c in core_of]
+    seen, phys = set(), []
+    for c in node_cpus:                       # one hardware thread per physical core
+        if core_of[c] not in seen:
+            seen.add(core_of[c])
+            phys.append(c)
+    cores = len(set(core_of.values()))
+    return {"cpus_allowed": len(allowed), "sockets": len({p for p, _ in core_of.values()}), "physical_cores": cores,
+            "threads_per_core": round(len(allowed) / max(1, cores), 2), "numa_nodes": max(1, len(nodes)),
+            "gpu_numa_node": node, "gpu_numa_node_raw": gpu_node, "node_physical_cpus": phys, "allowed": allowed}
+
+
+def cpu_child(spec):
+    """One reference CPU-tier pool (the pool starts once per process): times the requested tasks and prints one
+    JSON line. Tasks: "config0" (one layer at T = 1: top-8 of 384 + the shared expert), "layer" (layer 0 of the
+    decode step: T = 4, top-8 + shared), "jobs" (the reference's tier job shapes at the served DSV41 shape, random
+    experts of a 64-expert layer, x ~ N(0, 0.35), weights 0.15, as experimental/b70-tier/repro/smt_bench.py)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
+    from mi355moe import workload
     from mi355moe.store import synth_scales
+
+    spec = json.loads(spec)
     ref = os.path.join(ROOT, "oracle", "_ref", "libftref.so")
-    if not os.path.exists(ref):
-        return None
     R = ctypes.CDLL(ref)
-    ids, w = routes
-    experts = sorted(set(ids.ravel().tolist()))
-    keep = []
-    ptrs = np.zeros((E + 1, 3), np.int64)
-    for e in experts:
-        mats = []
-        for m in O.synth_expert_trellis(layer_seed, e, H, I):
-            b = np.zeros(m.size + 2048, np.uint16)      # tail pad: the AVX2 decode reads past a tile's end
-            b[: m.size] = m.ravel()
-            mats.append(b)
-        keep.append(mats)
-        ptrs[e] = [mm.ctypes.data for mm in mats]
-    sc = synth_scales(layer_seed, E + 1, H, I)
-    arrs = [np.ascontiguousarray(a) for a in (sc["w13_suh"][:, 0], sc["w13_svh"][:, 0], sc["w13_suh"][:, 1],
-                                               sc["w13_svh"][:, 1], sc["w2_suh"], sc["w2_svh"])]
+    R.ref_moe_forward.restype = ctypes.c_int
     P = lambda a: ctypes.c_void_p(a.ctypes.data)
-    cpus = sorted(os.sched_getaffinity(0))[:16]
+    keep = []
+
+    def add_layer(li, E, H, I, seed, experts):
+        ptrs = np.zeros((E, 3), np.int64)
+        for e in sorted(set(experts)):
+            mats = []
+            for m in O.synth_expert_trellis(seed, e, H, I):
+                b = np.zeros(m.size + 2048, np.uint16)      # tail pad: the AVX2 decode reads past a tile's end
+                b[: m.size] = m.ravel()
+                mats.append(b)
+            keep.append(mats)
+            ptrs[e] = [mm.ctypes.data for mm in mats]
+        sc = synth_scales(seed, E, H, I)
+        arrs = [np.ascontiguousarray(a).view(np.uint16) for a in (sc["w13_suh"][:, 0], sc["w13_svh"][:, 0],
+                                                                   sc["w13_suh"][:, 1], sc["w13_svh"][:, 1],
+                                                                   sc["w2_suh"], sc["w2_svh"])]
+        keep.append((ptrs, arrs))
+        R.ref_add_layer(li, E, H, I, P(ptrs), *[P(a) for a in arrs])
+
+    H, I, E, K = 4096, 2048, 384, 8
+    r0 = workload.zipf_routing(1, K, E, seed=2000)
+    r4 = workload.zipf_routing(4, K, E, seed=2000)
+    tasks = spec["tasks"]
+    if "config0" in tasks or "layer" in tasks:
+        add_layer(0, E + 1, H, I, 1000, list(r0[0].ravel()) + list(r4[0].ravel()) + [E])
+    DH, DI, DE = 5120, 2304, 64
+    if "jobs" in tasks:
+        add_layer(1, DE, DH, DI, 1000, range(DE))
+    cpus = spec["cpus"]
     carr = (ctypes.c_int * len(cpus))(*cpus)
-    R.ref_pool_start(len(cpus), carr, len(cpus))
+    R.ref_pool_start(int(spec["threads"]), carr, len(cpus))
     R.ref_set_limit(ctypes.c_float(10.0))
-    R.ref_add_layer(0, E + 1, H, I, P(ptrs), *[P(a.view(np.uint16)) for a in arrs])
-    x = np.random.default_rng(7).normal(0, 1, (T, H)).astype(np.float16).astype(np.float32)
-    tok = np.repeat(np.arange(T, dtype=np.int32), ids.shape[1])
-    exp = ids.ravel().astype(np.int32)
-    wt = w.ravel().astype(np.float32)
-    out = np.zeros((T, H), np.float32)
-    for _ in range(3):
-        mode = R.ref_moe_forward(0, P(x), T, P(tok), P(exp), P(wt), tok.size, P(out), -1)
-    ts = []
-    t_end = time.perf_counter() + budget_s
-    while len(ts) < 300 or time.perf_counter() < t_end:
-        t0 = time.perf_counter()
-        R.ref_moe_forward(0, P(x), T, P(tok), P(exp), P(wt), tok.size, P(out), -1)
-        ts.append(time.perf_counter() - t0)
-    ts.sort()
-    p50 = ts[len(ts) // 2]
-    return {"p50_layer_ms": p50 * 1e3, "p90_layer_ms": ts[int(len(ts) * 0.9)] * 1e3, "calls": len(ts), "cores": len(cpus),
-            "mode": {0: "AFFINE", 1: "EXACT", 2: "I16"}.get(mode, str(mode)), "experts": len(experts)}
+
+    def run(li, make, mode, warm, timed, budget_s):
+        ts, md = [], -1
+        t_end = time.perf_counter() + budget_s
+        for it in range(warm + timed):
+            x, tok, exp, wt, out = make(it)
+            t0 = time.perf_counter()
+            md = R.ref_moe_forward(li, P(x), x.shape[0], P(tok), P(exp), P(wt), tok.size, P(out), mode)
+            dt = time.perf_counter() - t0
+            if md < 0:
+                raise RuntimeError("reference CPU tier refused the call")
+            if it >= warm:
+                ts.append(dt)
+            if time.perf_counter() > t_end and len(ts) >= 20:
+                break
+        ts.sort()
+        return ts, {0: "AFFINE", 1: "EXACT", 2: "I16"}.get(md, str(md))
+
+    def fixed(ids, w, T, H):
+        ids = np.concatenate([ids, np.full((T, 1), E)], 1)
+        w = np.concatenate([w, np.ones((T, 1), np.float32)], 1)
+        x = np.random.default_rng(7).normal(0, 1, (T, H)).astype(np.float16).astype(np.float32)
+        tok = np.repeat(np.arange(T, dtype=np.int32), ids.shape[1])
+        job = (x, tok, ids.ravel().astype(np.int32), w.ravel().astype(np.float32), np.zeros((T, H), np.float32))
+        return job, len(np.unique(ids))
+
+    res = []
+    budget = float(spec.get("budget_s", 30.0))
+    for name, (ids, w) in (("config0", r0), ("layer", r4)):
+        if name not in tasks:
+            continue
+        T = ids.shape[0]
+        job, nexp = fixed(ids, w, T, H)
+        for mode in spec["modes"]:
+            ts, md = run(0, lambda it: job, mode, 50, 300, budget)
+            p50 = ts[len(ts) // 2]
+            res.append({"task": name, "tokens": T, "experts": nexp, "mode": "auto" if mode < 0 else md,
+                        "mode_used": md, "p50_ms": round(p50 * 1e3, 4), "p90_ms": round(ts[int(len(ts) * 0.9)] * 1e3, 4),
+                        "timed_jobs": len(ts), "warmup_jobs": 50,
+                        "gbs": round(nexp * expert_bytes(H, I) / p50 / 1e9, 2), "tok_s": round(T / p50, 2)})
+    if "jobs" in tasks:
+        rng = np.random.default_rng(0)
+        for m, k in CPU_JOB_SHAPES:
+            def make(it, m=m, k=k):
+                sel = np.stack([rng.choice(DE, k, replace=False) for _ in range(m)])
+                if m > 1:
+                    sel[1:, : k // 3] = sel[0, : k // 3]          # some sharing, as in real decode
+                x = (rng.normal(0, 0.35, (m, DH))).astype(np.float16).astype(np.float32)
+                tok = np.repeat(np.arange(m, dtype=np.int32), k)
+                return (x, tok, sel.ravel().astype(np.int32), np.full(m * k, 0.15, np.float32),
+                        np.zeros((m, DH), np.float32))
+            ts, md = run(1, make, -1, 50, 300, budget / 2)
+            res.append({"task": f"job m{m}k{k}", "shape": "H 5120 / I 2304", "tokens": m, "experts_per_token": k,
+                        "mode": "auto", "mode_used": md, "p50_ms": round(ts[len(ts) // 2] * 1e3, 4),
+                        "p90_ms": round(ts[int(len(ts) * 0.9)] * 1e3, 4), "timed_jobs": len(ts), "warmup_jobs": 50})
+    print(json.dumps({"threads": spec["threads"], "cpus": cpus, "results": res}), flush=True)
 
 
-def traffic_bytes(L, T):
-    """HBM bytes per launch of the gate/up decode kernel at this workload, from the committed rocprofv3 counter
-    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a calibration copy), or None for another workload."""
-    path = os.path.join(ROOT, "profiles", "traffic.json")
-    if L != 40 or T != 4 or not os.path.exists(path):
+def cpu_baseline(L=40, T=4):
+    """The reference CPU tier on this host, in child processes started before this process touches the GPU: (i)
+    every physical core of the GPU's NUMA node (config 0, the step's layer, the tier job shapes; auto and EXACT),
+    (ii) 22 threads as the reference serves it (ct/ct_vllm.py:46,79), placed on this process's CPUs the way the
+    reference's pool places them (cpus[w % ncpus]) when there are fewer than 22."""
+    if not os.path.exists(os.path.join(ROOT, "oracle", "_ref", "libftref.so")):
+        log("cpu baseline: oracle/_ref/libftref.so not built; skipped")
         return None
-    with open(path) as f:
-        return float(json.load(f)["traffic_bytes_per_launch"])
+    topo = host_topology()
+    sets = [{"label": "every physical core of the GPU's NUMA node", "threads": len(topo["node_physical_cpus"]),
+             "cpus": topo["node_physical_cpus"], "tasks": ["config0", "layer", "jobs"], "modes": [-1, 1],
+             "budget_s": 20.0},
+            {"label": "22 threads (the reference's DSV41_CT_THREADS)", "threads": 22, "cpus": topo["allowed"],
+             "tasks": ["config0", "layer"], "modes": [-1], "budget_s": 8.0}]
+    runs = []
+    for s in sets:
+        t0 = time.time()
+        spec = {k: s[k] for k in ("threads", "cpus", "tasks", "modes", "budget_s")}
+        p = subprocess.run([sys.executable, os.path.abspath(__file__), "--cpu-child", json.dumps(spec)],
+                           capture_output=True, text=True, timeout=240)
+        if p.returncode != 0:
+            log(f"cpu baseline child failed ({p.returncode}): {p.stderr[-2000:]}")
+            continue
+        r = json.loads(p.stdout.strip().splitlines()[-1])
+        r["label"] = s["label"]
+        r["oversubscribed"] = s["threads"] > len(s["cpus"])
+        runs.append(r)
+        log(f"cpu baseline: {s['label']}: {time.time() - t0:.1f}s {r['results']}")
+    if not runs:
+        return None
+    main = next((x for x in runs[0]["results"] if x["task"] == "layer" and x["mode"] == "auto"), None)
+    topo_out = {k: topo[k] for k in ("cpus_allowed", "sockets", "physical_cores", "threads_per_core", "numa_nodes",
+                                     "gpu_numa_node", "gpu_numa_node_raw")}
+    return {"value": round(T / (L * main["p50_ms"] * 1e-3), 3), "unit": "tok/s", "cores": runs[0]["threads"],
+            "kind": "reference",
+            "sample": f"layer 0 of the step ({main['experts']} experts, T={T}) on the reference CPU tier "
+                      f"(ft_core.h moe_forward, auto mode = {main['mode_used']}), {main['timed_jobs']} timed jobs "
+                      f"after 50 warm-up, p50 {main['p50_ms']:.3f} ms (p90 {main['p90_ms']:.3f}), scaled to {L} layers",
+            "topology": topo_out, "runs": runs}
 
 
-def bench_prefill(store, E, H, I, reps, tokens=16384, k=8, cap=32):
+# ------------------------------------------------------------------------------------------ GPU legs
+
+def free_gpu():
+    import torch
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+
+
+def synth_stores(E, H, I, L, dev):
+    import torch
+    from mi355moe.store import ExpertStore
+    t0 = time.time()
+    stores = []
+    for l in range(L):
+        stores.append(ExpertStore(E + 1, H, I, device=dev, limit=10.0).synthesize(1000 + l))
+        if l % 10 == 9 or l == L - 1:
+            torch.cuda.synchronize()
+            log(f"stores {H}/{I}: {l + 1}/{L} layers resident ({(l + 1) * (E + 1) * expert_bytes(H, I) / 1e9:.1f} GB) "
+                f"{time.time() - t0:.1f}s")
+    return stores
+
+
+def decode_step(stores, E, H, I, K, T, L, steps, warmup, roofline):
+    """The L-layer decode step at T tokens, replayed as one HIP graph; with `roofline`, the gate/up and down
+    partial-sum kernels' own per-layer launches are captured in graphs of their own and timed between events."""
+    import numpy as np
+    import torch
+    from mi355moe import workload
+    from mi355moe.moe import DecodeRunner
+    dev = stores[0].w13_suh.device
+    routes = [workload.zipf_routing(T, K, E, seed=2000 + l) for l in range(L)]
+    uniq = [len(np.unique(r[0])) for r in routes]
+    runners = []
+    for l in range(L):
+        R = DecodeRunner(E, H, I, T, K, device=dev)
+        R.set_routes(torch.from_numpy(routes[l][0]).to(dev), torch.from_numpy(routes[l][1]).to(dev))
+        runners.append(R)
+    x0 = torch.from_numpy(workload.activations(T, H, seed=7)).to(dev)
+    outs = [torch.empty((T, H), dtype=torch.float32, device=dev) for _ in range(2)]
+
+    def step():
+        # layer l reads the previous output (fp32), rescales it to unit RMS, rounds it through bf16 to the fp16
+        # expert input, and writes its own output
+        src = x0
+        for l in range(L):
+            src = runners[l].layer(stores[l], x=src, out=outs[l % 2], rescale=True)
+        return src
+
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        step()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        final = step()
+    torch.cuda.synchronize()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_start = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    ms_step = ev0.elapsed_time(ev1) / steps
+    out_rms = float(final.float().pow(2).mean().sqrt())
+    step_bytes = float(sum((u + 1) * expert_bytes(H, I) for u in uniq))
+    res = {"ms_step": ms_step, "ms_wall": wall * 1e3 / steps, "uniq": uniq, "step_bytes": step_bytes,
+           "out_rms": out_rms}
+    log(f"decode {H}/{I} T={T} top-{K}: step {ms_step:.3f} ms (wall {res['ms_wall']:.3f} ms), "
+        f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s, final output rms {out_rms:.4f}")
+    if roofline:
+        # every runner's workspace holds its layer's routing records from the step replays above
+        def kernel_graph(phase):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for l in range(L):
+                    runners[l].experts(stores[l], x=outs[0], phases=phase)
+            return g
+
+        def time_graph(g, reps=5):
+            g.replay()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) / (reps * L)     # ms per launch
+
+        g_gu, g_d = kernel_graph(2), kernel_graph(8)
+        res["t_gu"], res["t_d"] = time_graph(g_gu), time_graph(g_d)
+        bgu = 2 * trellis_bytes(H, I) + 2 * H * 2          # gate/up partial kernel: trellis + suh13 per expert
+        res["bytes_gu"] = float(np.mean([(u + 1) * bgu for u in uniq]))
+        res["bytes_d"] = float(np.mean([(u + 1) * trellis_bytes(I, H) for u in uniq]))
+        del g_gu, g_d
+    del graph
+    return res
+
+
+def bench_prefill(store, E, H, I, k, reps, tokens=16384, cap=32):
     """The 16k-token prefill layer: skewed routing (64 hot experts take 60 % of the assignments), every routed
     expert above `cap` routes on the fat-expert grouped GEMM. Returns timings and MFMA utilisation."""
     import numpy as np
     import torch
     from mi355moe import _lib, moe, workload
-    dev = torch.device("cuda", 0)
+    dev = store.w13_suh.device
     ids, w = workload.skewed_routing(tokens, k, E, seed=2000)
     counts = np.bincount(ids.ravel(), minlength=E)
     fat = counts > cap
@@ -132,15 +398,15 @@ def bench_prefill(store, E, H, I, reps, tokens=16384, k=8, cap=32):
         return e0.elapsed_time(e1) / reps
     t_layer = timed(layer)
     t_grouped = timed(grouped)
-    peak = 2.5e15
-    return {"workload": f"prefill {tokens} tokens through one MoE layer, top-{k} skewed routing (64 hot experts take "
-                        f"60 %), experts above {cap} routes on the grouped GEMM, bf16 input",
+    peak = MFMA_PEAK_TFLOPS * 1e12
+    return {"workload": f"prefill {tokens} tokens through one MoE layer (H {H}, I {I}), top-{k} skewed routing (64 "
+                        f"hot experts take 60 %), experts above {cap} routes on the grouped GEMM, bf16 input",
             "tokens": tokens, "fat_experts": int(fat.sum()), "fat_routes": int(counts[fat].sum()),
             "fat_flops": flops, "ms_layer": round(t_layer, 4), "ms_grouped_gemm": round(t_grouped, 4),
             "tok_s": round(tokens / (t_layer * 1e-3), 1),
             "mfma_util_layer": round(flops / (t_layer * 1e-3) / peak, 4),
             "mfma_util_grouped_gemm": round(flops / (t_grouped * 1e-3) / peak, 4),
-            "mfma_peak_tflops": peak / 1e12, "dtype": "fp16 MFMA, fp32 accumulation", "reps": reps}
+            "mfma_peak_tflops": MFMA_PEAK_TFLOPS, "dtype": "fp16 MFMA, fp32 accumulation", "reps": reps}
 
 
 def bench_split(calls=10000, per_graph=100):
@@ -223,6 +489,67 @@ def bench_split(calls=10000, per_graph=100):
     ts.sort()
     res["cpu_baseline"] = {"p50_us": round(ts[len(ts) // 2] * 1e6, 2), "cores": 1, "kind": "port",
                            "sample": "2,000 calls of the oracle's split and combine (C restatement) on one core"}
+    del g
+    return res
+
+
+def calibrate_peaks(dev):
+    """Rates measured in the same run: a 2 GiB device-to-device copy (read + write bytes / time), a 4 GiB read
+    (the library's read probe: 16-byte loads, every byte once) and a dense 8192^3 GEMM through torch.mm
+    (hipBLASLt) in fp16 and bf16."""
+    import torch
+    from mi355moe import _lib
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / reps
+    nb = 2 << 30
+    a = torch.empty(nb // 4, dtype=torch.float32, device=dev).fill_(1.0)
+    b = torch.empty_like(a)
+    t_copy = timed(lambda: b.copy_(a), 10)
+    del a, b
+    nr = 4 << 30
+    r = torch.empty(nr, dtype=torch.uint8, device=dev).fill_(3)
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    t_read = timed(lambda: _lib.call("mm_read_probe", r.data_ptr(), nr, sink.data_ptr(), 0, _lib.stream_ptr()), 10)
+    del r
+    res = {"hbm_copy_gbs": round(2 * nb / t_copy / 1e9, 1), "hbm_read_gbs": round(nr / t_read / 1e9, 1)}
+    n = 8192
+    for name, dt in (("fp16", torch.float16), ("bf16", torch.bfloat16)):
+        A = torch.randn((n, n), dtype=dt, device=dev)
+        B = torch.randn((n, n), dtype=dt, device=dev)
+        C = torch.empty((n, n), dtype=dt, device=dev)
+        t = timed(lambda: torch.mm(A, B, out=C), 20)
+        res[f"gemm_{name}_tflops"] = round(2.0 * n ** 3 / t / 1e12, 1)
+        del A, B, C
+    res["method"] = ("2 GiB torch copy (read + write bytes) and 4 GiB mm_read_probe (read bytes), 10 reps each; "
+                     "torch.mm 8192^3, 20 reps; HIP events")
+    return res
+
+
+def bench_dsv41(args, dev):
+    """The served DSV41 expert shape (H 5120, I 2304, top-6; experimental/b70-tier/repro/rep_ct.py:11): the 40-layer
+    decode step at T = 4 with 40 x 385 experts resident (204 GB) and the 16k prefill layer."""
+    H, I, E, K, L = 5120, 2304, 384, 6, args.layers
+    stores = synth_stores(E, H, I, L, dev)
+    d = decode_step(stores, E, H, I, K, 4, L, args.steps, args.warmup, roofline=False)
+    res = {"workload": f"decode step through {L} MoE layers, T=4, H {H}, I {I}, 384 routed experts top-{K} + 1 shared, "
+                       f"EXL3 3.0 bpw, all experts HBM-resident ({L * (E + 1) * expert_bytes(H, I) / 1e9:.1f} GB)",
+           "ms_per_step": round(d["ms_step"], 4), "tok_s": round(4 / (d["ms_step"] * 1e-3), 2),
+           "bytes_per_step": d["step_bytes"], "hbm_gbs": round(d["step_bytes"] / (d["ms_step"] * 1e-3) / 1e9, 1),
+           "frac_of_peak": round(d["step_bytes"] / (d["ms_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "mean_distinct_experts_per_layer": round(sum(d["uniq"]) / len(d["uniq"]), 2)}
+    if not args.no_prefill:
+        res["prefill"] = bench_prefill(stores[0], E, H, I, K, args.prefill_reps)
+        log(f"dsv41 prefill: {res['prefill']}")
+    del stores
     return res
 
 
@@ -244,7 +571,7 @@ def bench_cache(args):
                        "DSV41_EC_ADMIT": "48", "DSV41_EC_DECAY": "0.9", "DSV41_EC_HYST": "1.0",
                        "DSV41_EC_WARMUP": str(args.ec_warmup), "DSV41_EC_ASYNC": "1",
                        "DSV41_EC_PREFILL_TOKENS": "512", "DSV41_EC_REWARM_AFTER": "4", "DSV41_EC_ELASTIC": "1",
-                       "DSV41_EC_MARGIN_MB": "1500"})
+                       "DSV41_EC_MARGIN_MB": "1500", "DSV41_CPU_TIER": "1" if args.cpu_tier else "0"})
     exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS = 1, 8, 8, 513
     exl3.FAT_EXPERT_THRESHOLD = 32
     rows = cache.ExpertRows(H, I)
@@ -265,6 +592,10 @@ def bench_cache(args):
     c = ct_vllm.EC["cache"]
     assert c is not None and ct_vllm.S["started"]
     log(f"cache: {L} layers registered {time.time() - t0:.1f}s")
+    policy = None
+    if args.cpu_tier:
+        policy = ct_vllm.calibrate()
+        log(f"cache: host tier calibrated {policy}, self-test {ct_vllm.S['selftest']}")
     # pinned -> HBM copy-engine peak (one 2 GB transfer)
     nb = min(2 << 30, bufs[0].nbytes)
     dst = torch.empty(nb, dtype=torch.uint8, device=dev)
@@ -282,10 +613,6 @@ def bench_cache(args):
     rng = np.random.default_rng(2000)
     perms = [np.random.default_rng(2000 + l).permutation(E) for l in range(L)]
     prank = None
-    ones = torch.ones((T, 1), dtype=torch.float32, device=dev)
-    zeros = torch.zeros((T, 1), dtype=torch.long, device=dev)
-    xb = torch.empty((T, H), dtype=torch.bfloat16, device=dev)
-    x16 = torch.empty((T, H), dtype=torch.float16, device=dev)
     exl3._DMA_TIMING = []
     c.timing = []
 
@@ -351,18 +678,16 @@ def bench_cache(args):
     copy_bytes = sum(n for _, _, n in exl3._DMA_TIMING) + sum(n for _, _, n in c.timing)
     dec_tok_s = T * stats["decode_steps"] / max(stats["decode_s"], 1e-9)
     pre_tok_s = TP * stats["prefill_chunks"] / max(stats["prefill_s"], 1e-9)
+    summ = ct_vllm.summary()
     res = {
-        "metric": METRIC, "value": round(dec_tok_s, 3), "unit": "tok/s", "n_gpus": 1, "steps": stats["decode_steps"],
-        "warmup": args.cache_warmup, "ms_per_step": round(stats["decode_s"] * 1e3 / max(1, stats["decode_steps"]), 3),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
-        "data": "synthetic: seeded EXL3 3-bpw trellis + fp16 scales, Zipf(1.1) routing with 5 % rank drift every 64 "
-                "steps, bf16 N(0,1) input",
-        "config": {"workload": f"capacity-limited expert cache: {L} MoE layers (H 4096, I 2048, 384 routed experts "
-                               f"top-8 in pinned host memory + 1 HBM shared expert), {args.slots}-slot HBM cache, "
-                               f"decode T={T} with one {TP}-token prefill chunk every {args.chunk_every} steps, "
-                               "8 staging slots x 8 experts",
-                   "layers": L, "slots": args.slots, "chunk_tokens": TP, "chunk_every": args.chunk_every,
-                   "distinct_host_homes": NH},
+        "workload": f"capacity-limited expert cache: {L} MoE layers (H 4096, I 2048, 384 routed experts top-8 in "
+                    f"pinned host memory + 1 HBM shared expert), {args.slots}-slot HBM cache, decode T={T} with one "
+                    f"{TP}-token prefill chunk every {args.chunk_every} steps, 8 staging slots x 8 experts"
+                    + (", decode misses split between PCIe reads and the host tier" if args.cpu_tier else ""),
+        "layers": L, "slots": args.slots, "chunk_tokens": TP, "chunk_every": args.chunk_every,
+        "distinct_host_homes": NH, "steps": total_steps, "timed_decode_steps": stats["decode_steps"],
+        "warmup_steps": args.cache_warmup,
+        "decode_ms_per_step": round(stats["decode_s"] * 1e3 / max(1, stats["decode_steps"]), 3),
         "hit_rate": round(hits / max(1, hits + misses), 4), "hits": hits, "misses": misses,
         "h2d_gbs": round(copy_bytes / max(copy_ms * 1e-3, 1e-9) / 1e9, 2), "h2d_bytes": copy_bytes,
         "h2d_peak_gbs": round(h2d_peak, 2),
@@ -370,9 +695,17 @@ def bench_cache(args):
         "moe_tok_s": round((T * stats["decode_steps"] + TP * stats["prefill_chunks"]) /
                            max(stats["decode_s"] + stats["prefill_s"], 1e-9), 2),
         "prefill_chunks": stats["prefill_chunks"], "prefill_s": round(stats["prefill_s"], 3),
+        "cpu_tier": bool(args.cpu_tier), "host_experts": summ["cpu_experts"], "host_jobs": summ["host_jobs"],
+        "host_timeouts": summ["timeouts"], "policy": policy,
         "ec": ct_vllm.ec_summary(), "wall_s": round(total_s, 1),
     }
-    print(json.dumps(res), flush=True)
+    ct_vllm.uninstall(exl3)
+    ct_vllm.reset()
+    exl3._DMA_STATE.clear()
+    exl3._DMA_LAST.clear()
+    exl3._WS.clear()
+    del stores, shared, bufs
+    return res
 
 
 def main():
@@ -385,13 +718,16 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true")
     ap.add_argument("--no-split", action="store_true")
+    ap.add_argument("--no-dsv41", action="store_true")
+    ap.add_argument("--no-cache", action="store_true")
+    ap.add_argument("--no-peaks", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="after the measurements, copy 1 GiB device to device 3 times (torch copy kernel of known "
                          "bytes: 1 GiB read + 1 GiB written per launch), to scale HBM byte counters")
     ap.add_argument("--prefill-reps", type=int, default=5)
     ap.add_argument("--workload", choices=("decode", "cache"), default="decode",
-                    help="decode: the 40-layer HBM-resident decode step (+ the 16k prefill layer); cache: the "
-                         "capacity-limited expert cache")
+                    help="decode: the 40-layer HBM-resident decode step and every other leg; cache: the "
+                         "capacity-limited expert cache alone")
     ap.add_argument("--slots", type=int, default=709)
     ap.add_argument("--cache-steps", type=int, default=160)
     ap.add_argument("--chunk-every", type=int, default=64)
@@ -399,164 +735,84 @@ def main():
     ap.add_argument("--home-layers", type=int, default=4)
     ap.add_argument("--ec-warmup", type=int, default=16)
     ap.add_argument("--cache-warmup", type=int, default=48)
+    ap.add_argument("--no-cpu-tier", dest="cpu_tier", action="store_false",
+                    help="cache leg: every decode miss read over PCIe by the GPU (default: the host tier serves the "
+                         "share of the misses the split's cost model gives it, as the reference serves this "
+                         "configuration)")
+    ap.add_argument("--cpu-child", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
+    if args.cpu_child is not None:
+        return cpu_child(args.cpu_child)
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: measures one MI355X only (got --gpus {args.gpus}, WORLD_SIZE {world}); the multi-GPU "
               "expert-parallel design is documented but not built, so N > 1 is not run.", flush=True)
         sys.exit(2)
-    if args.workload == "cache":
-        return bench_cache(args)
+
+    # the CPU baseline runs first, in child processes, before this process touches the GPU
+    cpu = None
+    if args.workload == "decode" and not args.no_cpu_baseline:
+        log("cpu baseline: reference CPU tier")
+        cpu = cpu_baseline(L=args.layers, T=args.tokens)
 
     import numpy as np
     import torch
-    from mi355moe import _lib, workload
-    from mi355moe.moe import DecodeRunner
-    from mi355moe.store import ExpertStore
-
     dev = torch.device("cuda", 0)
+    if args.workload == "cache":
+        r = bench_cache(args)
+        out = {"metric": METRIC, "value": r["decode_tok_s"], "unit": "tok/s", "n_gpus": 1,
+               "steps": r["timed_decode_steps"], "warmup": r["warmup_steps"], "ms_per_step": r["decode_ms_per_step"],
+               "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+               "data": "synthetic: seeded EXL3 3-bpw trellis + fp16 scales, Zipf(1.1) routing with 5 % rank drift "
+                       "every 64 steps, bf16 N(0,1) input",
+               "config": {"workload": r["workload"]}, "cache": r}
+        print(json.dumps(out), flush=True)
+        return
+
     H, I, E, K_TOP, T, L = 4096, 2048, 384, 8, args.tokens, args.layers
-    t0 = time.time()
-    stores = []
-    for l in range(L):
-        stores.append(ExpertStore(E + 1, H, I, device=dev, limit=10.0).synthesize(1000 + l))
-        if l % 10 == 9 or l == L - 1:
-            torch.cuda.synchronize()
-            log(f"stores: {l + 1}/{L} layers resident ({(l + 1) * (E + 1) * BYTES_EXPERT / 1e9:.1f} GB) {time.time() - t0:.1f}s")
-    routes = [workload.zipf_routing(T, K_TOP, E, seed=2000 + l) for l in range(L)]
-    ids_ext = [np.concatenate([r[0], np.full((T, 1), E, np.int64)], 1) for r in routes]
-    w_ext = [np.concatenate([r[1], np.ones((T, 1), np.float32)], 1) for r in routes]
-    uniq = [len(np.unique(r[0])) for r in routes]
-    # one runner (routes + workspace) per layer, so every kernel reads its own layer's routing state
-    runners = []
-    for l in range(L):
-        R = DecodeRunner(E, H, I, T, K_TOP, device=dev)
-        R.set_routes(torch.from_numpy(routes[l][0]).to(dev), torch.from_numpy(routes[l][1]).to(dev))
-        runners.append(R)
-    x0 = torch.from_numpy(workload.activations(T, H, seed=7)).to(dev)
-    outs = [torch.empty((T, H), dtype=torch.float32, device=dev) for _ in range(2)]
-
-    def step():
-        # layer l reads the previous output (fp32), rescales it to unit RMS, rounds it through bf16 to the fp16
-        # expert input, and writes its own output
-        src = x0
-        for l in range(L):
-            src = runners[l].layer(stores[l], x=src, out=outs[l % 2], rescale=True)
-        return src
-
-    # eager warm-up, then capture the 40-layer step as one graph
-    side = torch.cuda.Stream()
-    side.wait_stream(torch.cuda.current_stream())
-    with torch.cuda.stream(side):
-        step()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        final = step()
-    torch.cuda.synchronize()
-    log("graph captured")
-
-    for _ in range(args.warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_start = time.perf_counter()
-    ev0.record()
-    for _ in range(args.steps):
-        graph.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    ms_step = ev0.elapsed_time(ev1) / args.steps
-    ms_wall = wall * 1e3 / args.steps
-    out_rms = float(final.float().pow(2).mean().sqrt())
-    log(f"step {ms_step:.3f} ms (wall {ms_wall:.3f} ms), final output rms {out_rms:.4f}")
-
-    # live roofline of the dominant kernel (gate/up decode GEMV partial sums) and of the down partial sums: each
-    # kernel's 40 per-layer launches are captured in a graph of their own and replayed between HIP events on the
-    # replay stream, so the average launch time carries no host launch gaps. Every runner's workspace holds its
-    # layer's routing records from the step replays above.
-    def kernel_graph(phase):
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g):
-            for l in range(L):
-                runners[l].experts(stores[l], x=outs[0], phases=phase)
-        return g
-
-    def time_graph(g, reps=5):
-        g.replay()
-        torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
-            g.replay()
-        e1.record()
-        torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / (reps * L)     # ms per launch
-
-    g_gu, g_d = kernel_graph(2), kernel_graph(8)
-    t_gu, t_d = time_graph(g_gu), time_graph(g_d)
-    bytes_gu = np.array([(u + 1) * BYTES_GU_PARTIAL for u in uniq], np.float64)
-    bytes_d = np.array([(u + 1) * BYTES_TRELLIS for u in uniq], np.float64)
-    gu_gbs = bytes_gu.mean() / (t_gu * 1e-3) / 1e9
-    d_gbs = bytes_d.mean() / (t_d * 1e-3) / 1e9
-    step_bytes = float(sum((u + 1) * BYTES_EXPERT for u in uniq))
-    step_gbs = step_bytes / (ms_step * 1e-3) / 1e9
-    log(f"gate/up kernel: {t_gu * 1e3:.1f} us avg, {gu_gbs:.0f} GB/s; down kernel: {t_d * 1e3:.1f} us avg, "
+    stores = synth_stores(E, H, I, L, dev)
+    d4 = decode_step(stores, E, H, I, K_TOP, T, L, args.steps, args.warmup, roofline=True)
+    ms_step = d4["ms_step"]
+    gu_gbs = d4["bytes_gu"] / (d4["t_gu"] * 1e-3) / 1e9
+    d_gbs = d4["bytes_d"] / (d4["t_d"] * 1e-3) / 1e9
+    step_gbs = d4["step_bytes"] / (ms_step * 1e-3) / 1e9
+    log(f"gate/up kernel: {d4['t_gu'] * 1e3:.1f} us avg, {gu_gbs:.0f} GB/s; down kernel: {d4['t_d'] * 1e3:.1f} us avg, "
         f"{d_gbs:.0f} GB/s; step {step_gbs:.0f} GB/s")
-
-    # decode at T = 1 through the same 40 layers (its own routing, runners and graph)
-    r1 = [workload.zipf_routing(1, K_TOP, E, seed=2000 + l) for l in range(L)]
-    run1 = []
-    for l in range(L):
-        R = DecodeRunner(E, H, I, 1, K_TOP, device=dev)
-        R.set_routes(torch.from_numpy(r1[l][0]).to(dev), torch.from_numpy(r1[l][1]).to(dev))
-        run1.append(R)
-    x1 = torch.from_numpy(workload.activations(1, H, seed=7)).to(dev)
-    o1 = [torch.empty((1, H), dtype=torch.float32, device=dev) for _ in range(2)]
-
-    def step1():
-        src = x1
-        for l in range(L):
-            src = run1[l].layer(stores[l], x=src, out=o1[l % 2], rescale=True)
-        return src
-    with torch.cuda.stream(side):
-        step1()
-    torch.cuda.current_stream().wait_stream(side)
-    torch.cuda.synchronize()
-    g1 = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g1):
-        step1()
-    for _ in range(args.warmup):
-        g1.replay()
-    torch.cuda.synchronize()
-    ev0.record()
-    for _ in range(args.steps):
-        g1.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    ms1 = ev0.elapsed_time(ev1) / args.steps
-    bytes1 = float(sum((len(np.unique(r[0])) + 1) * BYTES_EXPERT for r in r1))
-    log(f"decode T=1: {ms1:.3f} ms per step, {bytes1 / (ms1 * 1e-3) / 1e9:.0f} GB/s")
+    d1 = decode_step(stores, E, H, I, K_TOP, 1, L, args.steps, args.warmup, roofline=False)
+    ms1 = d1["ms_step"]
+    prefill = None
+    if not args.no_prefill:
+        log("prefill: 16384-token layer")
+        prefill = bench_prefill(stores[0], E, H, I, K_TOP, args.prefill_reps)
+        log(f"prefill: {prefill}")
+    del stores
+    free_gpu()
 
     split_res = None
     if not args.no_split:
         log("split/combine latency (10,000 graph-launched calls)")
         split_res = bench_split()
         log(f"split/combine: {split_res}")
+        free_gpu()
 
-    prefill = None
-    if not args.no_prefill:
-        del g_gu, g_d, g1
-        log("prefill: 16384-token layer")
-        prefill = bench_prefill(stores[0], E, H, I, args.prefill_reps)
-        log(f"prefill: {prefill}")
+    peaks = None
+    if not args.no_peaks:
+        peaks = calibrate_peaks(dev)
+        log(f"peaks: {peaks}")
+        free_gpu()
 
-    cpu = None
-    if not args.no_cpu_baseline:
-        log("cpu baseline: reference CPU tier, one layer")
-        cpu = cpu_baseline((ids_ext[0], w_ext[0]), T, H, I, E, 1000)
+    dsv = None
+    if not args.no_dsv41 and L == 40:
+        log("dsv41 shape: 40 layers of H 5120 / I 2304, top-6")
+        dsv = bench_dsv41(args, dev)
+        log(f"dsv41: {dsv}")
+        free_gpu()
+
+    cache_res = None
+    if not args.no_cache and L == 40:
+        log(f"cache: capacity-limited configuration, {args.cache_steps} steps")
+        cache_res = bench_cache(args)
+        free_gpu()
 
     res = {
         "metric": METRIC,
@@ -574,29 +830,36 @@ def main():
         "config": {"workload": f"decode step through {L} MoE layers, T={T} tokens, H=4096, I=2048, 384 routed experts "
                                "top-8 + 1 shared, EXL3 3.0 bpw, all experts HBM-resident",
                    "layers": L, "tokens": T, "hidden": H, "intermediate": I, "experts": E, "top_k": K_TOP,
-                   "shared_experts": 1, "mean_distinct_experts_per_layer": round(float(np.mean(uniq)), 2)},
+                   "shared_experts": 1, "mean_distinct_experts_per_layer": round(float(np.mean(d4["uniq"])), 2)},
         "roofline": {"bound": "hbm", "achieved": round(gu_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(L, T),
                      "kernel": "mm::k_partial<0> (gate/up decode GEMV partial sums)",
-                     "avg_launch_us": round(float(t_gu) * 1e3, 2),
-                     "bytes_per_launch": round(float(bytes_gu.mean()), 1)},
-        "step_hbm": {"bytes_per_step": step_bytes, "achieved_gbs": round(step_gbs, 1),
+                     "avg_launch_us": round(float(d4["t_gu"]) * 1e3, 2),
+                     "bytes_per_launch": round(float(d4["bytes_gu"]), 1)},
+        "step_hbm": {"bytes_per_step": d4["step_bytes"], "achieved_gbs": round(step_gbs, 1),
                      "frac_of_peak": round(step_gbs / HBM_PEAK_GBS, 4),
-                     "down_kernel_gbs": round(d_gbs, 1), "down_avg_launch_us": round(float(t_d) * 1e3, 2)},
-        "ms_per_step_wall": round(ms_wall, 4),
+                     "down_kernel_gbs": round(d_gbs, 1), "down_avg_launch_us": round(float(d4["t_d"]) * 1e3, 2)},
+        "ms_per_step_wall": round(d4["ms_wall"], 4),
         "decode_t1": {"ms_per_step": round(ms1, 4), "tok_s": round(1 / (ms1 * 1e-3), 2),
-                      "hbm_gbs": round(bytes1 / (ms1 * 1e-3) / 1e9, 1)},
+                      "hbm_gbs": round(d1["step_bytes"] / (ms1 * 1e-3) / 1e9, 1)},
     }
+    if peaks is not None:
+        res["peaks"] = peaks
+        res["roofline"]["frac_of_measured_read"] = round(gu_gbs / peaks["hbm_read_gbs"], 4)
+        res["step_hbm"]["frac_of_measured_read"] = round(step_gbs / peaks["hbm_read_gbs"], 4)
     if split_res is not None:
         res["split_combine"] = split_res
     if prefill is not None:
+        if peaks is not None:
+            gemm = peaks["gemm_fp16_tflops"] * 1e12
+            prefill["mfma_util_layer_vs_measured_gemm"] = round(prefill["fat_flops"] / (prefill["ms_layer"] * 1e-3) / gemm, 4)
         res["prefill"] = prefill
+    if dsv is not None:
+        res["dsv41"] = dsv
+    if cache_res is not None:
+        res["cache"] = cache_res
     if cpu is not None:
-        res["cpu_baseline"] = {"value": round(T / (L * cpu["p50_layer_ms"] * 1e-3), 3), "unit": "tok/s",
-                               "cores": cpu["cores"], "kind": "reference",
-                               "sample": f"one layer of the same step ({cpu['experts']} experts, T={T}) x {cpu['calls']} "
-                                         f"calls, reference CPU tier mode {cpu['mode']}, p50 {cpu['p50_layer_ms']:.3f} ms "
-                                         f"(p90 {cpu['p90_layer_ms']:.3f}) per layer, scaled to {L} layers"}
+        res["cpu_baseline"] = cpu
     print(json.dumps(res), flush=True)
     if args.copy_calibration:
         a = torch.empty(1 << 30, dtype=torch.uint8, device=dev).fill_(1)
@@ -605,6 +868,16 @@ def main():
             b.copy_(a)
         torch.cuda.synchronize()
         log("copy calibration: 3 x 1 GiB device copies done")
+
+
+def traffic_bytes(L, T):
+    """HBM bytes per launch of the gate/up decode kernel at this workload, from the committed rocprofv3 counter
+    summary (FETCH_SIZE and WRITE_SIZE passes scaled by a calibration copy), or None for another workload."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    if L != 40 or T != 4 or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return float(json.load(f)["traffic_bytes_per_launch"])
 
 
 if __name__ == "__main__":

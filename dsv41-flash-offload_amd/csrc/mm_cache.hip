@@ -29,6 +29,35 @@ __global__ __launch_bounds__(256) void k_slot_point(int64_t* __restrict__ gp, in
     if (slotof) slotof[e] = (int32_t)it[4];
 }
 
+// HBM read calibration: each thread streams 16-byte vectors (four in flight) over a grid-stride range; the xor of
+// every word read is folded per workgroup and xor-ed into one word.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_read_probe(const u32x4* __restrict__ src, uint64_t n16, uint32_t* sink)
+{
+    const uint64_t stride = (uint64_t)gridDim.x * blockDim.x;
+    uint64_t i = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    u32x4 acc = { 0u, 0u, 0u, 0u };
+    for (; i + 3 * stride < n16; i += 4 * stride)
+    {
+        const u32x4 a = __builtin_nontemporal_load(src + i);
+        const u32x4 b = __builtin_nontemporal_load(src + i + stride);
+        const u32x4 c = __builtin_nontemporal_load(src + i + 2 * stride);
+        const u32x4 d = __builtin_nontemporal_load(src + i + 3 * stride);
+        acc ^= a ^ b ^ c ^ d;
+    }
+    for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(src + i);
+    __shared__ uint32_t red[256];
+    red[threadIdx.x] = acc.x ^ acc.y ^ acc.z ^ acc.w;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1)
+    {
+        if (threadIdx.x < s) red[threadIdx.x] ^= red[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) atomicXor(sink, red[0]);
+}
+
 }  // namespace mm
 
 using namespace mm;
@@ -46,6 +75,25 @@ int mm_slot_point(int64_t* gate_ptr, int64_t* up_ptr, int64_t* down_ptr, int32_t
     hipLaunchKernelGGL(k_slot_point, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s, gate_ptr, up_ptr, down_ptr,
                        slotof, E, items, n);
     return check_launch("mm_slot_point");
+}
+
+int mm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, int blocks, mm_stream_t stream)
+{
+    MM_CHECK_ARG(src && sink && bytes % 16 == 0 && ((uintptr_t)src & 15) == 0,
+                 "mm_read_probe: need device src (16-byte aligned, bytes a multiple of 16) and sink");
+    MM_CHECK_ARG(blocks >= 0 && blocks <= (1 << 20), "mm_read_probe: blocks must be in [0, 2^20]");
+    if (bytes == 0) return MM_OK;
+    if (blocks == 0)
+    {
+        int dev = 0, cus = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+        blocks = 8 * cus;
+    }
+    hipLaunchKernelGGL(k_read_probe, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                       reinterpret_cast<const u32x4*>(src), bytes / 16, sink);
+    return check_launch("mm_read_probe");
 }
 
 int mm_stage_copy(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int n, mm_stream_t stream)

@@ -55,6 +55,7 @@ _SIGS = {
     "mm_fat_batched": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, vp, vp, i32, vp, vp, sz, vp]),
     "mm_slot_point": (i32, [vp, vp, vp, vp, i32, vp, i32, vp]),
     "mm_stage_copy": (i32, [vp, vp, vp, i32, vp]),
+    "mm_read_probe": (i32, [vp, u64, vp, i32, vp]),
     "mm_synth_u16": (i32, [vp, u64, u64, u64, vp]),
     "mm_synth_layer": (i32, [ctypes.POINTER(MMLayer), u64, vp]),
     "mm_expert_seed": (u64, [u64, u64]),

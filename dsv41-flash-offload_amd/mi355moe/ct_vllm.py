@@ -166,7 +166,14 @@ def calibrate(layer=None, experts=8):
         return (time.perf_counter() - t0) / 5 * 1e3
 
     zc = gpu_t(cold) / len(cold)
-    c1, cn = cpu_t(cold[:1]), cpu_t(cold)
+    serving = _tier.serving()
+    if serving:                     # synchronous host forwards need the mailbox worker stopped
+        _tier.stop()
+    try:
+        c1, cn = cpu_t(cold[:1]), cpu_t(cold)
+    finally:
+        if serving:
+            _tier.start()
     b = max((cn - c1) / max(1, len(cold) - 1), 1e-3)
     a = max(c1 - b, 0.0)
     set_policy(tzc=zc, thit=zc / 400.0, a=a, b=b)

@@ -11,6 +11,7 @@ kernels/cpu_avx2/ft_tier_ext.cpp:36-231, driven from ct/ct_vllm.py:56-87,143-152
   forward(li, x, sel, w, mode)        synchronous forward (tests, the tier's self-check and calibration)
   stats()                             jobs, picks, tokens, empty jobs, busy ns
 """
+import atexit
 import ctypes
 import os
 
@@ -18,7 +19,7 @@ import numpy as np
 
 from . import _lib
 
-_T = {"up": False, "layers": {}, "cpus": [], "threads": 0}
+_T = {"up": False, "running": False, "layers": {}, "cpus": [], "threads": 0}
 
 
 def _cpus_from_env():
@@ -51,6 +52,15 @@ def init(H, I, nlayers, mailbox=None, threads=None, cpus=None, mode=None):
     _lib.call("mm_tier_init", int(threads), carr, len(cpus), mb.get("ctrl"), mb.get("hx"), mb.get("picks"),
               mb.get("hout"), mode, int(H), int(I), int(nlayers))
     _T.update(up=True, cpus=cpus, threads=int(threads), H=int(H), I=int(I), mode=mode, mailbox=bool(mailbox))
+    if not _T.get("atexit"):
+        # the worker and the pool threads must be gone before the interpreter frees the pinned mailbox and homes
+        atexit.register(_at_exit)
+        _T["atexit"] = True
+
+
+def _at_exit():
+    if _T["up"]:
+        shutdown()
 
 
 def set_limit(limit):
@@ -80,19 +90,27 @@ def start(cpu0=None):
     if cpu0 is None:
         cpu0 = _T["cpus"][0] if _T["cpus"] else -1
     _lib.call("mm_tier_start", int(cpu0))
+    _T["running"] = True
 
 
 def stop():
     _lib.call("mm_tier_stop")
+    _T["running"] = False
 
 
 def shutdown():
     _lib.call("mm_tier_shutdown")
-    _T.update(up=False, layers={})
+    _T.update(up=False, running=False, layers={})
 
 
 def running():
+    """The tier is initialised (workers up)."""
     return _T["up"]
+
+
+def serving():
+    """The mailbox worker is running (synchronous forward() calls are refused meanwhile)."""
+    return _T["running"]
 
 
 def forward(li, x, sel, w, mode=-1):

@@ -248,6 +248,12 @@ int mm_synth_u16(uint16_t* dst, uint64_t n, uint64_t seed, uint64_t start, mm_st
 int mm_synth_layer(const mm_layer_t* layer, uint64_t layer_seed, mm_stream_t stream);
 uint64_t mm_expert_seed(uint64_t layer_seed, uint64_t expert);
 
+/* HBM read calibration (no counterpart in the reference; the benchmark's measured read roofline): every byte of
+ * src [bytes] (device memory, 16-byte aligned, bytes a multiple of 16) is loaded once in 16-byte vector loads by a
+ * grid of `blocks` x 256 threads (0: 8 workgroups per CU), and an xor of everything read is written to *sink
+ * (device memory) so that no load can be dropped. */
+int mm_read_probe(const void* src, uint64_t bytes, uint32_t* sink, int blocks, mm_stream_t stream);
+
 /* Convert an fp32 [T][H] activation to the expert input fp16 [T][H] through bf16, optionally rescaling each
  * row to unit RMS first (the decode-chain workload's between-layer step): x16 = fp16(bf16(x * s_t)),
  * s_t = 1/sqrt(mean(x_t^2)) if rescale else 1. Also writes bf16 [T][H] if x_bf16 != NULL. */

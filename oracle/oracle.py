@@ -45,7 +45,8 @@ def build():
 def lib():
     global _LIB
     if _LIB is None:
-        path = os.path.join(_HERE, "libmmoracle.so")
+        # MM_ORACLE_LIB names another build of the same source (the sanitizer build of asan_check.sh)
+        path = os.environ.get("MM_ORACLE_LIB") or os.path.join(_HERE, "libmmoracle.so")
         if not os.path.exists(path):
             build()
         L = ctypes.CDLL(path)

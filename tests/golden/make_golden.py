@@ -11,6 +11,8 @@ Inputs are stored with the outputs, except trellis words, which come from the sy
 (stored as seeds plus a checksum that the tests re-verify).
 
 Run from the repo root:  python tests/golden/make_golden.py
+With --check nothing is written: every vector is recomputed and compared bit for bit with the committed fixture
+(oracle/asan_check.sh runs this against the sanitizer build of the reference kernel, named by MM_REF_LIB).
 """
 import ctypes
 import hashlib
@@ -44,8 +46,35 @@ def sha(a):
 
 
 def main():
-    subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "ref", f"REF={REF}"], check=True)
-    R = ctypes.CDLL(os.path.join(ROOT, "oracle", "_ref", "libftref.so"))
+    check = "--check" in sys.argv[1:]
+    lib = os.environ.get("MM_REF_LIB")
+    if not lib:
+        subprocess.run(["make", "-s", "-C", os.path.join(ROOT, "oracle"), "ref", f"REF={REF}"], check=True)
+        lib = os.path.join(ROOT, "oracle", "_ref", "libftref.so")
+    R = ctypes.CDLL(lib)
+
+    def save(name, **rec):
+        path = os.path.join(OUT, name)
+        if not check:
+            np.savez_compressed(path, **rec)
+            return
+        old = np.load(path, allow_pickle=False)
+        worst = 0.0
+        for k, v in rec.items():
+            a, b = np.asarray(v), old[k]
+            if a.shape != b.shape:
+                raise SystemExit(f"{name}: {k} has another shape than the committed fixture")
+            if a.tobytes() == b.tobytes():
+                continue
+            if a.dtype != np.float32:
+                raise SystemExit(f"{name}: {k} differs from the committed fixture")
+            # fp32 outputs of a build at another optimisation level: the summation order may differ (the AFFINE
+            # tier mode forms KINV * S + KBIAS * sum(x), which amplifies it); the bound is the parity tolerance
+            rel = float(np.abs(a.astype(np.float64) - b).max() / max(np.abs(b).max(), 1e-30))
+            worst = max(worst, rel)
+            if rel > 2e-3:
+                raise SystemExit(f"{name}: {k} differs from the committed fixture (max rel {rel:.2e})")
+        print(f"{name}: {len(rec)} entries equal the committed fixture (fp32 outputs within {worst:.1e})")
 
     # dense weights
     K = N = 256
@@ -54,8 +83,7 @@ def main():
     W = np.empty((K, N), np.float32)
     trp = padded(tr)                       # keep the buffer alive across the call
     R.ref_dense(P(trp), K, N, P(W))
-    np.savez_compressed(os.path.join(OUT, "dense_256x256.npz"), seed=np.uint64(seed), K=K, N=N,
-                        trellis_sha256=sha(tr), W=W.astype(np.float16))
+    save("dense_256x256.npz", seed=np.uint64(seed), K=K, N=N, trellis_sha256=sha(tr), W=W.astype(np.float16))
 
     # single experts at the benchmark shape
     H, I = 4096, 2048
@@ -83,7 +111,7 @@ def main():
         for name, a in zip(("suh_g", "svh_g", "suh_u", "svh_u", "suh_d", "svh_d"), (sg, vg, su, vu, sd, vd)):
             rec[f"{name}{j}"] = a
         rec[f"trellis_sha256_{j}"] = sha(np.concatenate([tg.ravel(), tu.ravel(), td.ravel()]))
-    np.savez_compressed(os.path.join(OUT, "expert_4096x2048.npz"), **rec)
+    save("expert_4096x2048.npz", **rec)
 
     # CPU tier MoE forward, 4 tokens over 6 experts
     E = 6
@@ -111,8 +139,8 @@ def main():
         md = R.ref_moe_forward(0, P(x), T, P(tok), P(exp), P(wts), tok.size, P(out), mode)
         assert md == mode
         rec[f"out_mode{mode}"] = out
-    np.savez_compressed(os.path.join(OUT, "tier_t4.npz"), **rec)
-    print("golden vectors written to", OUT)
+    save("tier_t4.npz", **rec)
+    print("golden vectors checked" if check else f"golden vectors written to {OUT}")
 
 
 if __name__ == "__main__":
