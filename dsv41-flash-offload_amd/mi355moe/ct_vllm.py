@@ -13,6 +13,8 @@
                               cache.ExpertCache
   before_step(ntok)           the engine-step hook's part before a step (ct_vllm.py:459-475): release the cache
                               before prefill-sized steps; the hook calls ec_step after every step
+  install_step_hook(modules)  wraps GPUModelRunner.execute_model of the engine's model-runner modules with
+                              before_step / ec_step (ct_vllm.py:459-488); install(X) calls it
 
   calibrate(), set_policy(...)  the split's cost-model constants measured on this machine (per-expert time of a
                               zero-copy miss on the GPU and of an expert on the host tier), or set by hand
@@ -23,6 +25,7 @@ cores compute from their pinned home rows while the GPU reads the rest zero-copy
 share; the combine then adds the host partial (bounded wait, DSV41_CT_TIMEOUT_S). Without it the policy's
 force_n is 0 and every routed expert runs on the GPU.
 """
+import importlib
 import json
 import os
 
@@ -273,9 +276,48 @@ def before_step(ntok):
         c.release()
 
 
-def install(X):
-    """Wrap the plugin module X (exl3 here, or any module with the same two names)."""
-    if _ORIG:
+RUNNER_MODULES = ("vllm.v1.worker.gpu.model_runner", "vllm.v1.worker.gpu_model_runner")
+
+
+def install_step_hook(modules=RUNNER_MODULES):
+    """Wrap GPUModelRunner.execute_model of each importable module in `modules` (the engine's model runners,
+    ct/ct_vllm.py:459-488): before the step, before_step(total scheduled tokens) (the elastic cache's release
+    before prefill-sized steps); after it, ec_step(). Errors inside the hook are counted (S["hook_errors"]) and
+    never reach the engine. Returns the module names hooked; modules that do not import are skipped."""
+    hooked = []
+    for name in modules:
+        try:
+            mod = importlib.import_module(name)
+        except Exception:
+            continue
+        cls = getattr(mod, "GPUModelRunner", None)
+        if cls is None or getattr(cls.execute_model, "_mi355moe_step_hook", False):
+            continue
+        orig = cls.execute_model
+
+        def execute_model(self, *a, _o=orig, **k):
+            try:
+                so = a[0] if a else k.get("scheduler_output")
+                before_step(int(getattr(so, "total_num_scheduled_tokens", 0) or 0))
+            except Exception:
+                S["hook_errors"] = S.get("hook_errors", 0) + 1
+            r = _o(self, *a, **k)
+            try:
+                ec_step()
+            except Exception:
+                S["hook_errors"] = S.get("hook_errors", 0) + 1
+            return r
+        execute_model._mi355moe_step_hook = True
+        cls.execute_model = execute_model
+        _ORIG.setdefault("runners", []).append((cls, orig))
+        hooked.append(name)
+    return hooked
+
+
+def install(X, runner_modules=RUNNER_MODULES):
+    """Wrap the plugin module X (exl3 here, or any module with the same two names) and the engine's step
+    (install_step_hook over runner_modules)."""
+    if "fused" in _ORIG:
         return
     _ORIG["fused"] = X.apply_exl3_fused_moe
     X.apply_exl3_fused_moe = _fused
@@ -286,13 +328,16 @@ def install(X):
         register(layer)
     X.Exl3MoEMethod.process_weights_after_loading = pwal
     _ORIG["pwal"] = orig_pwal
+    S["step_hooks"] = install_step_hook(runner_modules)
 
 
 def uninstall(X):
-    if not _ORIG:
+    if "fused" not in _ORIG:
         return
     X.apply_exl3_fused_moe = _ORIG.pop("fused")
     X.Exl3MoEMethod.process_weights_after_loading = _ORIG.pop("pwal")
+    for cls, orig in _ORIG.pop("runners", []):
+        cls.execute_model = orig
 
 
 def reset():

@@ -69,3 +69,55 @@ def test_run_batch_builds_staged_inners():
     got.clear()
     dma_gemm.run_batch(D, st, 2, inners, counts, 32, "x", "ts", "ws", 10.0, "out", apply_fat, True)
     assert got == {}                     # no busy expert in batch 2: nothing runs
+
+
+def test_step_hook_releases_before_prefill_steps_and_steps_after(monkeypatch):
+    """install() wraps GPUModelRunner.execute_model of the engine's model-runner module (ct/ct_vllm.py:459-488): a
+    step with more scheduled tokens than the cache's prefill size releases the cache before it runs, every step is
+    followed by ec_step, hook errors never reach the engine, and uninstall() restores the method."""
+    import sys
+    from mi355moe import ct_vllm
+
+    log = []
+
+    class Runner:
+        def execute_model(self, scheduler_output, extra=None):
+            log.append(("exec", scheduler_output.total_num_scheduled_tokens))
+            return "result"
+
+    mod = types.ModuleType("vllm.v1.worker.gpu_model_runner")
+    mod.GPUModelRunner = Runner
+    monkeypatch.setitem(sys.modules, "vllm.v1.worker.gpu_model_runner", mod)
+
+    class Cache:
+        prefill_tokens, elastic, last_ntok = 512, True, 0
+
+        def release(self):
+            log.append(("release",))
+
+        def step(self):
+            log.append(("ec_step",))
+
+    X = types.SimpleNamespace(apply_exl3_fused_moe=lambda *a: None,
+                              Exl3MoEMethod=type("M", (), {"process_weights_after_loading": lambda self, l: None}))
+    ct_vllm.reset()
+    try:
+        ct_vllm.install(X)
+        assert ct_vllm.S["step_hooks"] == ["vllm.v1.worker.gpu_model_runner"]
+        ct_vllm.EC["cache"] = Cache()
+        ct_vllm.S["started"] = True
+        r = Runner().execute_model(types.SimpleNamespace(total_num_scheduled_tokens=8192))
+        assert r == "result" and log == [("release",), ("exec", 8192), ("ec_step",)]
+        log.clear()
+        Runner().execute_model(scheduler_output=types.SimpleNamespace(total_num_scheduled_tokens=4))
+        assert log == [("exec", 4), ("ec_step",)]
+        # a failing hook part is counted, the step still runs
+        ct_vllm.EC["cache"] = types.SimpleNamespace(prefill_tokens=1, elastic=True, last_ntok=0)   # no release()
+        log.clear()
+        assert Runner().execute_model(types.SimpleNamespace(total_num_scheduled_tokens=100)) == "result"
+        assert log == [("exec", 100)] and ct_vllm.S["hook_errors"] == 2
+        ct_vllm.uninstall(X)
+        assert not getattr(Runner.execute_model, "_mi355moe_step_hook", False)
+    finally:
+        ct_vllm.EC["cache"] = None
+        ct_vllm.reset()
