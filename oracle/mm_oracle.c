@@ -416,3 +416,64 @@ MMO_EXPORT void mmo_combine(float* out, const float* Y, const float* w, int T, i
             out[(size_t)t * H + h] = acc;
         }
 }
+
+/* ---------------------------------------------------------------------------------------------
+ * The decode chain's step between layers (a definition of the benchmark workload; the reference has no
+ * counterpart): fp16(bf16(x * s)) per row, s = 1 / sqrt(ss / H) in fp32 (correctly rounded divide and
+ * square root), s = 1 for rescale == 0 or ss == 0. ss is accumulated in fp32 in one fixed order, the one
+ * the device kernels use: 256 partial sums, partial j takes h = j, j + 256, j + 512, ... through fused
+ * multiply-adds; each group of 64 partials is combined by exchange at distances 32, 16, 8, 4, 2, 1 (every
+ * partial adds the one at its index xor the distance); the four group sums add as (g0 + g1) + (g2 + g3).
+ * bf16 rounds to nearest even (a NaN stays a quiet NaN), then fp16 rounds to nearest even.
+ * xb (optional) receives the bf16 bits, xh the fp16 bits, both [T, H].
+ * ------------------------------------------------------------------------------------------- */
+static uint16_t f2bf_rne(float f)
+{
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+MMO_EXPORT float mmo_row_sumsq(const float* row, int H)
+{
+    float p[256], q[64];
+    for (int j = 0; j < 256; ++j) {
+        float ss = 0.0f;
+        for (int h = j; h < H; h += 256) ss = fmaf(row[h], row[h], ss);
+        p[j] = ss;
+    }
+    float g[4];
+    for (int w = 0; w < 4; ++w) {
+        float* v = p + 64 * w;
+        for (int d = 32; d >= 1; d >>= 1) {
+            for (int l = 0; l < 64; ++l) q[l] = v[l] + v[l ^ d];
+            memcpy(v, q, sizeof q);
+        }
+        g[w] = v[0];
+    }
+    return (g[0] + g[1]) + (g[2] + g[3]);
+}
+
+MMO_EXPORT float mmo_row_scale(const float* row, int H)
+{
+    const float tot = mmo_row_sumsq(row, H);
+    return tot > 0.0f ? 1.0f / sqrtf(tot / (float)H) : 1.0f;
+}
+
+MMO_EXPORT void mmo_prepare_input(const float* x, int T, int H, int rescale, uint16_t* xb, uint16_t* xh)
+{
+    for (int t = 0; t < T; ++t) {
+        const float* row = x + (size_t)t * H;
+        const float s = rescale ? mmo_row_scale(row, H) : 1.0f;
+        for (int h = 0; h < H; ++h) {
+            const uint16_t b = f2bf_rne(row[h] * s);
+            const uint32_t bits = (uint32_t)b << 16;
+            float v;
+            memcpy(&v, &bits, 4);
+            if (xb) xb[(size_t)t * H + h] = b;
+            xh[(size_t)t * H + h] = mmo_f2h(v);
+        }
+    }
+}

@@ -19,7 +19,7 @@ What each function restates (paths relative to the reference checkout) and how i
   split            ct/ft_tier_cu_v.cu:16-101             pinned: brute-force argmin over k + set invariants
   permute          patch:204-236,296-312                 pinned: numpy stable argsort + bincount
   combine          ct/ft_tier_cu_v.cu:103-127            pinned: closed form (numpy einsum in float64)
-  prepare_input    build's decode-chain step (no ref.)   pinned: bf16 RNE against hand-computed tie cases + numpy
+  prepare_input    build's decode-chain step (no ref.)   pinned: fixed-order sum against an fma emulation, ties
   synth_u16        build's synthetic generator           pinned: golden checksum + GPU fill agreement
   ec (ec_oracle)   ct/ct_vllm.py:243-427                 pinned: invariants (see tests/test_ec.py)
 """
@@ -64,6 +64,10 @@ def lib():
         L.mmo_expert_seed.restype = ctypes.c_uint64
         L.mmo_expert_seed.argtypes = [ctypes.c_uint64, ctypes.c_uint64]
         L.mmo_synth_u16.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_uint64, ctypes.c_void_p]
+        L.mmo_row_scale.restype = ctypes.c_float
+        L.mmo_row_scale.argtypes = [ctypes.c_void_p, ctypes.c_int]
+        L.mmo_row_sumsq.restype = ctypes.c_float
+        L.mmo_row_sumsq.argtypes = [ctypes.c_void_p, ctypes.c_int]
         _LIB = L
     return _LIB
 
@@ -255,18 +259,31 @@ def bf16_rne(x):
     return u.view(np.float32)
 
 
-def prepare_input(x, rescale=True):
+def prepare_input(x, rescale=True, bits=False):
     """The decode-chain workload's step between layers (a definition of this build's benchmark, not of the
-    reference): each row scaled to unit RMS (scale 1 / sqrt(mean(x^2)) in float64, applied in fp32), rounded to
-    bf16 (RNE), then to fp16. Returns the fp16 values as float32 [T, H]."""
-    x = np.asarray(x, np.float64)
-    if rescale:
-        ms = np.mean(x * x, axis=1, keepdims=True)
-        s = np.where(ms > 0, 1.0 / np.sqrt(np.where(ms > 0, ms, 1.0)), 1.0)
-        y = x.astype(np.float32) * s.astype(np.float32)
-    else:
-        y = x.astype(np.float32)
-    return bf16_rne(y).astype(np.float16).astype(np.float32)
+    reference): each fp32 row scaled to unit RMS, rounded to bf16 (RNE), then to fp16; the scale's sum of
+    squares in the fixed fp32 order of mmo_prepare_input. Returns the fp16 values as float32 [T, H], or with
+    bits=True the (bf16, fp16) bit patterns as uint16."""
+    x = _c(np.atleast_2d(x), np.float32)
+    T, H = x.shape
+    xb = np.empty((T, H), np.uint16)
+    xh = np.empty((T, H), np.uint16)
+    lib().mmo_prepare_input(_p(x), T, H, 1 if rescale else 0, _p(xb), _p(xh))
+    if bits:
+        return xb, xh
+    return xh.view(np.float16).astype(np.float32)
+
+
+def row_scale(row):
+    """The unit-RMS scale of one fp32 row, 1 / sqrt(sum(x^2) / H), its sum in mmo_prepare_input's order."""
+    row = _c(row, np.float32)
+    return float(lib().mmo_row_scale(_p(row), row.size))
+
+
+def row_sumsq(row):
+    """The fp32 sum of squares of one row in mmo_prepare_input's order."""
+    row = _c(row, np.float32)
+    return float(lib().mmo_row_sumsq(_p(row), row.size))
 
 
 def tolerance_metrics(a, b):

@@ -304,3 +304,132 @@ def test_bf16_rne_ties_and_prepare_input():
     y = O.prepare_input(a)
     assert np.allclose(np.sqrt(np.mean(y.astype(np.float64) ** 2, 1)), 1.0, atol=5e-3)
     assert np.array_equal(O.bf16_rne(y), y) and np.array_equal(y.astype(np.float16).astype(np.float32), y)
+
+
+def _fma32(a, s):
+    """fp32 fma(a, a, s), correctly rounded, lane-wise: a*a is exact in float64, the float64 sum's rounding
+    error comes from TwoSum, and a float64 sum that lands on an fp32 midpoint is resolved by that error's sign."""
+    a2 = a.astype(np.float64) ** 2
+    s64 = s.astype(np.float64)
+    hi = a2 + s64
+    bb = hi - a2
+    err = (a2 - (hi - bb)) + (s64 - bb)
+    r = hi.astype(np.float32)
+    other = np.nextafter(r, np.where(hi > r.astype(np.float64), np.inf, -np.inf).astype(np.float32))
+    mid = (r.astype(np.float64) + other.astype(np.float64)) * 0.5 == hi
+    up = np.maximum(r, other)
+    dn = np.minimum(r, other)
+    return np.where(mid & (err > 0), up, np.where(mid & (err < 0), dn, r))
+
+
+def _scale_by_order(row, fused=True, butterfly=True, total=False):
+    """1 / sqrt(sum(x^2) / H) in fp32: 256 interleaved partial sums, each group of 64 combined by exchanges at
+    distance 32 .. 1, the group sums as (g0 + g1) + (g2 + g3); the flags swap in plausible mistakes (an unfused
+    multiply-add, a plain left-to-right sum of the 64 partials)."""
+    H = row.size
+    pad = np.zeros(-(-H // 256) * 256, np.float32)
+    pad[:H] = row
+    lanes = pad.reshape(-1, 256)
+    p = np.zeros(256, np.float32)
+    for k in range(lanes.shape[0]):
+        v = lanes[k]
+        live = np.arange(256) + 256 * k < H
+        nxt = _fma32(v, p) if fused else (v * v).astype(np.float32) + p
+        p = np.where(live, nxt, p).astype(np.float32)
+    g = []
+    for w in range(4):
+        v = p[64 * w:64 * w + 64].copy()
+        if butterfly:
+            for d in (32, 16, 8, 4, 2, 1):
+                v = (v + v[np.arange(64) ^ d]).astype(np.float32)
+            g.append(v[0])
+        else:
+            acc = np.float32(0)
+            for e in v:
+                acc = np.float32(acc + e)
+            g.append(acc)
+    tot = np.float32(np.float32(g[0] + g[1]) + np.float32(g[2] + g[3]))
+    if total:
+        return tot
+    return np.float32(1) / np.sqrt(tot / np.float32(H)) if tot > 0 else np.float32(1)
+
+
+def test_fma_emulation_against_exact_rationals():
+    """The fma emulation against exact rational arithmetic on values built to sit on and near fp32 midpoints."""
+    from fractions import Fraction
+    rng = np.random.default_rng(11)
+    a = rng.normal(0, 1, 4000).astype(np.float32)
+    s = rng.normal(0, 4, 4000).astype(np.float32)
+    # s chosen so that a*a + s is within a few float64 ulps of an fp32 midpoint
+    a[:1000] = (1 + rng.integers(0, 2 ** 11, 1000) * 2.0 ** -11).astype(np.float32)
+    s[:1000] = (np.float32(8.0) + np.float32(2.0 ** -21) * rng.integers(-4, 4, 1000)).astype(np.float32)
+    got = _fma32(a, s)
+
+    def rnd32(q):
+        # exact round-to-nearest-even of a rational to fp32 (normal range)
+        if q == 0:
+            return np.float32(0)
+        sign = -1 if q < 0 else 1
+        q = abs(q)
+        e = q.numerator.bit_length() - q.denominator.bit_length()
+        while Fraction(2) ** e > q:
+            e -= 1
+        while Fraction(2) ** (e + 1) <= q:
+            e += 1
+        ulp = Fraction(2) ** (e - 23)
+        n = q / ulp
+        fl = n.numerator // n.denominator
+        rem = n - fl
+        if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+            fl += 1
+        return np.float32(sign * float(fl * ulp))
+
+    want = np.array([rnd32(Fraction(float(x)) ** 2 + Fraction(float(y))) for x, y in zip(a, s)], np.float32)
+    assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("H", [4096, 5120, 7168, 300, 100])
+def test_prepare_input_fixed_order_scale(H):
+    """mmo_prepare_input's scale equals the fixed-order fp32 sum restated lane by lane in numpy (fma by exact
+    emulation), bit for bit, over rows of several magnitudes; the same restatement with an unfused multiply-add
+    or a left-to-right partial sum disagrees on some row, so the comparison can tell those orders apart."""
+    rng = np.random.default_rng(H)
+    rows = [rng.normal(0, sd, H).astype(np.float32) for sd in (1e-3, 0.3, 1, 2, 7, 40, 300)]
+    rows += [rng.standard_cauchy(H).astype(np.float32) for _ in range(8)]
+    exact = [O.row_scale(r) for r in rows]
+    sums = [O.row_sumsq(r) for r in rows]
+    assert [float(_scale_by_order(r)) for r in rows] == exact
+    assert [float(_scale_by_order(r, total=True)) for r in rows] == sums
+    if H >= 4096:
+        assert any(float(_scale_by_order(r, fused=False, total=True)) != e for r, e in zip(rows, sums))
+        assert any(float(_scale_by_order(r, butterfly=False, total=True)) != e for r, e in zip(rows, sums))
+    for r, e in zip(rows, exact):
+        ref = 1.0 / np.sqrt(np.mean(r.astype(np.float64) ** 2))
+        assert abs(e - ref) <= 4e-7 * ref
+
+
+def test_prepare_input_bits():
+    """Outputs: bf16(x * s) rounded to even, then fp16 (numpy's own conversion); a row of 2.0 has the exact
+    scale 0.5; a zero row keeps scale 1; without rescale the row is converted as is (beyond fp16's range: inf)."""
+    rng = np.random.default_rng(5)
+    H = 4096
+    x = rng.normal(0, 3, (4, H)).astype(np.float32)
+    x[1] = 2.0
+    x[2] = 0.0
+    xb, xh = O.prepare_input(x, bits=True)
+    for t in range(4):
+        s = np.float32(O.row_scale(x[t]))
+        y = (x[t] * s).astype(np.float32)
+        b = O.bf16_rne(y)
+        assert np.array_equal(xb[t], (b.view(np.uint32) >> 16).astype(np.uint16))
+        assert np.array_equal(xh[t], b.astype(np.float16).view(np.uint16))
+    assert O.row_scale(x[1]) == 0.5 and np.all(xh[1].view(np.float16) == 1.0)
+    assert O.row_scale(x[2]) == 1.0 and np.all(xh[2] == 0)
+    big = np.array([[1e5, -7e4, 65504.0, 3.0]], np.float32)
+    xb, xh = O.prepare_input(big, rescale=False, bits=True)
+    with np.errstate(over="ignore"):
+        want = O.bf16_rne(big[0]).astype(np.float16)
+    assert np.array_equal(xh[0], want.view(np.uint16))
+    assert list(xh[0].view(np.float16)[:2]) == [np.inf, -np.inf]
+
+
