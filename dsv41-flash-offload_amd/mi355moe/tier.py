@@ -23,8 +23,8 @@ _T = {"up": False, "running": False, "layers": {}, "cpus": [], "threads": 0}
 
 
 def _cpus_from_env():
-    """DSV41_CT_CPUS ("a-b,c"), else every CPU this process may use except the first (left to the serving
-    process's own threads)."""
+    """DSV41_CT_CPUS ("a-b,c"), else every CPU this process may use except the first two, which are left to the
+    serving process's own threads (the reference's default "2-23" leaves CPUs 0 and 1 likewise, ct_vllm.py:44-49)."""
     v = os.environ.get("DSV41_CT_CPUS", "")
     if v:
         out = []
@@ -33,7 +33,7 @@ def _cpus_from_env():
             out += list(range(int(a), int(b or a) + 1))
         return out
     avail = sorted(os.sched_getaffinity(0))
-    return avail[1:] if len(avail) > 1 else avail
+    return avail[2:] if len(avail) > 2 else (avail[1:] or avail)
 
 
 def _p(a):
