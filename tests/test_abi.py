@@ -1,6 +1,5 @@
 """The C-ABI library loads without a GPU and exports every entry point include/mi355moe.h declares; argument
 validation fails cleanly before any device work."""
-import ctypes
 import os
 import re
 import subprocess

@@ -5,7 +5,6 @@ import os
 import numpy as np
 import pytest
 
-import oracle as O
 from helpers import OracleLayer, make_store, within_tolerance
 
 pytestmark = pytest.mark.gpu

@@ -1,6 +1,4 @@
 """GPU parity of the routing kernels against the oracle (bit-exact for every integer output)."""
-import ctypes
-
 import numpy as np
 import pytest
 

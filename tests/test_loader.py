@@ -2,7 +2,6 @@
 from the synthetic generator loads into exactly the generator's words and scales; plan matching, refusal of the
 mcg codebook and of mismatched shapes."""
 import json
-import os
 
 import numpy as np
 import pytest

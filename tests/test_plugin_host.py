@@ -1,8 +1,6 @@
 """Host-side logic of the plugin surface without a GPU: install / uninstall wrapping, run_batch's staged inners."""
 import types
 
-import pytest
-
 
 def test_install_wraps_and_uninstall_restores():
     from mi355moe import ct_vllm
