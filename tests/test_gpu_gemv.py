@@ -155,10 +155,10 @@ def test_layer_input_types_and_rescale(dev):
     assert ok, m
 
 
-@pytest.mark.parametrize("T,k,E", [(200, 6, 6), (60, 4, 8)])
+@pytest.mark.parametrize("T,k,E", [(200, 6, 6), (60, 4, 8), (128, 8, 40)])
 def test_many_routes_per_expert_chunks(dev, T, k, E):
     """Experts with more routes than one MFMA pass (16), all on the decode path: through the permutation (> 1024
-    routes) and through the in-kernel routing."""
+    routes) and through the in-kernel routing (up to its limit of 1024 routes per call)."""
     import torch
     from mi355moe import moe
     H, I = 512, 256
