@@ -385,17 +385,17 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
 // ------------------------------------------------------------------------------------ 3. gate/up epilogue
 
 // For each of NS streams i: a[i] += p[i][q * stride + lane], b[i] += p[i][q * stride + lane + 64] for
-// q = 0 .. np - 1 in ascending q. Eight pieces of every stream are loaded before any is added (pieces past np
-// reload piece np - 1 and are not added), so a short count costs one memory round trip instead of one per piece.
-template <int NS>
-__device__ __forceinline__ void sum_pieces(const float* const (&p)[NS], size_t stride, int np, int lane, float (&a)[NS],
-                                           float (&b)[NS])
+// q = 0 .. np - 1 in ascending q. BATCH pieces of every stream are loaded before any is added (pieces past np
+// reload piece np - 1 and are not added), so a count up to BATCH costs one memory round trip.
+template <int NS, int BATCH>
+__device__ __forceinline__ void sum_pieces_batched(const float* const (&p)[NS], size_t stride, int np, int lane,
+                                                   float (&a)[NS], float (&b)[NS])
 {
-    for (int q0 = 0; q0 < np; q0 += 8)
+    for (int q0 = 0; q0 < np; q0 += BATCH)
     {
-        float va[NS][8], vb[NS][8];
+        float va[NS][BATCH], vb[NS][BATCH];
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < BATCH; ++k)
 #pragma unroll
             for (int i = 0; i < NS; ++i)
             {
@@ -404,7 +404,7 @@ __device__ __forceinline__ void sum_pieces(const float* const (&p)[NS], size_t s
                 vb[i][k] = pk[lane + 64];
             }
 #pragma unroll
-        for (int k = 0; k < 8; ++k)
+        for (int k = 0; k < BATCH; ++k)
             if (q0 + k < np)
 #pragma unroll
                 for (int i = 0; i < NS; ++i)
@@ -413,6 +413,18 @@ __device__ __forceinline__ void sum_pieces(const float* const (&p)[NS], size_t s
                     b[i] += vb[i][k];
                 }
     }
+}
+
+// Up to 8 pieces (4 or more active experts per call on the whole GPU) in one round trip of 8 loads per stream;
+// more (calls of 1-3 tokens, up to 24 pieces) in one round trip of 24.
+template <int NS>
+__device__ __forceinline__ void sum_pieces(const float* const (&p)[NS], size_t stride, int np, int lane, float (&a)[NS],
+                                           float (&b)[NS])
+{
+    if (np <= 8)
+        sum_pieces_batched<NS, 8>(p, stride, np, lane, a, b);
+    else
+        sum_pieces_batched<NS, 24>(p, stride, np, lane, a, b);
 }
 
 // Sum of p[0 .. count) by one wave, split so its first load shares a round trip with the loads after it:
