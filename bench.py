@@ -673,6 +673,8 @@ def bench_cache(args):
             log(f"cache: step {step}/{total_steps} decode {dt * 1e3:.1f} ms {ct_vllm.summary()}")
     total_s = time.perf_counter() - t_all
     st = ct_vllm.S["stats"].tolist()
+    if hit0 is None:                      # every step was a warm-up step
+        hit0 = st
     hits, misses = st[0] - hit0[0], st[1] - hit0[1]
     copy_ms = sum(a.elapsed_time(b) for a, b, _ in exl3._DMA_TIMING) + sum(a.elapsed_time(b) for a, b, _ in c.timing)
     copy_bytes = sum(n for _, _, n in exl3._DMA_TIMING) + sum(n for _, _, n in c.timing)

@@ -55,6 +55,7 @@ _SIGS = {
     "mm_fat_batched": (i32, [ctypes.POINTER(MMLayer), vp, i32, i32, i32, vp, vp, vp, vp, i32, vp, vp, sz, vp]),
     "mm_slot_point": (i32, [vp, vp, vp, vp, i32, vp, i32, vp]),
     "mm_stage_copy": (i32, [vp, vp, vp, i32, vp]),
+    "mm_copy_stream": (i32, [i32, i32, vp, ctypes.POINTER(vp)]),
     "mm_read_probe": (i32, [vp, u64, vp, i32, vp]),
     "mm_synth_u16": (i32, [vp, u64, u64, u64, vp]),
     "mm_synth_layer": (i32, [ctypes.POINTER(MMLayer), u64, vp]),
@@ -123,3 +124,31 @@ def stream_ptr(stream=None):
     import torch
     s = stream if stream is not None else torch.cuda.current_stream()
     return s.cuda_stream
+
+
+# copy stream roles (index of mm_copy_stream)
+COPY_STAGING, COPY_CACHE = 0, 1
+COPY_UNVERIFIED = 1
+_COPY_STREAMS = {}
+
+
+def copy_stream(device, index, compute=None):
+    """torch stream over the library's copy stream `index` of `device` for work that overlaps `compute` (default:
+    the device's current stream): a stream checked to run on another hardware queue than `compute`."""
+    import warnings
+    import torch
+    dev = torch.device(device)
+    d = dev.index if dev.index is not None else torch.cuda.current_device()
+    comp = compute if compute is not None else torch.cuda.current_stream(d)
+    key = (d, index, comp.cuda_stream)
+    s = _COPY_STREAMS.get(key)
+    if s is None:
+        out = vp()
+        rc = load().mm_copy_stream(d, index, comp.cuda_stream, ctypes.byref(out))
+        if rc == COPY_UNVERIFIED:
+            warnings.warn(f"mi355moe: no copy stream on device {d} was seen to run beside the compute stream; copies "
+                          "may serialise with compute (raise GPU_MAX_HW_QUEUES)")
+        elif rc != 0:
+            check(rc, "mm_copy_stream")
+        s = _COPY_STREAMS[key] = torch.cuda.ExternalStream(out.value, device=torch.device("cuda", d))
+    return s

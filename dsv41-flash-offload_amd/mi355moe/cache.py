@@ -319,8 +319,10 @@ class ExpertCache:
         for li, (ev, _) in per_layer.items():            # victims back to their home copies (compute stream)
             point(self.layers[li], ev, main)
         if self.async_copy:
-            if self.side is None:
-                self.side = torch.cuda.Stream(main.device)
+            side = _lib.copy_stream(main.device, _lib.COPY_CACHE, main)
+            if self.side is not None and side is not self.side:
+                side.wait_stream(self.side)               # copies on an earlier copy stream stay ordered
+            self.side = side
             self.side.wait_stream(main)                   # slots are free once every earlier reader ran
             cs = self.side
         else:

@@ -171,9 +171,7 @@ def _dma_issue(layer, sl, experts, dev):
     slot's last reader (patch:100-124). Returns the copy's event."""
     key = dev.index if dev.index is not None else 0
     st = _DMA_STATE[key]
-    if st["copy"] is None:
-        st["copy"] = torch.cuda.Stream(dev)
-    cs = st["copy"]
+    cs = st["copy"] = _lib.copy_stream(dev, _lib.COPY_STAGING)
     if st["free"][sl] is not None:
         cs.wait_event(st["free"][sl])
     pool = st["slots"]

@@ -5,7 +5,8 @@
  *   - All pointers are caller-owned: device memory, or host memory allocated with mm_host_alloc (mapped,
  *     coherent) where a parameter says "host-mapped". The library allocates nothing per call.
  *   - `stream` is a hipStream_t (0 = the null stream). Work is enqueued on it; no entry point synchronises
- *     the host, so every call can be captured into a HIP graph.
+ *     the host, so every call can be captured into a HIP graph (except mm_copy_stream, a set-up call whose first
+ *     call for a compute stream synchronises it).
  *   - Return 0 on success or a negative MM_ERR_* code; mm_last_error() gives a thread-local message.
  *   - Calls on distinct streams with distinct buffers are independent; calls sharing a workspace race.
  *
@@ -238,6 +239,22 @@ int mm_slot_point(int64_t* gate_ptr, int64_t* up_ptr, int64_t* down_ptr, int32_t
  * copy-engine transfers (hipMemcpyAsync) enqueued on `stream`. A copy whose source and destination both continue
  * the previous one is merged into it. Returns the number of transfers enqueued (>= 0) or a negative error. */
 int mm_stage_copy(const uint64_t* dst, const uint64_t* src, const uint64_t* bytes, int n, mm_stream_t stream);
+
+/* Copy stream `index` (0 .. MM_COPY_STREAMS - 1) of `device` for work that must overlap the kernels of `compute`
+ * (a stream of that device, or NULL for its null stream); replaces the reference's side streams for staging and
+ * cache copies (torch.cuda.Stream(dev) at ct/ct_vllm.py:358 and patches/vllm-exl3-host-dma.patch:99,116).
+ * HIP spreads streams over a few shared hardware queues (GPU_MAX_HW_QUEUES, 4 by default), so an ordinary side
+ * stream can share the compute stream's queue, and its transfers then wait for the compute kernels queued before
+ * them. The library keeps its own non-blocking streams and, on the first call for a (device, compute stream),
+ * checks that the one it returns runs while `compute` is held (it synchronises both streams, holds `compute` with
+ * a one-lane kernel that ends when the host releases it, and waits up to 50 ms for an empty kernel on the
+ * candidate), trying up to 8 streams; later calls return the same stream at once. Different indices get
+ * different streams where one is free. Returns MM_OK with *out the hipStream_t, MM_COPY_UNVERIFIED (> 0) with
+ * *out a usable stream that no check could clear, or a negative error (also when `compute` is capturing a
+ * graph). Streams live until the process ends. */
+#define MM_COPY_STREAMS 4
+#define MM_COPY_UNVERIFIED 1
+int mm_copy_stream(int device, int index, mm_stream_t compute, mm_stream_t* out);
 
 /* Synthetic trellis words: word i of a stream with `seed` is bits 16*(i%4)..+15 of
  * splitmix64(seed + (i/4 + 1) * 0x9E3779B97F4A7C15). Fills dst[j] = word(start + j) for j < n. */

@@ -71,6 +71,51 @@ def test_stage_copy_merges_and_moves_bytes(dev):
     assert np.array_equal(got, exp)
 
 
+def test_copy_streams_checked_kept_and_ordered(dev):
+    """mm_copy_stream: a stream seen to run beside the compute stream (MM_OK, not MM_COPY_UNVERIFIED), the same one
+    on later calls, another one for another index; bad indices, devices and a capturing compute stream are errors;
+    a staging copy on it ordered after the compute stream's write and before its read moves the right bytes."""
+    import ctypes
+    import torch
+    from mi355moe import _lib, cache
+    from mi355moe.hostmem import HostBuffer
+    print("copy streams", flush=True)
+    main = torch.cuda.current_stream()
+
+    def raw(d, i, comp):
+        p = _lib.vp()
+        return _lib.load().mm_copy_stream(d, i, comp, ctypes.byref(p)), p.value
+    rc0, p0 = raw(dev.index or 0, 0, main.cuda_stream)
+    rc0b, p0b = raw(dev.index or 0, 0, main.cuda_stream)
+    rc1, p1 = raw(dev.index or 0, 1, main.cuda_stream)
+    assert (rc0, rc0b, rc1) == (0, 0, 0)
+    assert p0 == p0b and p0 != p1 and p0 not in (None, main.cuda_stream)
+    assert _lib.copy_stream(dev, 0).cuda_stream == p0
+    for d, i in ((0, -1), (0, 4), (-1, 0), (torch.cuda.device_count(), 0)):
+        assert raw(d, i, main.cuda_stream)[0] < 0
+    side = torch.cuda.Stream()
+    one = torch.ones(1, device=dev)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        rc_cap = raw(dev.index or 0, 2, torch.cuda.current_stream().cuda_stream)[0]
+        one.add_(1)
+    assert rc_cap < 0
+    n = 3 << 20
+    hb = HostBuffer(n)
+    src = hb.array(np.uint8)
+    src[:] = np.random.default_rng(2).integers(0, 256, n, dtype=np.uint8)
+    dst = torch.empty(n, dtype=torch.uint8, device=dev)
+    dst.fill_(7)                                       # compute-stream write the copy must follow
+    cs = _lib.copy_stream(dev, _lib.COPY_STAGING)
+    cs.wait_stream(main)
+    cache.stage_copy([(dst.data_ptr(), hb.ptr, n)], cs)
+    ev = torch.cuda.Event()
+    ev.record(cs)
+    main.wait_event(ev)
+    assert np.array_equal(dst.cpu().numpy(), src)
+
+
 def test_host_resident_experts_zero_copy_equal_hbm(dev):
     """Experts read over PCIe from the pinned home give the HBM store's exact bits (same kernels, same words) and
     match the oracle; the synthetic words land in the host rows."""
