@@ -239,6 +239,13 @@ static int copy_choose(CopyDevice& D, int device, int index, hipStream_t compute
     hipError_t e = hipStreamIsCapturing(compute, &cap);
     if (e != hipSuccess) return set_error(MM_ERR_HIP, "mm_copy_stream: hipStreamIsCapturing: %s", hipGetErrorString(e));
     MM_CHECK_ARG(cap == hipStreamCaptureStatusNone, "mm_copy_stream: the compute stream is capturing a graph");
+    if (compute)
+    {
+        hipDevice_t sd = -1;
+        e = hipStreamGetDevice(compute, &sd);
+        if (e != hipSuccess) return set_error(MM_ERR_HIP, "mm_copy_stream: hipStreamGetDevice: %s", hipGetErrorString(e));
+        MM_CHECK_ARG(sd == device, "mm_copy_stream: the compute stream belongs to device %d, not %d", (int)sd, device);
+    }
     if (!D.flag)
     {
         e = hipHostMalloc((void**)&D.flag, 64, hipHostMallocMapped | hipHostMallocPortable | hipHostMallocCoherent);

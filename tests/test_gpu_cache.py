@@ -93,6 +93,11 @@ def test_copy_streams_checked_kept_and_ordered(dev):
     assert _lib.copy_stream(dev, 0).cuda_stream == p0
     for d, i in ((0, -1), (0, 4), (-1, 0), (torch.cuda.device_count(), 0)):
         assert raw(d, i, main.cuda_stream)[0] < 0
+    comp = torch.cuda.Stream()                         # another compute stream: its own checked copy stream
+    rc2, p2 = raw(dev.index or 0, 0, comp.cuda_stream)
+    assert rc2 == 0 and p2 not in (None, comp.cuda_stream)
+    with torch.cuda.stream(comp):
+        assert _lib.copy_stream(dev, 0).cuda_stream == p2
     side = torch.cuda.Stream()
     one = torch.ones(1, device=dev)
     torch.cuda.synchronize()
