@@ -18,8 +18,16 @@ constexpr float HAD = 0.088388347648f;
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float h2f(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
-__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)f); }   // RNE
-__device__ __forceinline__ float r16(float f) { return (float)(_Float16)f; }
+// fp32 -> fp16 rounds the fp32 value it is given (RNE). The empty asm hides where the value came from: otherwise
+// the compiler folds a multiply and the rounding after it into one v_fma_mix*_f16, which rounds the exact product
+// to fp16 once, where the reference rounds the fp32 product first (1 ulp apart on rare inputs).
+__device__ __forceinline__ float fp32_operand(float f)
+{
+    asm("" : "+v"(f));
+    return f;
+}
+__device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uint16_t, (_Float16)fp32_operand(f)); }
+__device__ __forceinline__ float r16(float f) { return (float)(_Float16)fp32_operand(f); }
 
 // fp32 -> bf16 bits, round to nearest even; NaN stays a (quiet) NaN.
 __device__ __forceinline__ uint16_t f2bf(float f)

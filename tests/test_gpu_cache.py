@@ -40,9 +40,10 @@ def test_slot_point_last_item_wins_and_skips_out_of_range(dev):
             for j in range(3):
                 exp[j][e] = it[1 + j]
             exp_s[e] = it[4]
+    items_d = _t(items, dev)
     print("slot point 300 items", flush=True)
     _lib.call("mm_slot_point", tabs[0].data_ptr(), tabs[1].data_ptr(), tabs[2].data_ptr(), slotof.data_ptr(), E,
-              _t(items, dev).data_ptr(), len(items), _lib.stream_ptr())
+              items_d.data_ptr(), len(items), _lib.stream_ptr())
     torch.cuda.synchronize()
     for j in range(3):
         assert np.array_equal(tabs[j].cpu().numpy(), exp[j])

@@ -176,6 +176,56 @@ def test_many_routes_per_expert_chunks(dev, T, k, E):
     assert ok, m
 
 
+def _operand_index(k):
+    """Position of input row k in the MFMA operand order of the decode path's transformed inputs."""
+    r = k & 15
+    d = r >> 1
+    return (k & ~31) + 8 * (d & 3) + 4 * ((k >> 4) & 1) + 2 * (d >> 2) + (r & 1)
+
+
+def test_route_prep_transform_bitwise_vs_oracle(dev):
+    """The decode path's input transform xt = r16(FWHT128(x * suh) * HAD), read back from the workspace after the
+    route-prep phase alone, equals the oracle's prep_block bit for bit for every route, matrix and row: the fp32
+    product is rounded before the fp16 rounding, as the reference rounds (a multiply folded into the fp16
+    conversion would round the exact product once and differ on about 1 element in 4,000)."""
+    import torch
+    from mi355moe import _lib
+    H, I, E, T, k = 4096, 2048, 17, 3, 4
+    st = make_store(E, H, I, 4100, device=dev)
+    rng = np.random.default_rng(41)
+    ids = np.stack([rng.choice(E, k, replace=False) for _ in range(T)]).astype(np.int64)
+    x16 = rng.normal(0, 1, (T, H)).astype(np.float16)
+    n = T * k
+    wsb = _lib.load().mm_gemv_workspace(n, E, H, I)
+    ws = torch.zeros(wsb, dtype=torch.uint8, device=dev)
+    xd, idd = _t(x16, dev), _t(ids, dev)       # held: a temporary's memory could be handed out again before the launch
+    print("route prep only, 12 routes at 4096/2048", flush=True)
+    _lib.call("mm_expert_gemv", st.mm_layer(), xd.data_ptr(), _lib.DTYPE_F16, 0, T, n, k, idd.data_ptr(), None, None,
+              None, None, n, None, ws.data_ptr(), wsb, 1, _lib.stream_ptr())
+    torch.cuda.synchronize()
+    w = ws.cpu().numpy()
+    # workspace layout of the decode path: expert records, counts, pos_of, route_at, e_at, transformed inputs, ...
+    al = lambda v: (v + 255) & ~255
+    nb, cap = (H + 511) // 512, min(32, max(4, 8192 // n))
+    sizes = [al(min(n, E) * 48), al(8), al(n * 4), al(n * 4), al(n * 4), al(n * 2 * H * 2), al(n * 2 * nb * 4),
+             al(cap * n * 2 * I * 4), al(n * I * 2), al(n * (I // 128) * 4), al(cap * n * H * 4)]
+    assert sum(sizes) == wsb, "decode workspace layout changed"
+    off = np.cumsum([0] + sizes)
+    pos_of = w[off[2]:off[2] + n * 4].view(np.int32)
+    xa = w[off[5]:off[5] + n * 2 * H * 2].view(np.uint16).reshape(n, 2, H)
+    oi = np.array([_operand_index(j) for j in range(H)])
+    suh = st.w13_suh.cpu().numpy()
+    bad = 0
+    for s in range(n):
+        e, t = int(ids.flat[s]), s // k
+        for m in range(2):
+            got = xa[pos_of[s], m][oi]
+            exp = np.concatenate([O.prep_block(x16[t, b:b + 128].astype(np.float32), suh[e, m, b:b + 128])
+                                  for b in range(0, H, 128)]).astype(np.float16).view(np.uint16)
+            bad += int((got != exp).sum())
+    assert bad == 0, f"{bad} of {n * 2 * H} transformed inputs differ from the oracle"
+
+
 @pytest.mark.parametrize("H", [4096, 5120, 7168, 300])
 def test_prepare_input_matches_oracle(dev, H):
     """mm_prepare_input bit for bit against the oracle's fixed-order restatement (the scale's fp32 sum of
@@ -194,8 +244,8 @@ def test_prepare_input_matches_oracle(dev, H):
         print(f"prepare_input H={H} rescale={rescale}", flush=True)
         xb = torch.empty((T, H), dtype=torch.int16, device=dev)
         xh = torch.empty((T, H), dtype=torch.int16, device=dev)
-        _lib.call("mm_prepare_input", _t(x, dev).data_ptr(), T, H, rescale, xb.data_ptr(), xh.data_ptr(),
-                  _lib.stream_ptr())
+        xd = _t(x, dev)
+        _lib.call("mm_prepare_input", xd.data_ptr(), T, H, rescale, xb.data_ptr(), xh.data_ptr(), _lib.stream_ptr())
         torch.cuda.synchronize()
         wb, wh = O.prepare_input(x, rescale=bool(rescale), bits=True)
         assert np.array_equal(xb.cpu().numpy().view(np.uint16), wb)

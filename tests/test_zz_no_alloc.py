@@ -49,7 +49,7 @@ def test_noalloc_decode_equals_workspace_decode(dev):
     # beyond the scratch: a clear error, no device work
     T = 8
     ids = np.tile(np.arange(9, dtype=np.int64), (T, 1))
+    idd, wd, out = _t(ids, dev), _t(np.ones((T, 9), np.float32), dev), torch.empty((T, H), device=dev)
     with pytest.raises(RuntimeError, match="scratch"):
-        _lib.call("mm_moe_decode_noalloc", st.mm_layer(), x.data_ptr(), _lib.DTYPE_BF16, 1, T, 9,
-                  _t(ids, dev).data_ptr(), _t(np.ones((T, 9), np.float32), dev).data_ptr(), T * 9,
-                  torch.empty((T, H), device=dev).data_ptr(), _lib.stream_ptr())
+        _lib.call("mm_moe_decode_noalloc", st.mm_layer(), x.data_ptr(), _lib.DTYPE_BF16, 1, T, 9, idd.data_ptr(),
+                  wd.data_ptr(), T * 9, out.data_ptr(), _lib.stream_ptr())
