@@ -650,8 +650,9 @@ def bench_cache(args):
             ts = time.perf_counter()
             run_layers(xp, lambda l: (perm_d[l][pr_ids], pr_w), TP)
             torch.cuda.synchronize()
-            stats["prefill_s"] += time.perf_counter() - ts
-            stats["prefill_chunks"] += 1
+            if step >= args.cache_warmup:          # the same window as the timed decode steps
+                stats["prefill_s"] += time.perf_counter() - ts
+                stats["prefill_chunks"] += 1
             ct_vllm.ec_step()
             log(f"cache: prefill chunk at step {step}: {time.perf_counter() - ts:.2f}s {ct_vllm.ec_summary()}")
         routes = [workload.zipf_ids(T, K, E, rng, perms[l]) for l in range(L)]
@@ -731,12 +732,14 @@ def main():
                     help="decode: the 40-layer HBM-resident decode step and every other leg; cache: the "
                          "capacity-limited expert cache alone")
     ap.add_argument("--slots", type=int, default=709)
-    ap.add_argument("--cache-steps", type=int, default=160)
+    ap.add_argument("--cache-steps", type=int, default=480)
     ap.add_argument("--chunk-every", type=int, default=64)
     ap.add_argument("--chunk-tokens", type=int, default=8192)
     ap.add_argument("--home-layers", type=int, default=4)
     ap.add_argument("--ec-warmup", type=int, default=16)
-    ap.add_argument("--cache-warmup", type=int, default=48)
+    ap.add_argument("--cache-warmup", type=int, default=320,
+                    help="untimed steps of the cache leg: the 709-slot cache fills in about 240 steps at 48 admits "
+                         "per 16-step replan")
     ap.add_argument("--no-cpu-tier", dest="cpu_tier", action="store_false",
                     help="cache leg: every decode miss read over PCIe by the GPU (default: the host tier serves the "
                          "share of the misses the split's cost model gives it, as the reference serves this "
