@@ -484,8 +484,10 @@ struct Tier
     const uint16_t* hx = nullptr;
     const int32_t* picks = nullptr;
     float* hout = nullptr;
-    int mode = -1, H = 0, I = 0;
-    float limit = 0.0f;
+    int H = 0, I = 0;
+    // set at any time (mm_tier_set_mode / mm_tier_set_limit), read by the worker at each job
+    std::atomic<int> mode{ -1 };
+    std::atomic<float> limit{ 0.0f };
     std::thread th;
     std::atomic<bool> quit{ false }, running{ false };
     std::atomic<int64_t> jobs{ 0 }, experts{ 0 }, tokens{ 0 }, empty{ 0 }, busy_ns{ 0 };
@@ -515,7 +517,7 @@ static void run_job(Tier& Tr, int li, int bsz, int np)
         memcpy(&Tr.pw[p], &Tr.picks[3 * p + 2], 4);
     }
     run_picks(Tr.pool, Tr.layers[li], H, Tr.I, Tr.xf.data(), bsz, Tr.pt.data(), Tr.pe.data(), Tr.pw.data(), np,
-              eff_mode(Tr.mode), Tr.limit, Tr.hout, Tr.job);
+              eff_mode(Tr.mode.load()), Tr.limit.load(), Tr.hout, Tr.job);
     if (np == 0) Tr.empty++;
     Tr.experts += np;
     Tr.tokens += bsz;
@@ -565,7 +567,7 @@ int impl_init(int threads, const int* cpus, int ncpus, int64_t* ctrl, const void
     T->hx = static_cast<const uint16_t*>(hx);
     T->picks = picks;
     T->hout = hout;
-    T->mode = mode;
+    T->mode.store(mode);
     T->H = H;
     T->I = I;
     T->layers.resize(nlayers);
@@ -600,14 +602,14 @@ int impl_add_layer(int li, int E, const int64_t* ptrs, const void* suh_g, const 
 int impl_set_limit(float limit)
 {
     if (!g_tier) return set_error(MM_ERR_ARG, "mm_tier_set_limit: mm_tier_init first");
-    g_tier->limit = limit;
+    g_tier->limit.store(limit);
     return MM_OK;
 }
 
 int impl_set_mode(int mode)
 {
     if (!g_tier) return set_error(MM_ERR_ARG, "mm_tier_set_mode: mm_tier_init first");
-    g_tier->mode = mode;
+    g_tier->mode.store(mode);
     return MM_OK;
 }
 
@@ -667,7 +669,7 @@ int impl_forward(int li, const float* x, int m, const int32_t* sel, const float*
             pw.push_back(w[(size_t)t * k + j]);
         }
     run_picks(T->pool, T->layers[li], T->H, T->I, x, m, pt.data(), pe.data(), pw.data(), (int)pt.size(),
-              eff_mode(mode >= 0 ? mode : T->mode), T->limit, out, T->job);
+              eff_mode(mode >= 0 ? mode : T->mode.load()), T->limit.load(), out, T->job);
     return MM_OK;
 }
 
