@@ -189,3 +189,31 @@ def test_router_matches_oracle(dev, T):
             assert np.min(np.abs(np.diff(srt[: k + 1]))) < 1e-5, t
         else:
             assert np.allclose(w.cpu().numpy()[t], rw[t], rtol=1e-5, atol=1e-6)
+
+
+def test_router_ties_pick_the_lower_expert(dev):
+    """Exact ties in the router: gate rows duplicated in pairs give bit-identical logit pairs, and with an odd k the
+    last slot splits a pair, which must go to the lower expert id; an all-zero gate ties every expert, so the
+    picks are experts 0 .. k - 1 with equal weights."""
+    import torch
+    from mi355moe import _lib, workload
+    H, E, k, T = 1024, 64, 5, 3
+    x = workload.activations(T, H, seed=11)
+    xb = _t((x.view(np.uint32) >> 16).astype(np.uint16), dev)
+    base = np.random.default_rng(6).normal(0, 0.02, (E // 2, H)).astype(np.float32)
+    for G in (np.repeat(base, 2, axis=0), np.zeros((E, H), np.float32)):
+        Gd = _t(G, dev)
+        ids = torch.empty((T, k), dtype=torch.int64, device=dev)
+        w = torch.empty((T, k), dtype=torch.float32, device=dev)
+        logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+        print("router ties", flush=True)
+        _lib.call("mm_router_topk", xb.data_ptr(), T, H, Gd.data_ptr(), E, k, logits.data_ptr(), ids.data_ptr(),
+                  w.data_ptr(), _lib.stream_ptr())
+        torch.cuda.synchronize()
+        lg, gi, gw = logits.cpu().numpy(), ids.cpu().numpy(), w.cpu().numpy()
+        assert np.array_equal(lg[:, 0::2], lg[:, 1::2])              # the duplicated rows give equal logits
+        for t in range(T):
+            want = sorted(range(E), key=lambda e: (-float(lg[t, e]), e))[:k]
+            assert list(gi[t]) == want, (t, list(gi[t]), want)
+            z = np.exp(lg[t, want].astype(np.float64) - lg[t, want].max())
+            assert np.allclose(gw[t], z / z.sum(), rtol=1e-5, atol=1e-6)
