@@ -105,6 +105,8 @@ struct PrepArgs
     int32_t* pos_of;          // [n] sorted position of each route, -1 if its id is outside [0, E)
     int32_t* route_at;        // [n] route at each sorted position
     int32_t* e_at;            // [n] expert at each sorted position
+    int32_t* ai_at;           // [n] active index (record) of the expert at each sorted position
+    int32_t* ai_of;           // [n] active index of each route's expert
     uint16_t* xa;             // [n][2][H] fp16 in operand order
     float* xsum;              // [n][2][nb] sums of xa over each workgroup's rows
     int n, topk, E, H, nb, x_dtype, rescale;

@@ -9,7 +9,7 @@
 //                      conversion and the optional unit-RMS rescale happen here too).
 //   2. k_partial<0>    gate/up partial sums, one launch that fills the GPU once: the work -- every
 //                      (active expert, matrix, 128 output columns) segment of 256 tile rows -- is cut into
-//                      equal row ranges, one per wave, from the active-expert count on the device. A wave
+//                      equal runs of rows, one per wave, from the active-expert count on the device. A wave
 //                      streams its rows (8 tiles = 768 contiguous bytes each) from HBM into a 4-deep
 //                      wave-private LDS ring with buffer-to-LDS loads, decodes each tile in registers and
 //                      multiplies two tile rows at a time on v_mfma_f32_16x16x32_f16 against the inputs of up
@@ -41,12 +41,43 @@ constexpr int WAVES_PER_CU = 24;      // partial kernels: 6 workgroups of 4 wave
 constexpr int PREP_ROWS = 512;        // input rows per route-prep workgroup
 constexpr int MAX_TOPK = 16;
 
-// Row ranges per segment of a partial launch: as many equal pieces as fit one wave each (at least 1, at most
-// cap). Kernels 2-5 derive it from the same inputs, so they agree on the layout of the partial sums.
-__device__ __forceinline__ int pieces_per_segment(int nwaves, int nseg, int cap)
+// Rows of a partial launch: nseg segments of KT tile rows each (KT a multiple of 8), in segment order, cut into
+// nw runs of equal length (within 4 rows) that start and end on multiples of 4 rows, one per wave, so every wave
+// streams as many rows as every other. A run that reaches the end of a segment goes on in the next one; the wave
+// then computes one piece of each, and a segment's pieces are the runs that meet it, numbered from 0 in row
+// order. nw is the launch's wave count, lowered where runs that short would cut a segment into more than cap
+// pieces (the partial sums hold cap per segment): nw runs over Q quads of rows start in any K consecutive quads
+// at most ceil(K nw / Q) times, so with nw <= (cap - 1) Q / K a segment of K quads meets at most cap runs.
+// Kernels 2-5 derive the split from the same inputs, so they agree on the layout of the partial sums.
+struct RowSplit
 {
-    const int p = nseg > 0 ? nwaves / nseg : 1;
-    return p < 1 ? 1 : (p > cap ? cap : p);
+    int64_t quads;
+    int nw;
+};
+__device__ __forceinline__ RowSplit row_split(int nwaves, int nseg, int KT, int cap)
+{
+    const int64_t quads = (int64_t)nseg * (KT / 4);
+    const int64_t most = (int64_t)(cap - 1) * nseg;      // (cap - 1) quads / (KT / 4)
+    int64_t nw = nwaves;
+    nw = nw < quads ? nw : quads;
+    nw = nw < most ? nw : most;
+    return { quads, (int)nw };
+}
+// floor(x / d) for 0 <= x < 2^53 and 0 < d < 2^31, in fp64: both operands convert exactly and the division
+// rounds correctly, and a quotient below an integer k falls short of it by at least 1 / d, far more than half an
+// ulp of k, so the rounded quotient never reaches k (a few fp64 instructions where an int64 division takes about
+// a hundred)
+__device__ __forceinline__ int floor_div(int64_t x, int64_t d) { return (int)floor((double)x / (double)d); }
+// first quad of wave w's run (w <= nw)
+__device__ __forceinline__ int run_start(const RowSplit& s, int w) { return floor_div((int64_t)w * s.quads, s.nw); }
+// the wave whose run holds quad q
+__device__ __forceinline__ int run_of(const RowSplit& s, int64_t q) { return floor_div((q + 1) * s.nw - 1, s.quads); }
+// (a wave-uniform count: computed on the vector unit, returned as a scalar so the branches on it stay scalar)
+__device__ __forceinline__ int seg_pieces(const RowSplit& s, int seg, int KT)
+{
+    if (s.nw <= 0) return 1;      // no rows: the one piece a caller may read is left out by it
+    return __builtin_amdgcn_readfirstlane(run_of(s, (int64_t)(seg + 1) * (KT / 4) - 1) -
+                                          run_of(s, (int64_t)seg * (KT / 4)) + 1);
 }
 
 // ------------------------------------------------------------------------------------------ 1. route prep
@@ -69,6 +100,7 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
     __shared__ uint32_t s_bm[32];
     __shared__ int s_cnt[4][4];
     __shared__ float s_ss[4];
+    __shared__ int s_ai;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int blk = blockIdx.x % a.nb, m = (blockIdx.x / a.nb) & 1, idx = blockIdx.x / (2 * a.nb);
     const bool writer = m == 0 && blk == 0;      // the one workgroup of a route that writes its routing data
@@ -86,6 +118,15 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
     int64_t rid[GV_ROUTE_MAX / 256];
 #pragma unroll
     for (int k = 0; k < GV_ROUTE_MAX / 256; ++k) rid[k] = a.ids[min(tid + 256 * k, a.n - 1)];
+    // with a permutation: the active experts (ascending, at most E <= 4 x 256), searched for the route's expert
+    int32_t act[4] = { -1, -1, -1, -1 };
+    int nact_perm = 0;
+    if (perm && writer)
+    {
+        nact_perm = a.nactive_in[0];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) act[k] = a.active[min(tid + 256 * k, a.E - 1)];
+    }
     if (a.rescale)
         // the row's sum of squares, h = tid, tid + 256, ... in order; eight loads in flight before they are used
         for (int hb = tid; hb < a.H; hb += 256 * 8)
@@ -113,7 +154,11 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
         wt2 = a.wtab2[e];
     }
     if (tid < 32) s_bm[tid] = 0;
+    if (tid == 0) s_ai = -1;
     __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (tid + 256 * k < nact_perm && act[k] == e) s_ai = tid + 256 * k;     // one match at most
     // in-kernel routing: position = routes of lower experts + earlier routes of the same expert
     int less = 0, same = 0, rank = 0, nv = 0;
 #pragma unroll
@@ -150,42 +195,40 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
     // an expert with more than cap routes belongs to the fat-expert path: its positions stay reserved, but it gets
     // an empty record and its routes no transformed inputs and no outputs
     const bool fat = valid && (perm ? pcnt : same) > a.cap;
+    // in-kernel routing: the experts present below the route's expert (its record index) and in all, from the
+    // bitmap by one reduction over the first wave
+    int below = 0, present = 0;
+    if (!perm && wave == 0 && (writer || blockIdx.x == 0))
+    {
+        const uint32_t wd = lane < 32 ? s_bm[lane] : 0u;
+        const int eb = valid ? (e >> 5) : -1;
+        below = wave_sum_int(lane < eb ? __popc(wd) : (lane == eb ? __popc(wd & ((1u << (e & 31)) - 1u)) : 0));
+        present = wave_sum_int(__popc(wd));
+    }
     if (tid == 0 && (writer || blockIdx.x == 0))
     {
         if (blockIdx.x == 0)
         {
-            int nact = 0;
-            if (!perm)
-                for (int wd = 0; wd < 32; ++wd) nact += __popc(s_bm[wd]);
-            a.counts[0] = perm ? a.nactive_in[0] : nact;
+            a.counts[0] = perm ? a.nactive_in[0] : present;
             a.counts[1] = perm ? nvalid_perm : nv;
         }
         if (writer)
         {
+            // the expert's active index: experts present below it (in-kernel routing), or its place in the
+            // permutation's active list (-1 if absent there)
+            const int ai = !valid ? -1 : (perm ? s_ai : below);
             a.pos_of[s] = valid && !fat ? pos : -1;
+            a.ai_of[s] = valid && !fat ? ai : -1;
             if (valid)
             {
                 a.route_at[pos] = s;
                 a.e_at[pos] = fat ? -1 : e;
+                a.ai_at[pos] = fat ? -1 : ai;
                 // the expert's first route writes its record
-                int ai = -1, cnt = 0;
-                if (!perm && rank == 0)
+                const bool first_route = perm ? pos == a.offsets[e] : rank == 0;
+                if (first_route && ai >= 0)
                 {
-                    ai = 0;
-                    for (int wd = 0; wd < (e >> 5); ++wd) ai += __popc(s_bm[wd]);
-                    ai += __popc(s_bm[e >> 5] & ((1u << (e & 31)) - 1u));
-                    cnt = same;
-                }
-                else if (perm && pos == a.offsets[e])
-                {
-                    const int na = a.nactive_in[0];
-                    ai = 0;
-                    while (ai < na && a.active[ai] != e) ++ai;
-                    if (ai == na) ai = -1;
-                    cnt = a.offsets[e + 1] - pos;
-                }
-                if (ai >= 0)
-                {
+                    const int cnt = perm ? a.offsets[e + 1] - pos : same;
                     ExpertRec r{ e, fat ? 0 : cnt, pos, 0, { wt0, wt1, wt2 }, 0 };
                     a.rec[ai] = r;
                 }
@@ -233,6 +276,14 @@ struct PartArgs
     int npos, K, N, ncb, cap; // npos: sorted positions the workspace holds
 };
 
+// One pass of a partial-sum wave (k_partial): r0 of the run's rows [tr0, tr0 + nrow) of segment seg.
+struct Pass
+{
+    __amdgpu_buffer_rsrc_t wres;     // the pass's matrix
+    uint32_t wcol;                   // byte offset of the segment's 768-byte column chunk in a tile row
+    int seg, piece, tr0, nrow, r0, nr, first, cnt, m, cb;
+};
+
 template <int MODE, bool EXACT>
 __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
 {
@@ -248,9 +299,10 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
     const int nb = gridDim.x;
     const int b = (nb & 7) == 0 ? (int)(blockIdx.x & 7) * (nb >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
     const int nwaves = nb * GV_WAVES;
-    const int nseg = a.counts[0] * NMAT * a.ncb;
-    const int pps = pieces_per_segment(nwaves, nseg, a.cap);
     const int KT = a.K / 16, NT = a.N / 16;
+    const RowSplit split = row_split(nwaves, a.counts[0] * NMAT * a.ncb, KT, a.cap);
+    const int w = b * GV_WAVES + wave;
+    if (w >= split.nw) return;
     const uint32_t row_bytes = (uint32_t)NT * 96;
     const uint32_t wbytes = (uint32_t)KT * row_bytes;                   // one matrix
     const uint32_t xbytes = (uint32_t)((size_t)a.npos * NMAT * a.K * 2);   // the input array
@@ -264,134 +316,192 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
     const int llo = 4 * (blo / 3) + blo % 3, lhi = 4 * (bhi / 3) + bhi % 3;     // their places in a staged tile
     const uint32_t sh = 31u - (uint32_t)(eb & 31);
 
-    for (int p = b * GV_WAVES + wave; p < nseg * pps; p += nwaves)
-    {
-        const int seg = p / pps, piece = p % pps;
-        const int cb = seg % a.ncb, r = seg / a.ncb;
-        const int m = r % NMAT, ai = r / NMAT;
-        const int tr0 = piece * KT / pps, nrow = (piece + 1) * KT / pps - tr0;
-        // fields read through the pointer: a local copy indexed by the runtime matrix would live in scratch
-        const ExpertRec* rc = a.rec + ai;
-        const int cnt = rc->cnt, first = rc->first;
+    // The run's passes, in row order: for each segment the run meets, one pass per 16 routes of the segment's
+    // expert over the run's rows of that segment (its piece). The ring's loads run GV_RING rows ahead of the
+    // multiplies and, past the end of a pass, fetch the next pass's first rows: pieces start and end on multiples
+    // of 4 rows, so row i of the next pass lands in ring slot i % GV_RING as its own first loads would put it,
+    // and a wave streams its whole run without a pause between passes.
+    // this lane's input row of pass P (route position, matrix) and k-group: routes past nr repeat a valid one
+    // and their outputs are never stored
+    // (from an opaque copy of the lane index, so none of it is computed ahead and held across the loop)
+    auto xoff_of = [&](const Pass& P) {
+        int l = lane;
+        asm volatile("" : "+v"(l));
+        const int pos = P.first + P.r0 + max(0, min(l & 15, P.nr - 1));
+        return (uint32_t)(((size_t)pos * NMAT + P.m) * a.K * 2) + (uint32_t)(l >> 4) * 16;
+    };
+    const int end = 4 * (int)run_start(split, w + 1);
+    // the run's first segment and this wave's piece of it; every later segment the run meets starts inside the
+    // run, so the wave computes its piece 0
+    const int seg0 = 4 * run_start(split, w) / KT, piece0 = w - run_of(split, (int64_t)seg0 * (KT / 4));
+    // pass r0 of the run's rows [tr0, tr0 + nrow) of segment seg; nr = 0 if its expert has no routes past r0
+    auto load_pass = [&](int seg, int tr0, int nrow, int r0) {
+        Pass P;
+        P.seg = seg;
+        P.tr0 = tr0;
+        P.nrow = nrow;
+        P.r0 = r0;
+        P.piece = seg == seg0 ? piece0 : 0;
+        P.cb = seg % a.ncb;
+        const int r = seg / a.ncb;
+        P.m = r % NMAT;
+        const int ai = r / NMAT;
+        // fields read through the pointer (a local copy indexed by the runtime matrix would live in scratch), in
+        // the constant address space: the records do not change during the launch, so the reads are scalar loads,
+        // which the ring's vector-load waits do not count
+        typedef __attribute__((address_space(4))) const ExpertRec ConstRec;
+        ConstRec* rc = (ConstRec*)(a.rec + ai);
+        P.cnt = rc->cnt;
+        P.first = rc->first;
         // per-matrix buffer descriptor in SGPRs. readfirstlane returns int: each half goes through uint32_t
         // before widening, or a low word >= 2^31 would sign-extend into the high word.
-        const uint64_t wp = (uint64_t)rc->w[MODE == 0 ? m : 2];
+        const uint64_t wp = (uint64_t)rc->w[MODE == 0 ? P.m : 2];
         const uint32_t wlo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)wp);
         const uint32_t whi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(wp >> 32));
-        const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(
-            reinterpret_cast<void*>((uintptr_t)((uint64_t)wlo | ((uint64_t)whi << 32))), (short)0, (int)wbytes,
-            0x00020000);
-        const uint32_t wcol = (uint32_t)cb * ROW_BYTES;
-
-        for (int r0 = 0; r0 < cnt; r0 += 16)
+        P.wres = __builtin_amdgcn_make_buffer_rsrc(reinterpret_cast<void*>((uintptr_t)((uint64_t)wlo | ((uint64_t)whi << 32))),
+                                                   (short)0, (int)wbytes, 0x00020000);
+        P.wcol = (uint32_t)P.cb * ROW_BYTES;
+        P.nr = max(0, min(16, P.cnt - r0));
+        return P;
+    };
+    // the pass after P in this run, skipping segments of experts without routes; none: nr = nrow = 0 (its loads
+    // are then the empty ones, on P's matrix)
+    auto next_pass = [&](const Pass& P) {
+        if (P.r0 + 16 < P.cnt) return load_pass(P.seg, P.tr0, P.nrow, P.r0 + 16);
+        Pass Q = P;
+        Q.nr = 0;
+        for (int seg = P.seg + 1, row = seg * KT; row < end; ++seg, row += KT)
         {
-            const int nr = min(16, cnt - r0);
-            // this lane's A row: routes past nr repeat a valid one and their outputs are never stored
-            const int pos = first + r0 + min(col, nr - 1);
-            const uint32_t xoff = (uint32_t)(((size_t)pos * NMAT + m) * a.K * 2) + (uint32_t)g * 16;
-            float4_t acc[8];
-#pragma unroll
-            for (int c = 0; c < 8; ++c) acc[c] = float4_t{ 0.f, 0.f, 0.f, 0.f };
-            uint2 areg[GV_RING];
-            // row t of the range: one 768-byte trellis load into ring slot j and the lane's 8 input bytes.
-            // Rows past the range are issued with offsets beyond the buffers, which the buffer unit answers with
-            // zeros and no memory access, so every row keeps the same two loads and the waits stay uniform.
-            auto issue = [&](int j, int t) {
-                const bool in = t < nrow;
-                const uint32_t tr = (uint32_t)(tr0 + t);
-                __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, &ring[(wave * GV_RING + j) * SLOT], 12,
-                                                         (uint32_t)lane * 12, in ? tr * row_bytes + wcol : wbytes, 0, 0);
-                // operand order: tile row tr's 4 inputs of k-group g at byte 64 (tr / 2) + 16 g + 8 (tr % 2)
-                const uint32_t xrow = (tr >> 1) * 64 + (tr & 1) * 8;
-                areg[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xres, xoff, in ? xrow : xbytes, 0));
-            };
-            // rows j and j + 1 (ring slots) through one MFMA per tile; a row past the range has zero inputs
-            auto pair_mma = [&](int j) {
-                const uint32_t* s0 = &ring[(wave * GV_RING + j) * SLOT];
-                const uint32_t* s1 = s0 + SLOT;
-                const half4_t a0 = __builtin_bit_cast(half4_t, areg[j]), a1 = __builtin_bit_cast(half4_t, areg[j + 1]);
-                const half8_t A = { a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3] };
-#pragma unroll
-                for (int c = 0; c < 8; ++c)
-                {
-                    const half4_t b0 = decode4<EXACT>(s0[c * 32 + lhi], s0[c * 32 + llo], sh);
-                    const half4_t b1 = decode4<EXACT>(s1[c * 32 + lhi], s1[c * 32 + llo], sh);
-                    const half8_t B = { b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3] };
-                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[c], 0, 0, 0);
-                }
-            };
-#pragma unroll
-            for (int j = 0; j < GV_RING; ++j) issue(j, j);
-            // rows t and t + 1 hold the oldest 4 of the 2 GV_RING loads in flight; their slots are refilled with
-            // rows t + GV_RING and t + GV_RING + 1 once the slots' LDS reads have returned
-            for (int t0 = 0; t0 < nrow; t0 += GV_RING)
-            {
-#pragma unroll
-                for (int j = 0; j < GV_RING; j += 2)
-                {
-                    if (t0 + j < nrow)
-                    {
-                        wait_vmcnt<2 * (GV_RING - 2)>();
-                        pair_mma(j);
-                        wait_lgkm0();
-                    }
-                    issue(j, t0 + j + GV_RING);
-                    issue(j + 1, t0 + j + 1 + GV_RING);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-            }
-            wait_vmcnt<0>();      // the trailing (empty) loads, so the ring is quiet when it is reused or left
+            Q = load_pass(seg, 0, min(KT, end - row), 0);
+            if (Q.nr > 0) break;
+        }
+        if (Q.nr == 0) Q.nrow = 0;
+        return Q;
+    };
+    // the current pass, carried from one pass to the next as four plain integers (its segment, first row, row
+    // count and first route) and rebuilt from them, so the loop carries nothing else
+    int cseg, ctr0, cnrow, cr0;
+    {
+        const int row = 4 * (int)run_start(split, w), seg = row / KT, tr0 = row - seg * KT;
+        Pass P = load_pass(seg, tr0, min(KT - tr0, end - row), 0);
+        if (P.nr == 0) P = next_pass(P);
+        if (P.nr == 0) return;
+        cseg = P.seg;
+        ctr0 = P.tr0;
+        cnrow = P.nrow;
+        cr0 = P.r0;
+    }
 
-            // D layout: lane (column col, group g) holds routes 4g .. 4g+3 of column col of each tile. The sums leave
-            // through the wave's ring, free now, so each route row goes out as one 512-byte run of 16-byte stores:
-            // per pass 8 rows (groups 2p and 2p + 1), row q at dword 128 q.
-            uint32_t* stage = &ring[wave * GV_RING * SLOT];
-            // lane indices recomputed here from an opaque copy, so nothing of this block is held across the loop
-            int sl = lane;
-            asm volatile("" : "+v"(sl));
-            const int sg = sl >> 4, scol = sl & 15;
-            for (int p8 = 0; p8 < nr; p8 += 8)
+    uint2 areg[GV_RING];
+    // row t of pass P: one 768-byte trellis load into ring slot j and the lane's 8 input bytes (xo = xoff_of(P)).
+    // Rows past the pass are issued with offsets beyond the buffers, which the buffer unit answers with zeros and
+    // no memory access, so every row keeps the same two loads and the waits stay uniform.
+    auto issue = [&](const Pass& P, uint32_t xo, int j, int t) {
+        const bool in = t < P.nrow;
+        const uint32_t tr = (uint32_t)(P.tr0 + t);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(P.wres, &ring[(wave * GV_RING + j) * SLOT], 12, (uint32_t)lane * 12,
+                                                 in ? tr * row_bytes + P.wcol : wbytes, 0, 0);
+        // operand order: tile row tr's 4 inputs of k-group g at byte 64 (tr / 2) + 16 g + 8 (tr % 2)
+        const uint32_t xrow = (tr >> 1) * 64 + (tr & 1) * 8;
+        areg[j] = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xres, xo, in ? xrow : xbytes, 0));
+    };
+    {
+        const Pass P = load_pass(cseg, ctr0, cnrow, cr0);
+        const uint32_t xo = xoff_of(P);
+#pragma unroll
+        for (int j = 0; j < GV_RING; ++j) issue(P, xo, j, j);
+    }
+    for (;;)
+    {
+        const Pass cur = load_pass(__builtin_amdgcn_readfirstlane(cseg), __builtin_amdgcn_readfirstlane(ctr0),
+                                   __builtin_amdgcn_readfirstlane(cnrow), __builtin_amdgcn_readfirstlane(cr0));
+        const uint32_t xoff = xoff_of(cur);
+        float4_t acc[8];
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+        // rows j and j + 1 (ring slots) through one MFMA per tile
+        auto pair_mma = [&](int j) {
+            const uint32_t* s0 = &ring[(wave * GV_RING + j) * SLOT];
+            const uint32_t* s1 = s0 + SLOT;
+            const half4_t a0 = __builtin_bit_cast(half4_t, areg[j]), a1 = __builtin_bit_cast(half4_t, areg[j + 1]);
+            const half8_t A = { a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3] };
+#pragma unroll
+            for (int c = 0; c < 8; ++c)
             {
-                if ((sg >> 1) == (p8 >> 3))
-                {
+                const half4_t b0 = decode4<EXACT>(s0[c * 32 + lhi], s0[c * 32 + llo], sh);
+                const half4_t b1 = decode4<EXACT>(s1[c * 32 + lhi], s1[c * 32 + llo], sh);
+                const half8_t B = { b0[0], b0[1], b0[2], b0[3], b1[0], b1[1], b1[2], b1[3] };
+                acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A, B, acc[c], 0, 0, 0);
+            }
+        };
+        // rows t and t + 1 hold the oldest 4 of the 2 GV_RING loads in flight; their slots are refilled with
+        // rows t + GV_RING and t + GV_RING + 1 once the slots' LDS reads have returned. Pass lengths are multiples
+        // of GV_RING, so the last GV_RING rows refill their slots with the next pass's first rows, each in the
+        // slot its own first loads would use.
+        for (int t0 = 0; t0 + GV_RING < cur.nrow; t0 += GV_RING)
+        {
 #pragma unroll
-                    for (int v = 0; v < 4; ++v)
-                    {
-                        const int q = 4 * (sg & 1) + v;
-                        if (p8 + q < nr)
-#pragma unroll
-                            for (int c = 0; c < 8; ++c)
-                                stage[128 * q + 16 * c + scol] = __float_as_uint(acc[c][v]);
-                    }
-                }
-#pragma unroll
-                for (int h = 0; h < 4; ++h)
-                {
-                    const int q = 2 * h + (sl >> 5), c4 = 4 * (sl & 31);
-                    if (p8 + q < nr)
-                    {
-                        const uint4 v4 = *reinterpret_cast<const uint4*>(&stage[128 * q + c4]);
-                        float* dst = a.part + ((size_t)(piece * a.npos + first + r0 + p8 + q) * NMAT + m) * a.N +
-                                     cb * GV_COLS + c4;
-                        *reinterpret_cast<uint4*>(dst) = v4;
-                    }
-                }
-                wait_lgkm0();     // the rows are read before the ring is written again
+            for (int j = 0; j < GV_RING; j += 2)
+            {
+                wait_vmcnt<2 * (GV_RING - 2)>();
+                pair_mma(j);
+                wait_lgkm0();
+                issue(cur, xoff, j, t0 + j + GV_RING);
+                issue(cur, xoff, j + 1, t0 + j + 1 + GV_RING);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
+        // the next pass, looked up here: its record's load is waited for with the first pair's LDS reads
+        const Pass nxt = next_pass(cur);
+        {
+            const uint32_t nxo = xoff_of(nxt);
+#pragma unroll
+            for (int j = 0; j < GV_RING; j += 2)
+            {
+                wait_vmcnt<2 * (GV_RING - 2)>();
+                pair_mma(j);
+                wait_lgkm0();
+                issue(nxt, nxo, j, j);
+                issue(nxt, nxo, j + 1, j + 1);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+
+        // D layout: lane (column col, group g) holds routes 4g .. 4g+3 of column col of each tile; each store
+        // writes 4 runs of 16 columns (64 bytes). The ring keeps streaming meanwhile. (Staging the rows through
+        // LDS for 16-byte stores of whole rows was measured slower.)
+        {
+            // lane indices from an opaque copy, so nothing of this block is held across the loop
+            int l = lane;
+            asm volatile("" : "+v"(l));
+            const int sg = l >> 4;
+            float* dst = a.part + ((size_t)(cur.piece * a.npos + cur.first + cur.r0 + 4 * sg) * NMAT + cur.m) * a.N +
+                         cur.cb * GV_COLS + (l & 15);
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (4 * sg + v < cur.nr)
+#pragma unroll
+                    for (int c = 0; c < 8; ++c) dst[(size_t)v * NMAT * a.N + 16 * c] = acc[c][v];
+        }
+        if (nxt.nr == 0) break;
+        cseg = nxt.seg;
+        ctr0 = nxt.tr0;
+        cnrow = nxt.nrow;
+        cr0 = nxt.r0;
     }
+    wait_vmcnt<0>();      // the trailing (empty) loads, so the ring is quiet when the wave leaves
 }
 
 // ------------------------------------------------------------------------------------ 3. gate/up epilogue
 
 // For each of NS streams i: a[i] += p[i][q * stride + lane], b[i] += p[i][q * stride + lane + 64] for
-// q = 0 .. np - 1 in ascending q. BATCH pieces of every stream are loaded before any is added (pieces past np
-// reload piece np - 1 and are not added), so a count up to BATCH costs one memory round trip.
+// q = 0 .. np[i] - 1 in ascending q. BATCH pieces of every stream are loaded before any is added (pieces past
+// np[i] reload piece np[i] - 1 and are not added), so counts up to BATCH cost one memory round trip.
 template <int NS, int BATCH>
-__device__ __forceinline__ void sum_pieces_batched(const float* const (&p)[NS], size_t stride, int np, int lane,
-                                                   float (&a)[NS], float (&b)[NS])
+__device__ __forceinline__ void sum_pieces_batched(const float* const (&p)[NS], size_t stride, const int (&np)[NS],
+                                                   int most, int lane, float (&a)[NS], float (&b)[NS])
 {
-    for (int q0 = 0; q0 < np; q0 += BATCH)
+    for (int q0 = 0; q0 < most; q0 += BATCH)
     {
         float va[NS][BATCH], vb[NS][BATCH];
 #pragma unroll
@@ -399,15 +509,15 @@ __device__ __forceinline__ void sum_pieces_batched(const float* const (&p)[NS], 
 #pragma unroll
             for (int i = 0; i < NS; ++i)
             {
-                const float* pk = p[i] + (size_t)min(q0 + k, np - 1) * stride;
+                const float* pk = p[i] + (size_t)min(q0 + k, np[i] - 1) * stride;
                 va[i][k] = pk[lane];
                 vb[i][k] = pk[lane + 64];
             }
 #pragma unroll
         for (int k = 0; k < BATCH; ++k)
-            if (q0 + k < np)
 #pragma unroll
-                for (int i = 0; i < NS; ++i)
+            for (int i = 0; i < NS; ++i)
+                if (q0 + k < np[i])
                 {
                     a[i] += va[i][k];
                     b[i] += vb[i][k];
@@ -415,16 +525,22 @@ __device__ __forceinline__ void sum_pieces_batched(const float* const (&p)[NS], 
     }
 }
 
-// Up to 8 pieces (4 or more active experts per call on the whole GPU) in one round trip of 8 loads per stream;
-// more (calls of 1-3 tokens, up to 24 pieces) in one round trip of 24.
+// Up to 8 pieces per stream (a call with at least 4 tokens at top-8 cuts segments into 8 or 9) in one round
+// trip of 8 loads per stream, up to 12 in one of 12, more (calls of 1-3 tokens, up to 32 pieces) in round trips
+// of 24.
 template <int NS>
-__device__ __forceinline__ void sum_pieces(const float* const (&p)[NS], size_t stride, int np, int lane, float (&a)[NS],
-                                           float (&b)[NS])
+__device__ __forceinline__ void sum_pieces(const float* const (&p)[NS], size_t stride, const int (&np)[NS], int lane,
+                                           float (&a)[NS], float (&b)[NS])
 {
-    if (np <= 8)
-        sum_pieces_batched<NS, 8>(p, stride, np, lane, a, b);
+    int most = np[0];
+#pragma unroll
+    for (int i = 1; i < NS; ++i) most = max(most, np[i]);
+    if (most <= 8)
+        sum_pieces_batched<NS, 8>(p, stride, np, most, lane, a, b);
+    else if (most <= 12)
+        sum_pieces_batched<NS, 12>(p, stride, np, most, lane, a, b);
     else
-        sum_pieces_batched<NS, 24>(p, stride, np, lane, a, b);
+        sum_pieces_batched<NS, 24>(p, stride, np, most, lane, a, b);
 }
 
 // Sum of p[0 .. count) by one wave, split so its first load shares a round trip with the loads after it:
@@ -448,11 +564,12 @@ struct GuEpiArgs
     const float* xsum;        // [n][2][nb]
     const int32_t* counts;
     const int32_t* e_at;
+    const int32_t* ai_at;
     const uint16_t* svh13;    // [E][2][I]
     const uint16_t* suh2;     // [E][I]
     uint16_t* xd;             // [n][I] fp16 in operand order
     float* xdsum;             // [n][I / 128] sums of xd over each 128-column block
-    int npos, I, nb, nwaves, cap, affine;
+    int npos, H, I, nb, nwaves, cap, affine;
     float limit;
 };
 
@@ -467,9 +584,15 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     // round trip 1: the counts and the position's expert (read before the range check: only the last
     // workgroup's spare waves are past n, and they read position n - 1)
     const int nvalid = a.counts[1], nact = a.counts[0];
-    const int e = a.e_at[min(pos, a.npos - 1)];
-    if (pos >= nvalid || e < 0) return;      // past the routes, or a route of an expert above the cap
-    const int pps = pieces_per_segment(a.nwaves, nact * 2 * ncb, a.cap);
+    // (the wave's position is one, so e and ai are too: read as scalars, the piece counts and the branches on
+    // them below stay scalar)
+    const int e = __builtin_amdgcn_readfirstlane(a.e_at[min(pos, a.npos - 1)]);
+    const int ai = __builtin_amdgcn_readfirstlane(a.ai_at[min(pos, a.npos - 1)]);
+    asm volatile("" ::"s"(nact), "s"(e), "s"(ai));      // one round trip, not the count after the branch below
+    if (pos >= nvalid || e < 0 || ai < 0) return;      // past the routes, or a route of an expert above the cap
+    const int KT = a.H / 16;
+    const RowSplit split = row_split(a.nwaves, nact * 2 * ncb, KT, a.cap);
+    const int np[2] = { seg_pieces(split, (ai * 2 + 0) * ncb + cb, KT), seg_pieces(split, (ai * 2 + 1) * ncb + cb, KT) };
     const int c = cb * GV_COLS;
     // round trip 2: scales, input sums and partial sums
     const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c;
@@ -487,7 +610,7 @@ __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
     }
     const float* const pgu[2] = { a.part + ((size_t)pos * 2 + 0) * a.I + c, a.part + ((size_t)pos * 2 + 1) * a.I + c };
     float s0[2] = { 0.f, 0.f }, s1[2] = { 0.f, 0.f };
-    sum_pieces<2>(pgu, (size_t)a.npos * 2 * a.I, pps, lane, s0, s1);
+    sum_pieces<2>(pgu, (size_t)a.npos * 2 * a.I, np, lane, s0, s1);
     float ga = s0[0], gb = s1[0], ua = s0[1], ub = s1[1];
     if (a.affine)
     {
@@ -521,6 +644,8 @@ struct DEpiArgs
     const int32_t* pos_of;
     const int32_t* route_at;
     const int32_t* e_at;
+    const int32_t* ai_at;
+    const int32_t* ai_of;
     const int64_t* ids;
     const float* w;           // route weights (combine)
     const uint16_t* svh2;     // [E][H]
@@ -534,17 +659,19 @@ struct DEpiArgs
 // fixup), output transform.
 // nact = active experts (counts[0]), read by the caller with its other first loads; the scales, input sums and
 // partial sums then share one round trip.
-__device__ __forceinline__ void down_block(const DEpiArgs& a, int nact, int pos, int c, int64_t e, int lane, float& ya,
-                                           float& yb)
+__device__ __forceinline__ void down_block(const DEpiArgs& a, int nact, int ai, int pos, int c, int64_t e, int lane,
+                                           float& ya, float& yb)
 {
-    const int pps = pieces_per_segment(a.nwaves, nact * (a.H / GV_COLS), a.cap);
+    const int KT = a.I / 16, ncb = a.H / GV_COLS;
+    const RowSplit split = row_split(a.nwaves, nact * ncb, KT, a.cap);
+    const int np[1] = { seg_pieces(split, ai * ncb + c / GV_COLS, KT) };
     const uint16_t* sv = a.svh2 + (size_t)e * a.H + c;
     const float sva = h2f(sv[lane]), svb = h2f(sv[lane + 64]);
     const float* xs = a.xdsum + (size_t)pos * (a.I / GV_COLS);
     float sx = a.affine ? wave_sum_first(xs, a.I / GV_COLS, lane) : 0.f;
     const float* const pd[1] = { a.part + (size_t)pos * a.H + c };
     float s0[1] = { 0.f }, s1[1] = { 0.f };
-    sum_pieces<1>(pd, (size_t)a.npos * a.H, pps, lane, s0, s1);
+    sum_pieces<1>(pd, (size_t)a.npos * a.H, np, lane, s0, s1);
     ya = s0[0];
     yb = s1[0];
     if (a.affine)
@@ -566,11 +693,14 @@ __global__ __launch_bounds__(256) void k_down_y(DEpiArgs a)
     const int pos = item / ncb, cb = item % ncb;
     const int nvalid = a.counts[1], nact = a.counts[0];
     const int pc = min(pos, a.npos - 1);
-    const int s = a.route_at[pc], e = a.e_at[pc];
-    if (pos >= nvalid || e < 0) return;
+    // one position per wave: read as scalars
+    const int s = __builtin_amdgcn_readfirstlane(a.route_at[pc]), e = __builtin_amdgcn_readfirstlane(a.e_at[pc]);
+    const int ai = __builtin_amdgcn_readfirstlane(a.ai_at[pc]);
+    asm volatile("" ::"s"(nact), "s"(s), "s"(e), "s"(ai));      // one round trip, not the count after the branch
+    if (pos >= nvalid || e < 0 || ai < 0) return;
     const int c = cb * GV_COLS;
     float ya, yb;
-    down_block(a, nact, pos, c, e, lane, ya, yb);
+    down_block(a, nact, ai, pos, c, e, lane, ya, yb);
     a.Y[(size_t)s * a.H + c + lane] = ya;
     a.Y[(size_t)s * a.H + c + lane + 64] = yb;
 }
@@ -588,16 +718,17 @@ __global__ __launch_bounds__(1024) void k_down_combine(DEpiArgs a)
     const int t = blockIdx.x / ncb, c = (blockIdx.x % ncb) * GV_COLS;
     if (j < a.topk)
     {
-        // round trip 1: the route's position, expert and weight and the active-expert count. A pick outside
-        // [0, E) (position -1) is computed on position 0 and expert 0 and left out of the sum, so no branch keeps
-        // the expert's load from being issued with the others.
-        const int s = t * a.topk + j;
-        const int pos = a.pos_of[s];
+        // round trip 1: the route's position, expert, active index and weight and the active-expert count. A pick
+        // outside [0, E) (position -1) is computed on position 0 and expert 0 and left out of the sum, so no branch
+        // keeps the expert's load from being issued with the others.
+        const int s = t * a.topk + j;     // one route per wave: its fields are read as scalars
+        const int pos = __builtin_amdgcn_readfirstlane(a.pos_of[s]), ai = __builtin_amdgcn_readfirstlane(a.ai_of[s]);
         const int64_t e = a.ids[s];
         const float wt = a.w[s];
         const int nact = a.counts[0];
+        asm volatile("" ::"s"(nact), "s"(pos), "s"(ai), "v"(e), "v"(wt));     // all in one round trip
         float ya, yb;
-        down_block(a, nact, max(pos, 0), c, pos >= 0 ? e : 0, lane, ya, yb);
+        down_block(a, nact, pos >= 0 ? ai : 0, max(pos, 0), c, pos >= 0 ? e : 0, lane, ya, yb);
         ys[j][lane] = ya;
         ys[j][lane + 64] = yb;
         if (lane == 0)
@@ -632,6 +763,8 @@ struct Ws
     uint16_t* xd;
     float* xdsum;
     float* part_d;
+    int32_t* ai_at;
+    int32_t* ai_of;
     size_t bytes;
 };
 
@@ -661,14 +794,14 @@ static Ws carve(void* base, int n, int npos, int E, int H, int I)
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t m = (size_t)npos;
     const size_t na = (size_t)(npos < E ? npos : E), cap = (size_t)piece_cap(npos);
-    const size_t sizes[11] = { al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al(m * 4),
+    const size_t sizes[13] = { al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al(m * 4),
                                al(m * 4), al(m * 2 * H * 2), al(m * 2 * prep_blocks(H) * 4),
                                al(cap * m * 2 * I * 4), al(m * I * 2), al(m * (I / GV_COLS) * 4),
-                               al(cap * m * H * 4) };
+                               al(cap * m * H * 4), al(m * 4), al((size_t)n * 4) };
     char* p = static_cast<char*>(base);
-    char* at[11];
+    char* at[13];
     size_t off = 0;
-    for (int i = 0; i < 11; ++i)
+    for (int i = 0; i < 13; ++i)
     {
         at[i] = p ? p + off : nullptr;
         off += sizes[i];
@@ -676,7 +809,8 @@ static Ws carve(void* base, int n, int npos, int E, int H, int I)
     return { reinterpret_cast<ExpertRec*>(at[0]), reinterpret_cast<int32_t*>(at[1]), reinterpret_cast<int32_t*>(at[2]),
              reinterpret_cast<int32_t*>(at[3]), reinterpret_cast<int32_t*>(at[4]), reinterpret_cast<uint16_t*>(at[5]),
              reinterpret_cast<float*>(at[6]), reinterpret_cast<float*>(at[7]), reinterpret_cast<uint16_t*>(at[8]),
-             reinterpret_cast<float*>(at[9]), reinterpret_cast<float*>(at[10]), off };
+             reinterpret_cast<float*>(at[9]), reinterpret_cast<float*>(at[10]), reinterpret_cast<int32_t*>(at[11]),
+             reinterpret_cast<int32_t*>(at[12]), off };
 }
 
 // Waves of one partial launch: the whole GPU once (WAVES_PER_CU per CU), a multiple of 8 workgroups.
@@ -709,6 +843,8 @@ static int check_common(const mm_layer_t* L, const void* x, int x_dtype, int T, 
                  "%s: x_dtype must be MM_DTYPE_F16, MM_DTYPE_BF16 or MM_DTYPE_F32", who);
     MM_CHECK_ARG(T > 0 && n > 0 && topk > 0 && n <= T * topk, "%s: bad T/n/topk", who);
     MM_CHECK_ARG((size_t)n * 2 * (L->H > L->I ? L->H : L->I) * 2 < ((size_t)1 << 31), "%s: too many routes", who);
+    // tile rows of a partial launch (active experts x 2 matrices x column blocks x tile rows) count in int
+    MM_CHECK_ARG((size_t)(n < L->E ? n : L->E) * L->H / 1024 * L->I < ((size_t)1 << 31), "%s: too many routes", who);
     MM_CHECK_ARG(max_rows > 0, "%s: max_rows must be at least 1", who);
     const bool perm = offsets != nullptr;
     MM_CHECK_ARG(perm ? (order && active && nactive) : n <= GV_ROUTE_MAX,
@@ -731,8 +867,8 @@ static void launch_prep(const mm_layer_t* L, const Ws& w, const void* x, int x_d
     // positions past npos are not visited: their routes' pos_of must read "no position"
     if (npos < n) hipLaunchKernelGGL(k_fill_pos, dim3((unsigned)min((n + 255) / 256, 1024)), dim3(256), 0, s, w.pos_of, n);
     PrepArgs p{ x, ids, offsets, order, active, nactive, L->gate_ptr, L->up_ptr, L->down_ptr, L->suh13,
-                w.rec, w.counts, w.pos_of, w.route_at, w.e_at, w.xa, w.xsum, n, topk, L->E, L->H, nb, x_dtype, rescale,
-                cap, npos };
+                w.rec, w.counts, w.pos_of, w.route_at, w.e_at, w.ai_at, w.ai_of, w.xa, w.xsum, n, topk, L->E, L->H, nb,
+                x_dtype, rescale, cap, npos };
     launch_route_prep(p, s);
 }
 
@@ -751,7 +887,7 @@ static void launch_partial(const mm_layer_t* L, const Ws& w, int npos, hipStream
 
 static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int npos, hipStream_t s)
 {
-    GuEpiArgs g{ w.part_gu, w.xsum, w.counts, w.e_at, L->svh13, L->suh2, w.xd, w.xdsum, npos, L->I,
+    GuEpiArgs g{ w.part_gu, w.xsum, w.counts, w.e_at, w.ai_at, L->svh13, L->suh2, w.xd, w.xdsum, npos, L->H, L->I,
                  prep_blocks(L->H), partial_waves(), piece_cap(npos), (L->flags & MM_LAYER_EXACT) ? 0 : 1, L->limit };
     hipLaunchKernelGGL(k_gu_epilogue, dim3((npos * (L->I / GV_COLS) + 3) / 4), dim3(256), 0, s, g);
 }
@@ -759,7 +895,7 @@ static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int npos, hipSt
 static DEpiArgs down_args(const mm_layer_t* L, const Ws& w, int npos, int topk, const int64_t* ids, const float* wt,
                           float* Y, float* out, int accumulate)
 {
-    return DEpiArgs{ w.part_d, w.xdsum, w.counts, w.pos_of, w.route_at, w.e_at, ids, wt, L->svh2, Y, out, npos, L->H,
+    return DEpiArgs{ w.part_d, w.xdsum, w.counts, w.pos_of, w.route_at, w.e_at, w.ai_at, w.ai_of, ids, wt, L->svh2, Y, out, npos, L->H,
                      L->I, topk, partial_waves(), piece_cap(npos), (L->flags & MM_LAYER_EXACT) ? 0 : 1, accumulate };
 }
 

@@ -246,7 +246,8 @@ def test_route_prep_transform_bitwise_vs_oracle(dev):
     al = lambda v: (v + 255) & ~255
     nb, cap = (H + 511) // 512, min(32, max(4, 8192 // n))
     sizes = [al(min(n, E) * 48), al(8), al(n * 4), al(n * 4), al(n * 4), al(n * 2 * H * 2), al(n * 2 * nb * 4),
-             al(cap * n * 2 * I * 4), al(n * I * 2), al(n * (I // 128) * 4), al(cap * n * H * 4)]
+             al(cap * n * 2 * I * 4), al(n * I * 2), al(n * (I // 128) * 4), al(cap * n * H * 4), al(n * 4),
+             al(n * 4)]
     assert sum(sizes) == wsb, "decode workspace layout changed"
     off = np.cumsum([0] + sizes)
     pos_of = w[off[2]:off[2] + n * 4].view(np.int32)
