@@ -794,10 +794,12 @@ static Ws carve(void* base, int n, int npos, int E, int H, int I)
     auto al = [](size_t x) { return (x + 255) & ~(size_t)255; };
     const size_t m = (size_t)npos;
     const size_t na = (size_t)(npos < E ? npos : E), cap = (size_t)piece_cap(npos);
+    // the small routing arrays first and together (records, counts, pos_of, route_at, e_at, ai_at, ai_of), so the
+    // epilogues' first loads fall in the same few pages
     const size_t sizes[13] = { al(na * sizeof(ExpertRec)), al(2 * 4), al((size_t)n * 4), al(m * 4),
-                               al(m * 4), al(m * 2 * H * 2), al(m * 2 * prep_blocks(H) * 4),
-                               al(cap * m * 2 * I * 4), al(m * I * 2), al(m * (I / GV_COLS) * 4),
-                               al(cap * m * H * 4), al(m * 4), al((size_t)n * 4) };
+                               al(m * 4), al(m * 4), al((size_t)n * 4), al(m * 2 * H * 2),
+                               al(m * 2 * prep_blocks(H) * 4), al(cap * m * 2 * I * 4), al(m * I * 2),
+                               al(m * (I / GV_COLS) * 4), al(cap * m * H * 4) };
     char* p = static_cast<char*>(base);
     char* at[13];
     size_t off = 0;
@@ -806,11 +808,22 @@ static Ws carve(void* base, int n, int npos, int E, int H, int I)
         at[i] = p ? p + off : nullptr;
         off += sizes[i];
     }
-    return { reinterpret_cast<ExpertRec*>(at[0]), reinterpret_cast<int32_t*>(at[1]), reinterpret_cast<int32_t*>(at[2]),
-             reinterpret_cast<int32_t*>(at[3]), reinterpret_cast<int32_t*>(at[4]), reinterpret_cast<uint16_t*>(at[5]),
-             reinterpret_cast<float*>(at[6]), reinterpret_cast<float*>(at[7]), reinterpret_cast<uint16_t*>(at[8]),
-             reinterpret_cast<float*>(at[9]), reinterpret_cast<float*>(at[10]), reinterpret_cast<int32_t*>(at[11]),
-             reinterpret_cast<int32_t*>(at[12]), off };
+    Ws w;
+    w.rec = reinterpret_cast<ExpertRec*>(at[0]);
+    w.counts = reinterpret_cast<int32_t*>(at[1]);
+    w.pos_of = reinterpret_cast<int32_t*>(at[2]);
+    w.route_at = reinterpret_cast<int32_t*>(at[3]);
+    w.e_at = reinterpret_cast<int32_t*>(at[4]);
+    w.ai_at = reinterpret_cast<int32_t*>(at[5]);
+    w.ai_of = reinterpret_cast<int32_t*>(at[6]);
+    w.xa = reinterpret_cast<uint16_t*>(at[7]);
+    w.xsum = reinterpret_cast<float*>(at[8]);
+    w.part_gu = reinterpret_cast<float*>(at[9]);
+    w.xd = reinterpret_cast<uint16_t*>(at[10]);
+    w.xdsum = reinterpret_cast<float*>(at[11]);
+    w.part_d = reinterpret_cast<float*>(at[12]);
+    w.bytes = off;
+    return w;
 }
 
 // Waves of one partial launch: the whole GPU once (WAVES_PER_CU per CU), a multiple of 8 workgroups.

@@ -242,16 +242,16 @@ def test_route_prep_transform_bitwise_vs_oracle(dev):
               None, None, n, None, ws.data_ptr(), wsb, 1, _lib.stream_ptr())
     torch.cuda.synchronize()
     w = ws.cpu().numpy()
-    # workspace layout of the decode path: expert records, counts, pos_of, route_at, e_at, transformed inputs, ...
+    # workspace layout of the decode path: expert records, counts, pos_of, route_at, e_at, ai_at, ai_of,
+    # transformed inputs, ...
     al = lambda v: (v + 255) & ~255
     nb, cap = (H + 511) // 512, min(32, max(4, 8192 // n))
-    sizes = [al(min(n, E) * 48), al(8), al(n * 4), al(n * 4), al(n * 4), al(n * 2 * H * 2), al(n * 2 * nb * 4),
-             al(cap * n * 2 * I * 4), al(n * I * 2), al(n * (I // 128) * 4), al(cap * n * H * 4), al(n * 4),
-             al(n * 4)]
+    sizes = [al(min(n, E) * 48), al(8), al(n * 4), al(n * 4), al(n * 4), al(n * 4), al(n * 4), al(n * 2 * H * 2),
+             al(n * 2 * nb * 4), al(cap * n * 2 * I * 4), al(n * I * 2), al(n * (I // 128) * 4), al(cap * n * H * 4)]
     assert sum(sizes) == wsb, "decode workspace layout changed"
     off = np.cumsum([0] + sizes)
     pos_of = w[off[2]:off[2] + n * 4].view(np.int32)
-    xa = w[off[5]:off[5] + n * 2 * H * 2].view(np.uint16).reshape(n, 2, H)
+    xa = w[off[7]:off[7] + n * 2 * H * 2].view(np.uint16).reshape(n, 2, H)
     oi = np.array([_operand_index(j) for j in range(H)])
     suh = st.w13_suh.cpu().numpy()
     bad = 0
