@@ -507,16 +507,23 @@ static void run_job(Tier& Tr, int li, int bsz, int np)
     const int H = Tr.H;
     Tr.xf.resize((size_t)(bsz > 0 ? bsz : 1) * H);
     for (size_t i = 0; i < (size_t)bsz * H; ++i) Tr.xf[i] = h2f(Tr.hx[i]);
+    // picks whose token or expert is out of range are left out (as mm_tier_forward leaves them out), so a
+    // malformed job cannot index past the layer's experts or the job's rows
+    const int E = Tr.layers[li].E;
     Tr.pt.resize(np);
     Tr.pe.resize(np);
     Tr.pw.resize(np);
+    int nk = 0;
     for (int p = 0; p < np; ++p)
     {
-        Tr.pt[p] = Tr.picks[3 * p];
-        Tr.pe[p] = Tr.picks[3 * p + 1];
-        memcpy(&Tr.pw[p], &Tr.picks[3 * p + 2], 4);
+        const int32_t t = Tr.picks[3 * p], e = Tr.picks[3 * p + 1];
+        if (t < 0 || t >= bsz || e < 0 || e >= E) continue;
+        Tr.pt[nk] = t;
+        Tr.pe[nk] = e;
+        memcpy(&Tr.pw[nk], &Tr.picks[3 * p + 2], 4);
+        ++nk;
     }
-    run_picks(Tr.pool, Tr.layers[li], H, Tr.I, Tr.xf.data(), bsz, Tr.pt.data(), Tr.pe.data(), Tr.pw.data(), np,
+    run_picks(Tr.pool, Tr.layers[li], H, Tr.I, Tr.xf.data(), bsz, Tr.pt.data(), Tr.pe.data(), Tr.pw.data(), nk,
               eff_mode(Tr.mode.load()), Tr.limit.load(), Tr.hout, Tr.job);
     if (np == 0) Tr.empty++;
     Tr.experts += np;

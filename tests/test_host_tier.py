@@ -127,14 +127,14 @@ def test_forward_matches_reference_tier_modes(tier):
 
 def test_mailbox_worker_serves_jobs(tier):
     """The worker thread serves jobs published in the split's mailbox layout and answers with the done word; the
-    partial equals the synchronous forward bit for bit; an empty job zeroes the partial; forward is refused while
-    the worker runs."""
+    partial equals the synchronous forward bit for bit; an empty job zeroes the partial; picks whose expert or
+    token is out of range are left out; forward is refused while the worker runs."""
     H, I, E, T, k = 512, 256, 8, 4, 3
     seed = 4711
     ptrs, sc, keep = _layer(seed, E, H, I)
     ctrl = np.zeros(16, np.int64)
     hx = np.zeros((T, H), np.float16)
-    picks = np.zeros((T * k, 3), np.int32)
+    picks = np.zeros((T * k + 3, 3), np.int32)
     hout = np.full((T, H), np.nan, np.float32)
     mb = {k_: a.ctypes.data for k_, a in (("ctrl", ctrl), ("hx", hx), ("picks", picks), ("hout", hout))}
     tier.init(H, I, 2, mailbox=mb, threads=3, cpus=sorted(os.sched_getaffinity(0))[:3], mode=0)
@@ -167,4 +167,11 @@ def test_mailbox_worker_serves_jobs(tier):
     assert np.count_nonzero(hout) == 0
     s = tier.stats()
     assert s["jobs"] == 2 and s["picks"] == len(flat) and s["empty"] == 1 and s["tokens"] == 2 * T
+    # a malformed job: an expert past E, a negative expert and a token past the job's rows among the valid picks
+    bad = [(0, E, 1.0), (1, -1, 1.0), (T, int(sel[0, 0]), 1.0)]
+    rows = flat[:5] + bad + flat[5:]
+    for p, (t, e, wt) in enumerate(rows):
+        picks[p] = (t, e, np.float32(wt).view(np.int32))
+    job(3, len(rows))
+    assert np.array_equal(hout, want)
     tier.stop()
