@@ -294,8 +294,8 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
     __shared__ __align__(16) uint32_t ring[GV_WAVES * GV_RING * SLOT];
 
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // consecutive pieces (the row ranges of one segment, then adjacent 768-byte column chunks: the same
-    // inputs) go to one XCD; workgroups are dealt to the 8 XCDs round-robin
+    // consecutive runs (the pieces of one segment, then adjacent 768-byte column chunks: the same inputs) go to
+    // one XCD; workgroups are dealt to the 8 XCDs round-robin
     const int nb = gridDim.x;
     const int b = (nb & 7) == 0 ? (int)(blockIdx.x & 7) * (nb >> 3) + (int)(blockIdx.x >> 3) : (int)blockIdx.x;
     const int nwaves = nb * GV_WAVES;
@@ -321,9 +321,10 @@ __global__ __launch_bounds__(GV_THREADS, 6) void k_partial(PartArgs a)
     // multiplies and, past the end of a pass, fetch the next pass's first rows: pieces start and end on multiples
     // of 4 rows, so row i of the next pass lands in ring slot i % GV_RING as its own first loads would put it,
     // and a wave streams its whole run without a pause between passes.
-    // this lane's input row of pass P (route position, matrix) and k-group: routes past nr repeat a valid one
-    // and their outputs are never stored
-    // (from an opaque copy of the lane index, so none of it is computed ahead and held across the loop)
+
+    // This lane's input row of pass P (route position, matrix) and k-group: routes past nr repeat a valid one
+    // and their outputs are never stored. Computed from an opaque copy of the lane index, so none of it is
+    // computed ahead and held across the loop.
     auto xoff_of = [&](const Pass& P) {
         int l = lane;
         asm volatile("" : "+v"(l));
