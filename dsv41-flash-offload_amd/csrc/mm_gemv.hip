@@ -14,10 +14,10 @@
 //                      wave-private LDS ring with buffer-to-LDS loads, decodes each tile in registers and
 //                      multiplies two tile rows at a time on v_mfma_f32_16x16x32_f16 against the inputs of up
 //                      to 16 routes (L2 reads, prefetched with the same depth).
-//   3. k_gu_epilogue   per (route, 128 columns of I): row ranges added in order, output transforms, SwiGLU, the
+//   3. k_gu_epilogue   per (route, 128 columns of I): the pieces added in order, output transforms, SwiGLU, the
 //                      down-input transform (MFMA operand order) and its sums.
 //   4. k_partial<1>    down partial sums, as 2.
-//   5. k_down_combine  per (token, 128 columns of H): row ranges, output transform, weighted sum of the token's
+//   5. k_down_combine  per (token, 128 columns of H): the pieces, output transform, weighted sum of the token's
 //                      routes in ascending order; or k_down_y: per-route rows.
 //
 // Codebook (kernels/cpu_avx2/ft_core.h:75-83): w = fp16(fma(1024 + bytesum, KINV, KBIAS)). By default the
@@ -574,7 +574,7 @@ struct GuEpiArgs
     float limit;
 };
 
-// One wave per (sorted position, 128-column block of I): row ranges added in order (then the AFFINE fixup),
+// One wave per (sorted position, 128-column block of I): pieces added in order (then the AFFINE fixup),
 // output transforms, SwiGLU, the down-input transform.
 __global__ __launch_bounds__(256) void k_gu_epilogue(GuEpiArgs a)
 {
@@ -656,7 +656,7 @@ struct DEpiArgs
     int accumulate;           // combine: out += the sum instead of out = the sum
 };
 
-// Down output of one (sorted position, 128-column block of H): row ranges added in order (then the AFFINE
+// Down output of one (sorted position, 128-column block of H): pieces added in order (then the AFFINE
 // fixup), output transform.
 // nact = active experts (counts[0]), read by the caller with its other first loads; the scales, input sums and
 // partial sums then share one round trip.
@@ -782,7 +782,7 @@ void launch_route_prep(const PrepArgs& p, hipStream_t s)
         hipLaunchKernelGGL(k_route_prep<MM_DTYPE_F32>, grid, block, 0, s, p);
 }
 
-// Most row ranges per segment a partial launch may use: bounded so the partial sums stay a few MB.
+// Most pieces per segment a partial launch may use: bounded so the partial sums stay a few MB.
 static int piece_cap(int n)
 {
     const int c = n > 0 ? 8192 / n : 32;
