@@ -243,10 +243,23 @@ static inline float act_gu(float g, float u, float limit)
 
 // ------------------------------------------------------------------------------------------------ GEMV
 
-// y[t][0..127] (raw sums, before the output transform) of column block cb of matrix m for MT tokens whose
-// transformed inputs are xt[t][0..K) and sums xs[t]. EXACT: fp16-rounded weights; else the centred AFFINE codes.
+// The rows of a group of tokens: token t's transformed input is xt + t * xstride (K values), its input sum
+// xs[t * sstride], its output row y + t * ystride (128 values of the column block).
+struct Rows
+{
+    const float* xt;
+    size_t xstride;
+    const float* xs;
+    size_t sstride;
+    float* y;
+    size_t ystride;
+    Rows at(int t) const { return { xt + t * xstride, xstride, xs + t * sstride, sstride, y + t * ystride, ystride }; }
+};
+
+// y[t][0..127] (raw sums, before the output transform) of column block cb of matrix m for MT tokens. EXACT:
+// fp16-rounded weights; else the centred AFFINE codes.
 template <int MT, bool EXACT>
-static void gemv_block(const Mat& m, int cb, const float* const* xt, const float* xs, float* const* y)
+static void gemv_block(const Mat& m, int cb, const Rows& R)
 {
     const int NT = m.N / 16, KT = m.K / 16;
     const __m512i vmask = _mm512_set1_epi32(0xffff), vmul = _mm512_set1_epi32((int)MUL1);
@@ -283,7 +296,7 @@ static void gemv_block(const Mat& m, int cb, const float* const* xt, const float
                     w = _mm512_cvtph_ps(_mm512_cvtps_ph(_mm512_fmadd_ps(w, vkinv, vkbias),
                                                         _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
                 const int k = tk * 16 + r;
-                for (int t = 0; t < MT; ++t) acc[t][j] = _mm512_fmadd_ps(_mm512_set1_ps(xt[t][k]), w, acc[t][j]);
+                for (int t = 0; t < MT; ++t) acc[t][j] = _mm512_fmadd_ps(_mm512_set1_ps(R.xt[t * R.xstride + k]), w, acc[t][j]);
             }
         }
     }
@@ -291,31 +304,33 @@ static void gemv_block(const Mat& m, int cb, const float* const* xt, const float
     {
         if constexpr (EXACT)
         {
-            for (int j = 0; j < 8; ++j) _mm512_storeu_ps(y[t] + 16 * j, acc[t][j]);
+            for (int j = 0; j < 8; ++j) _mm512_storeu_ps(R.y + t * R.ystride + 16 * j, acc[t][j]);
         }
         else
         {
-            const __m512 off = _mm512_set1_ps((float)((double)kbias() + CENTER * (double)kinv()) * xs[t]);
-            for (int j = 0; j < 8; ++j) _mm512_storeu_ps(y[t] + 16 * j, _mm512_fmadd_ps(vkinv, acc[t][j], off));
+            const __m512 off = _mm512_set1_ps((float)((double)kbias() + CENTER * (double)kinv()) * R.xs[t * R.sstride]);
+            for (int j = 0; j < 8; ++j) _mm512_storeu_ps(R.y + t * R.ystride + 16 * j, _mm512_fmadd_ps(vkinv, acc[t][j], off));
         }
     }
 }
 
 template <bool EXACT>
-static void gemv_tokens(const Mat& m, int cb, int nt, const float* const* xt, const float* xs, float* const* y)
+static void gemv_tokens(const Mat& m, int cb, int nt, const Rows& R)
 {
     for (int t0 = 0; t0 < nt; t0 += MAX_MT)
     {
         const int mt = nt - t0 < MAX_MT ? nt - t0 : MAX_MT;
-        if (mt == 3) gemv_block<3, EXACT>(m, cb, xt + t0, xs + t0, y + t0);
-        else if (mt == 2) gemv_block<2, EXACT>(m, cb, xt + t0, xs + t0, y + t0);
-        else gemv_block<1, EXACT>(m, cb, xt + t0, xs + t0, y + t0);
+        if (mt == 3) gemv_block<3, EXACT>(m, cb, R.at(t0));
+        else if (mt == 2) gemv_block<2, EXACT>(m, cb, R.at(t0));
+        else gemv_block<1, EXACT>(m, cb, R.at(t0));
     }
 }
 
 // ------------------------------------------------------------------------------------------------ a job
 
 // The picks of one call grouped by expert: expert g's tokens are tok[first[g] .. first[g + 1]) (pick order).
+// Every buffer lives here and keeps its capacity from job to job, so serving a job allocates only when it is
+// larger than every job before it.
 struct Job
 {
     const Layer* L = nullptr;
@@ -326,16 +341,21 @@ struct Job
     std::vector<float> wt;                  // weight of each group entry
     std::vector<int> pick_of;               // group entry of pick p (the combine's order)
     std::vector<int> tok_pick_start, tok_picks;   // picks of token t in pick order
+    std::vector<int> cnt, slot, fill, tfill;      // grouping scratch
     // per group entry (expert e, token t): transformed inputs and intermediate rows
     std::vector<float> xt, xs, gu, xd, xds, yd;
     float* out = nullptr;                   // [T][H]
 };
 
+static int group_of(const Job& J, int u)
+{
+    return (int)(std::upper_bound(J.first.begin(), J.first.end(), u) - J.first.begin()) - 1;
+}
+
 static void ph_input(void* c, int u)          // u = group entry
 {
     Job& J = *static_cast<Job*>(c);
-    const int g = (int)(std::upper_bound(J.first.begin(), J.first.end(), u) - J.first.begin()) - 1;
-    const Expert& E = J.L->ex[J.gexp[g]];
+    const Expert& E = J.L->ex[J.gexp[group_of(J, u)]];
     const float* x = J.x + (size_t)J.tok[u] * J.H;
     float* xt = J.xt.data() + (size_t)u * 2 * J.H;
     J.xs[2 * u + 0] = prep_input(x, E.g.suh, J.H, xt);
@@ -350,30 +370,22 @@ static void ph_gateup(void* c, int u)         // u = (group, matrix, column bloc
     const Expert& E = J.L->ex[J.gexp[g]];
     const Mat& M = mm == 0 ? E.g : E.u;
     const int f = J.first[g], nt = J.first[g + 1] - f;
-    std::vector<const float*> xt(nt);
-    std::vector<float*> y(nt);
-    std::vector<float> xs(nt);
-    for (int t = 0; t < nt; ++t)
-    {
-        xt[t] = J.xt.data() + (size_t)(f + t) * 2 * J.H + (size_t)mm * J.H;
-        xs[t] = J.xs[2 * (f + t) + mm];
-        y[t] = J.gu.data() + (size_t)(f + t) * 2 * J.I + (size_t)mm * J.I + cb * 128;
-    }
-    if (J.mode == 1) gemv_tokens<true>(M, cb, nt, xt.data(), xs.data(), y.data());
-    else gemv_tokens<false>(M, cb, nt, xt.data(), xs.data(), y.data());
-    for (int t = 0; t < nt; ++t) out_block(y[t], M.svh + cb * 128);
+    const Rows R = { J.xt.data() + (size_t)f * 2 * J.H + (size_t)mm * J.H, (size_t)2 * J.H,
+                     J.xs.data() + 2 * (size_t)f + mm, 2,
+                     J.gu.data() + (size_t)f * 2 * J.I + (size_t)mm * J.I + cb * 128, (size_t)2 * J.I };
+    if (J.mode == 1) gemv_tokens<true>(M, cb, nt, R);
+    else gemv_tokens<false>(M, cb, nt, R);
+    for (int t = 0; t < nt; ++t) out_block(R.y + t * R.ystride, M.svh + cb * 128);
 }
 
-static void ph_act(void* c, int u)            // u = group entry: SwiGLU, then the down input transform
+static void ph_act(void* c, int u)            // u = group entry: SwiGLU (in place of the gate row), down input
 {
     Job& J = *static_cast<Job*>(c);
-    const int g = (int)(std::upper_bound(J.first.begin(), J.first.end(), u) - J.first.begin()) - 1;
-    const Expert& E = J.L->ex[J.gexp[g]];
-    const float* gg = J.gu.data() + (size_t)u * 2 * J.I;
+    const Expert& E = J.L->ex[J.gexp[group_of(J, u)]];
+    float* gg = J.gu.data() + (size_t)u * 2 * J.I;
     const float* uu = gg + J.I;
-    std::vector<float> a(J.I);
-    for (int i = 0; i < J.I; ++i) a[i] = r16(act_gu(gg[i], uu[i], J.limit));
-    J.xds[u] = prep_input(a.data(), E.d.suh, J.I, J.xd.data() + (size_t)u * J.I);
+    for (int i = 0; i < J.I; ++i) gg[i] = r16(act_gu(gg[i], uu[i], J.limit));
+    J.xds[u] = prep_input(gg, E.d.suh, J.I, J.xd.data() + (size_t)u * J.I);
 }
 
 static void ph_down(void* c, int u)           // u = (group, column block of H)
@@ -383,18 +395,11 @@ static void ph_down(void* c, int u)           // u = (group, column block of H)
     const int cb = u % ncb, g = u / ncb;
     const Mat& M = J.L->ex[J.gexp[g]].d;
     const int f = J.first[g], nt = J.first[g + 1] - f;
-    std::vector<const float*> xt(nt);
-    std::vector<float*> y(nt);
-    std::vector<float> xs(nt);
-    for (int t = 0; t < nt; ++t)
-    {
-        xt[t] = J.xd.data() + (size_t)(f + t) * J.I;
-        xs[t] = J.xds[f + t];
-        y[t] = J.yd.data() + (size_t)(f + t) * J.H + cb * 128;
-    }
-    if (J.mode == 1) gemv_tokens<true>(M, cb, nt, xt.data(), xs.data(), y.data());
-    else gemv_tokens<false>(M, cb, nt, xt.data(), xs.data(), y.data());
-    for (int t = 0; t < nt; ++t) out_block(y[t], M.svh + cb * 128);
+    const Rows R = { J.xd.data() + (size_t)f * J.I, (size_t)J.I, J.xds.data() + f, 1,
+                     J.yd.data() + (size_t)f * J.H + cb * 128, (size_t)J.H };
+    if (J.mode == 1) gemv_tokens<true>(M, cb, nt, R);
+    else gemv_tokens<false>(M, cb, nt, R);
+    for (int t = 0; t < nt; ++t) out_block(R.y + t * R.ystride, M.svh + cb * 128);
 }
 
 static void ph_combine(void* c, int u)        // u = (token, 512-column chunk): out = sum of w * y in pick order
@@ -414,7 +419,8 @@ static void ph_combine(void* c, int u)        // u = (token, 512-column chunk): 
     }
 }
 
-// Runs the picks (token, expert, weight) of one layer: out [T][H] (every token row written).
+// Runs the picks (token, expert, weight) of one layer: out [T][H] (every token row written). The picks must name
+// tokens in [0, T) and experts in [0, L.E).
 static void run_picks(Pool& pool, const Layer& L, int H, int I, const float* x, int T, const int32_t* pt,
                       const int32_t* pe, const float* pw, int np, int mode, float limit, float* out, Job& J)
 {
@@ -427,26 +433,26 @@ static void run_picks(Pool& pool, const Layer& L, int H, int I, const float* x, 
     J.x = x;
     J.out = out;
     // group the picks by expert (ascending id), tokens in pick order
-    std::vector<int> cnt(L.E, 0);
-    for (int p = 0; p < np; ++p) cnt[pe[p]]++;
+    J.cnt.assign(L.E, 0);
+    for (int p = 0; p < np; ++p) J.cnt[pe[p]]++;
     J.gexp.clear();
     J.first.assign(1, 0);
-    std::vector<int> slot(L.E, -1);
+    J.slot.assign(L.E, -1);
     for (int e = 0; e < L.E; ++e)
-        if (cnt[e])
+        if (J.cnt[e])
         {
-            slot[e] = (int)J.gexp.size();
+            J.slot[e] = (int)J.gexp.size();
             J.gexp.push_back(e);
-            J.first.push_back(J.first.back() + cnt[e]);
+            J.first.push_back(J.first.back() + J.cnt[e]);
         }
     const int ng = (int)J.gexp.size();
     J.tok.assign(np, 0);
     J.wt.assign(np, 0.0f);
     J.pick_of.assign(np, 0);
-    std::vector<int> fill(J.first.begin(), J.first.end() - 1);
+    J.fill.assign(J.first.begin(), J.first.end() - 1);
     for (int p = 0; p < np; ++p)
     {
-        const int ge = fill[slot[pe[p]]]++;
+        const int ge = J.fill[J.slot[pe[p]]]++;
         J.tok[ge] = pt[p];
         J.wt[ge] = pw[p];
         J.pick_of[p] = ge;
@@ -455,8 +461,8 @@ static void run_picks(Pool& pool, const Layer& L, int H, int I, const float* x, 
     for (int p = 0; p < np; ++p) J.tok_pick_start[pt[p] + 1]++;
     for (int t = 0; t < T; ++t) J.tok_pick_start[t + 1] += J.tok_pick_start[t];
     J.tok_picks.assign(np, 0);
-    std::vector<int> tf(J.tok_pick_start.begin(), J.tok_pick_start.end() - 1);
-    for (int p = 0; p < np; ++p) J.tok_picks[tf[pt[p]]++] = p;
+    J.tfill.assign(J.tok_pick_start.begin(), J.tok_pick_start.end() - 1);
+    for (int p = 0; p < np; ++p) J.tok_picks[J.tfill[pt[p]]++] = p;
     J.xt.resize((size_t)np * 2 * H);
     J.xs.resize((size_t)np * 2);
     J.gu.resize((size_t)np * 2 * I);
@@ -480,21 +486,25 @@ struct Tier
     Pool pool;
     std::vector<int> cpus;
     std::vector<Layer> layers;
+    // the mailbox and its capacity: hx [maxtok][H] fp16, picks [maxpicks][3], hout [maxtok][H] fp32
     int64_t* ctrl = nullptr;
     const uint16_t* hx = nullptr;
     const int32_t* picks = nullptr;
     float* hout = nullptr;
+    int maxtok = 0, maxpicks = 0;
     int H = 0, I = 0;
     // set at any time (mm_tier_set_mode / mm_tier_set_limit), read by the worker at each job
     std::atomic<int> mode{ -1 };
     std::atomic<float> limit{ 0.0f };
     std::thread th;
     std::atomic<bool> quit{ false }, running{ false };
-    std::atomic<int64_t> jobs{ 0 }, experts{ 0 }, tokens{ 0 }, empty{ 0 }, busy_ns{ 0 };
+    std::atomic<int64_t> jobs{ 0 }, experts{ 0 }, tokens{ 0 }, empty{ 0 }, busy_ns{ 0 }, rejected{ 0 }, stale{ 0 };
     std::vector<float> xf;
     std::vector<int32_t> pt, pe;
     std::vector<float> pw;
     Job job;
+    void (*hook)(void*, int, int64_t) = nullptr;   // test hook (impl_set_test_hook)
+    void* hook_arg = nullptr;
 };
 
 static Tier* g_tier = nullptr;
@@ -502,36 +512,99 @@ static Tier* g_tier = nullptr;
 // mode: 0 AFFINE, 1 EXACT, -1 auto (AFFINE)
 static int eff_mode(int m) { return m == 1 ? 1 : 0; }
 
-static void run_job(Tier& Tr, int li, int bsz, int np)
+// The mailbox's x rows fp16 -> fp32. The words are read as relaxed atomics: the publisher may rewrite them while
+// they are read (after a timed-out job), which the sequence check after the copy detects.
+struct Convert
+{
+    const uint16_t* h;
+    float* f;
+    size_t n;
+};
+constexpr size_t CONVERT_UNIT = (size_t)1 << 15;     // halves per pool unit of a large job's conversion
+
+static void convert_range(const uint16_t* h, float* f, size_t lo, size_t hi)
+{
+    size_t i = lo;
+    if (((uintptr_t)(h + i) & 7) == 0)
+        for (; i + 8 <= hi; i += 8)
+        {
+            const uint64_t a = __atomic_load_n(reinterpret_cast<const uint64_t*>(h + i), __ATOMIC_RELAXED);
+            const uint64_t b = __atomic_load_n(reinterpret_cast<const uint64_t*>(h + i + 4), __ATOMIC_RELAXED);
+            _mm256_storeu_ps(f + i, _mm256_cvtph_ps(_mm_set_epi64x((long long)b, (long long)a)));
+        }
+    for (; i < hi; ++i) f[i] = h2f(__atomic_load_n(h + i, __ATOMIC_RELAXED));
+}
+
+static void ph_convert(void* c, int u)
+{
+    const Convert& C = *static_cast<const Convert*>(c);
+    const size_t lo = (size_t)u * CONVERT_UNIT, hi = std::min(C.n, lo + CONVERT_UNIT);
+    convert_range(C.h, C.f, lo, hi);
+}
+
+// One published job, sequence s. The sizes come from the mailbox: a job larger than the mailbox, or naming a
+// layer that was never added, is not computed (the rows of hout that exist are zeroed, so the combine adds
+// nothing) and counted as rejected. The x rows and the picks are copied out first; if the sequence moved on
+// meanwhile, the publisher (the GPU split, after the combine gave up waiting for this job) has been rewriting
+// them, the copy may be torn, and the job is dropped and counted as stale: nobody waits for its partial any more.
+static void serve_job(Tier& Tr, int64_t s, int64_t li, int64_t bsz, int64_t np)
 {
     const int H = Tr.H;
-    Tr.xf.resize((size_t)(bsz > 0 ? bsz : 1) * H);
-    for (size_t i = 0; i < (size_t)bsz * H; ++i) Tr.xf[i] = h2f(Tr.hx[i]);
+    if (li < 0 || li >= (int64_t)Tr.layers.size() || Tr.layers[(size_t)li].E <= 0 || bsz < 0 || np < 0 ||
+        bsz > Tr.maxtok || np > Tr.maxpicks)
+    {
+        const int64_t rows = bsz < 0 ? 0 : (bsz > Tr.maxtok ? Tr.maxtok : bsz);
+        memset(Tr.hout, 0, (size_t)rows * H * sizeof(float));
+        Tr.rejected++;
+        return;
+    }
+    const size_t nx = (size_t)bsz * H;
+    Tr.xf.resize(nx > 0 ? nx : 1);
+    if (nx > CONVERT_UNIT)
+    {
+        Convert C = { Tr.hx, Tr.xf.data(), nx };
+        Tr.pool.run(ph_convert, &C, (int)((nx + CONVERT_UNIT - 1) / CONVERT_UNIT));
+    }
+    else
+        convert_range(Tr.hx, Tr.xf.data(), 0, nx);
     // picks whose token or expert is out of range are left out (as mm_tier_forward leaves them out), so a
     // malformed job cannot index past the layer's experts or the job's rows
-    const int E = Tr.layers[li].E;
-    Tr.pt.resize(np);
-    Tr.pe.resize(np);
-    Tr.pw.resize(np);
+    const Layer& L = Tr.layers[(size_t)li];
+    Tr.pt.resize((size_t)np);
+    Tr.pe.resize((size_t)np);
+    Tr.pw.resize((size_t)np);
     int nk = 0;
-    for (int p = 0; p < np; ++p)
+    for (int64_t p = 0; p < np; ++p)
     {
-        const int32_t t = Tr.picks[3 * p], e = Tr.picks[3 * p + 1];
-        if (t < 0 || t >= bsz || e < 0 || e >= E) continue;
+        const int32_t t = __atomic_load_n(Tr.picks + 3 * p, __ATOMIC_RELAXED);
+        const int32_t e = __atomic_load_n(Tr.picks + 3 * p + 1, __ATOMIC_RELAXED);
+        const int32_t wb = __atomic_load_n(Tr.picks + 3 * p + 2, __ATOMIC_RELAXED);
+        if (t < 0 || t >= bsz || e < 0 || e >= L.E) continue;
         Tr.pt[nk] = t;
         Tr.pe[nk] = e;
-        memcpy(&Tr.pw[nk], &Tr.picks[3 * p + 2], 4);
+        memcpy(&Tr.pw[nk], &wb, 4);
         ++nk;
     }
-    run_picks(Tr.pool, Tr.layers[li], H, Tr.I, Tr.xf.data(), bsz, Tr.pt.data(), Tr.pe.data(), Tr.pw.data(), nk,
+    if (Tr.hook) Tr.hook(Tr.hook_arg, 0, s);
+    // every read of the copy above happens before the sequence is read again
+    std::atomic_thread_fence(std::memory_order_acquire);
+    if (__atomic_load_n(Tr.ctrl, __ATOMIC_RELAXED) != s)
+    {
+        Tr.stale++;
+        return;
+    }
+    run_picks(Tr.pool, L, H, Tr.I, Tr.xf.data(), (int)bsz, Tr.pt.data(), Tr.pe.data(), Tr.pw.data(), nk,
               eff_mode(Tr.mode.load()), Tr.limit.load(), Tr.hout, Tr.job);
+    if (Tr.hook) Tr.hook(Tr.hook_arg, 1, s);
     if (np == 0) Tr.empty++;
-    Tr.experts += np;
+    Tr.experts += nk;
     Tr.tokens += bsz;
 }
 
 // `last` is the job sequence when the tier started: read by the starting thread, so a job published right after
-// mm_tier_start returns is not mistaken for an old one.
+// mm_tier_start returns is not mistaken for an old one. Every job seen is answered with ctrl[1] = its sequence,
+// computed or not; the combine waits for its own sequence only, so an answer to an older job is never taken for
+// a newer one.
 static void worker_main(Tier* Tr, int cpu0, int64_t last)
 {
     Pool::pin(cpu0);
@@ -547,10 +620,8 @@ static void worker_main(Tier* Tr, int cpu0, int64_t last)
         }
         idle = 0;
         const double t0 = now_s();
-        const int li = (int)__atomic_load_n(Tr->ctrl + 2, __ATOMIC_RELAXED);
-        const int bsz = (int)__atomic_load_n(Tr->ctrl + 3, __ATOMIC_RELAXED);
-        const int np = (int)__atomic_load_n(Tr->ctrl + 4, __ATOMIC_RELAXED);
-        if (li >= 0 && li < (int)Tr->layers.size() && Tr->layers[li].E > 0 && bsz >= 0 && np >= 0) run_job(*Tr, li, bsz, np);
+        serve_job(*Tr, s, __atomic_load_n(Tr->ctrl + 2, __ATOMIC_RELAXED), __atomic_load_n(Tr->ctrl + 3, __ATOMIC_RELAXED),
+                  __atomic_load_n(Tr->ctrl + 4, __ATOMIC_RELAXED));
         Tr->busy_ns += (int64_t)((now_s() - t0) * 1e9);
         Tr->jobs++;
         last = s;
@@ -562,18 +633,38 @@ static void worker_main(Tier* Tr, int cpu0, int64_t last)
 
 namespace tier {
 
-int impl_init(int threads, const int* cpus, int ncpus, int64_t* ctrl, const void* hx, const int32_t* picks,
-              float* hout, int mode, int H, int I, int nlayers)
+// At process exit the worker and the pool must be gone before the memory they read (the pinned mailbox and the
+// expert homes, which the GPU runtime releases at its own teardown) is: exit handlers run in the reverse order of
+// their registration, and this one is registered after the runtime and the caller's buffers exist.
+static void at_exit()
 {
+    impl_shutdown();
+}
+
+int impl_init(int threads, const int* cpus, int ncpus, int64_t* ctrl, const void* hx, const int32_t* picks,
+              float* hout, int maxtok, int maxpicks, int mode, int H, int I, int nlayers)
+{
+    static bool exit_hook = false;
     if (g_tier) return set_error(MM_ERR_ARG, "mm_tier_init: the tier is already initialised");
     if (threads < 1 || H <= 0 || I <= 0 || H % 512 || I % 128 || nlayers <= 0 || (ncpus > 0 && !cpus))
         return set_error(MM_ERR_ARG, "mm_tier_init: need threads >= 1, H a multiple of 512, I of 128, nlayers > 0");
+    const bool mailbox = ctrl || hx || picks || hout;
+    if (mailbox && (!ctrl || !hx || !picks || !hout || maxtok <= 0 || maxpicks <= 0))
+        return set_error(MM_ERR_ARG, "mm_tier_init: a mailbox needs ctrl, hx, picks and hout and capacities maxtok > 0, "
+                                     "maxpicks > 0 (got %d, %d)", maxtok, maxpicks);
+    if (!exit_hook)
+    {
+        if (atexit(at_exit) != 0) return set_error(MM_ERR_ARG, "mm_tier_init: atexit failed");
+        exit_hook = true;
+    }
     Tier* T = new Tier();
     if (ncpus > 0) T->cpus.assign(cpus, cpus + ncpus);
     T->ctrl = ctrl;
     T->hx = static_cast<const uint16_t*>(hx);
     T->picks = picks;
     T->hout = hout;
+    T->maxtok = mailbox ? maxtok : 0;
+    T->maxpicks = mailbox ? maxpicks : 0;
     T->mode.store(mode);
     T->H = H;
     T->I = I;
@@ -664,18 +755,19 @@ int impl_forward(int li, const float* x, int m, const int32_t* sel, const float*
     if (li < 0 || li >= (int)T->layers.size() || T->layers[li].E <= 0 || m < 0 || k <= 0 || !x || !sel || !w || !out)
         return set_error(MM_ERR_ARG, "mm_tier_forward: bad layer or argument");
     const int E = T->layers[li].E;
-    std::vector<int32_t> pt, pe;
-    std::vector<float> pw;
+    T->pt.clear();
+    T->pe.clear();
+    T->pw.clear();
     for (int t = 0; t < m; ++t)
         for (int j = 0; j < k; ++j)
         {
             const int e = sel[(size_t)t * k + j];
             if (e < 0 || e >= E) continue;
-            pt.push_back(t);
-            pe.push_back(e);
-            pw.push_back(w[(size_t)t * k + j]);
+            T->pt.push_back(t);
+            T->pe.push_back(e);
+            T->pw.push_back(w[(size_t)t * k + j]);
         }
-    run_picks(T->pool, T->layers[li], T->H, T->I, x, m, pt.data(), pe.data(), pw.data(), (int)pt.size(),
+    run_picks(T->pool, T->layers[li], T->H, T->I, x, m, T->pt.data(), T->pe.data(), T->pw.data(), (int)T->pt.size(),
               eff_mode(mode >= 0 ? mode : T->mode.load()), T->limit.load(), out, T->job);
     return MM_OK;
 }
@@ -686,7 +778,7 @@ int impl_stats(int64_t* out)
     if (!out) return set_error(MM_ERR_ARG, "mm_tier_stats: null pointer");
     if (!T)
     {
-        for (int i = 0; i < 5; ++i) out[i] = 0;
+        for (int i = 0; i < MM_TIER_NSTATS; ++i) out[i] = 0;
         return MM_OK;
     }
     out[0] = T->jobs.load();
@@ -694,6 +786,18 @@ int impl_stats(int64_t* out)
     out[2] = T->tokens.load();
     out[3] = T->empty.load();
     out[4] = T->busy_ns.load();
+    out[5] = T->rejected.load();
+    out[6] = T->stale.load();
+    return MM_OK;
+}
+
+int impl_set_test_hook(void (*fn)(void*, int, int64_t), void* arg)
+{
+    Tier* T = g_tier;
+    if (!T) return set_error(MM_ERR_ARG, "impl_set_test_hook: mm_tier_init first");
+    if (T->running.load()) return set_error(MM_ERR_ARG, "impl_set_test_hook: the worker is running");
+    T->hook = fn;
+    T->hook_arg = arg;
     return MM_OK;
 }
 

@@ -19,12 +19,12 @@ bool g_ok = false;     // the CPU passed the check in mm_tier_init
 extern "C" {
 
 int mm_tier_init(int threads, const int* cpus, int ncpus, int64_t* ctrl, const void* hx, const int32_t* picks,
-                 float* hout, int mode, int H, int I, int nlayers)
+                 float* hout, int maxtok, int maxpicks, int mode, int H, int I, int nlayers)
 {
     if (!cpu_ok())
         return mm::set_error(MM_ERR_UNSUP, "mm_tier_init: the host tier needs AVX-512 (F, BW, VL, VBMI2, VNNI), F16C and FMA");
     g_ok = true;
-    return tier::impl_init(threads, cpus, ncpus, ctrl, hx, picks, hout, mode, H, I, nlayers);
+    return tier::impl_init(threads, cpus, ncpus, ctrl, hx, picks, hout, maxtok, maxpicks, mode, H, I, nlayers);
 }
 
 #define NEED_INIT(who) \
@@ -78,7 +78,7 @@ int mm_tier_stats(int64_t* out)
     if (!out) return mm::set_error(MM_ERR_ARG, "mm_tier_stats: null pointer");
     if (!g_ok)
     {
-        for (int i = 0; i < 5; ++i) out[i] = 0;
+        for (int i = 0; i < MM_TIER_NSTATS; ++i) out[i] = 0;
         return MM_OK;
     }
     return tier::impl_stats(out);

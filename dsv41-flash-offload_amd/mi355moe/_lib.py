@@ -61,7 +61,7 @@ _SIGS = {
     "mm_synth_layer": (i32, [ctypes.POINTER(MMLayer), u64, vp]),
     "mm_expert_seed": (u64, [u64, u64]),
     "mm_prepare_input": (i32, [vp, i32, i32, i32, vp, vp, vp]),
-    "mm_tier_init": (i32, [i32, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32]),
+    "mm_tier_init": (i32, [i32, vp, i32, vp, vp, vp, vp, i32, i32, i32, i32, i32, i32]),
     "mm_tier_add_layer": (i32, [i32, i32, vp, vp, vp, vp, vp, vp, vp]),
     "mm_tier_set_limit": (i32, [f32]),
     "mm_tier_set_mode": (i32, [i32]),

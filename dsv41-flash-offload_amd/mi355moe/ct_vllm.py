@@ -75,7 +75,8 @@ def _init(layer):
     S["nlayers"] = int(os.environ.get("DSV41_CT_LAYERS", "40"))
     if S["cpu_tier"]:
         _tier.init(H, layer.I, S["nlayers"], mailbox={"ctrl": S["ctrl"], "hx": S["hx"], "picks": S["picks"],
-                                                        "hout": S["hout"]})
+                                                        "hout": S["hout"], "maxtok": S["maxbsz"],
+                                                        "maxpicks": S["maxpicks"], "owner": S["mail"]})
         S["limit"] = _f("DSV41_CT_LIMIT", 10.0)
         _tier.set_limit(S["limit"] if S["limit"] > 0 else 0.0)
     S["init"] = True
@@ -347,8 +348,9 @@ def uninstall(X):
 
 
 def reset():
-    """Forget every registered layer, the cache and the host tier (tests, benchmarks)."""
-    if S.get("cpu_tier") and _tier.running():
+    """Forget every registered layer, the cache and the host tier (tests, benchmarks). The tier is shut down
+    before the mailbox it reads is released."""
+    if _tier.running():
         _tier.shutdown()
     S.clear()
     S.update({"layers": [], "started": False, "init": False, "selftest": None, "cpu_tier": False})

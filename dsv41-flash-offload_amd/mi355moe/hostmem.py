@@ -12,6 +12,7 @@ class HostBuffer:
     fence are visible to the CPU, and CPU writes to the GPU)."""
 
     def __init__(self, nbytes):
+        self.holders = 0          # users that read the memory from other threads (the host tier): free() refuses
         self.nbytes = int(nbytes)
         p = ctypes.c_void_p()
         _lib.call("mm_host_alloc", ctypes.byref(p), max(self.nbytes, 1))
@@ -27,7 +28,17 @@ class HostBuffer:
     def data_ptr(self, offset=0):
         return self.ptr + offset
 
+    def hold(self):
+        """Mark the memory as read by a thread this object does not control (the host tier's workers); free() is
+        refused until release(). The holder keeps a reference, so garbage collection cannot free it either."""
+        self.holders += 1
+
+    def release(self):
+        self.holders = max(0, self.holders - 1)
+
     def free(self):
+        if self.holders:
+            raise RuntimeError("HostBuffer.free: the memory is still read by the host tier (shut it down first)")
         if self.ptr:
             _lib.call("mm_host_free", self.ptr)
             self.ptr = None

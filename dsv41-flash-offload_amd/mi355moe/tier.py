@@ -2,14 +2,19 @@
 home rows, for the picks the decode split sends to the host (the reference's tier_* extension,
 kernels/cpu_avx2/ft_tier_ext.cpp:36-231, driven from ct/ct_vllm.py:56-87,143-152).
 
-  init(H, I, nlayers, mailbox=None)   workers and the mailbox (ctrl / hx / picks / hout addresses, or None for
-                                      forward() only); threads, CPUs and mode from DSV41_CT_THREADS, DSV41_CT_CPUS
-                                      and DSV41_CT_MODE as in the reference
+  init(H, I, nlayers, mailbox=None)   workers and the mailbox (ctrl / hx / picks / hout addresses, its capacity
+                                      maxtok / maxpicks and the buffer that owns it, or None for forward() only);
+                                      threads, CPUs and mode from DSV41_CT_THREADS, DSV41_CT_CPUS and DSV41_CT_MODE
+                                      as in the reference
   add_layer(li, layer)                a layer with a pinned host home (ExpertStore): its home rows and host copies
                                       of its scales
   start() / stop() / shutdown()       the serving thread
   forward(li, x, sel, w, mode)        synchronous forward (tests, the tier's self-check and calibration)
-  stats()                             jobs, picks, tokens, empty jobs, busy ns
+  stats()                             jobs, picks, tokens, empty jobs, busy ns, rejected and stale jobs
+
+Host memory the workers read (the mailbox, the layers' pinned expert homes) is held while the tier is up: the
+tier keeps a reference to each owning buffer and marks it held (HostBuffer.hold), so it can be neither collected
+nor freed before shutdown(). The library's own exit handler stops the threads at process exit in any case.
 """
 import atexit
 import ctypes
@@ -19,7 +24,23 @@ import numpy as np
 
 from . import _lib
 
-_T = {"up": False, "running": False, "layers": {}, "cpus": [], "threads": 0}
+_T = {"up": False, "running": False, "layers": {}, "cpus": [], "threads": 0, "held": []}
+
+STATS = ("jobs", "picks", "tokens", "empty", "busy_ns", "rejected", "stale")
+
+
+def _hold(owner):
+    if owner is not None and hasattr(owner, "hold"):
+        owner.hold()
+    if owner is not None:
+        _T["held"].append(owner)
+
+
+def _release_all():
+    for o in _T["held"]:
+        if hasattr(o, "release"):
+            o.release()
+    _T["held"] = []
 
 
 def _cpus_from_env():
@@ -50,8 +71,10 @@ def init(H, I, nlayers, mailbox=None, threads=None, cpus=None, mode=None):
     carr = (ctypes.c_int * max(1, len(cpus)))(*cpus)
     mb = mailbox or {}
     _lib.call("mm_tier_init", int(threads), carr, len(cpus), mb.get("ctrl"), mb.get("hx"), mb.get("picks"),
-              mb.get("hout"), mode, int(H), int(I), int(nlayers))
-    _T.update(up=True, cpus=cpus, threads=int(threads), H=int(H), I=int(I), mode=mode, mailbox=bool(mailbox))
+              mb.get("hout"), int(mb.get("maxtok", 0)), int(mb.get("maxpicks", 0)), mode, int(H), int(I), int(nlayers))
+    _T.update(up=True, cpus=cpus, threads=int(threads), H=int(H), I=int(I), mode=mode, mailbox=bool(mailbox),
+              held=[])
+    _hold(mb.get("owner"))
     if not _T.get("atexit"):
         # the worker and the pool threads must be gone before the interpreter frees the pinned mailbox and homes
         atexit.register(_at_exit)
@@ -75,6 +98,9 @@ def add_layer(li, layer=None, ptrs=None, scales=None):
     """Register layer li: an ExpertStore with a pinned host home, or explicit `ptrs` (int64 [E, 3] host
     addresses) and `scales` (dict of fp16 arrays suh_g, svh_g, suh_u, svh_u, suh_d, svh_d, [E, .])."""
     if layer is not None:
+        home = getattr(layer, "host_home", None)
+        if home is not None:
+            _hold(getattr(home, "buffer", home))      # the workers read the pinned home rows in place
         ptrs = layer.home.numpy() if hasattr(layer.home, "numpy") else np.asarray(layer.home)
         s13, v13 = layer.w13_suh.cpu().numpy(), layer.w13_svh.cpu().numpy()
         scales = {"suh_g": s13[:, 0], "svh_g": v13[:, 0], "suh_u": s13[:, 1], "svh_u": v13[:, 1],
@@ -101,6 +127,7 @@ def stop():
 def shutdown():
     _lib.call("mm_tier_shutdown")
     _T.update(up=False, running=False, layers={})
+    _release_all()
 
 
 def running():
@@ -125,6 +152,6 @@ def forward(li, x, sel, w, mode=-1):
 
 
 def stats():
-    a = np.zeros(5, np.int64)
+    a = np.zeros(len(STATS), np.int64)
     _lib.call("mm_tier_stats", _p(a))
-    return {"jobs": int(a[0]), "picks": int(a[1]), "tokens": int(a[2]), "empty": int(a[3]), "busy_ns": int(a[4])}
+    return {k: int(v) for k, v in zip(STATS, a)}

@@ -286,12 +286,16 @@ int mm_prepare_input(const float* x, int T, int H, int rescale, void* x_bf16, vo
  * mm_tier_init (tier_init, ft_tier_ext.cpp:36-56): `threads` workers pinned to cpus[0 .. ncpus) (the serving thread
  * is worker 0 and runs on cpus[0]); the mailbox is the split's: ctrl int64 [16] (ctrl[0] job sequence, written by
  * the GPU last; ctrl[1] done sequence, written here last; ctrl[2] layer, ctrl[3] tokens, ctrl[4] picks), hx fp16
- * [tokens][H], picks int32 [picks][3] = (token, expert, weight fp32 bits), hout fp32 [tokens][H] (all host
- * memory the GPU maps, e.g. mm_host_alloc); they may be NULL when only mm_tier_forward is used. mode: 1 EXACT
- * (fp16-rounded weights), 0 AFFINE, -1 automatic (AFFINE; the reference's automatic choice of its int16 path is
- * not built). H a multiple of 512, I of 128. */
+ * [maxtok][H], picks int32 [maxpicks][3] = (token, expert, weight fp32 bits), hout fp32 [maxtok][H] (all host
+ * memory the GPU maps, e.g. mm_host_alloc); they may be NULL (and the capacities 0) when only mm_tier_forward is
+ * used. A published job with more than maxtok tokens or maxpicks picks, or naming a layer never added, is not
+ * computed: the serving thread zeroes the hout rows that exist, answers it, and counts it as rejected (the
+ * reference's worker trusts ctrl[3] and ctrl[4]). mode: 1 EXACT (fp16-rounded weights), 0 AFFINE, -1 automatic
+ * (AFFINE; the reference's automatic choice of its int16 path is not built). H a multiple of 512, I of 128.
+ * The first call registers a process exit handler that stops the serving thread and the workers before memory
+ * released at exit (the mailbox, the expert homes) can go away. */
 int mm_tier_init(int threads, const int* cpus, int ncpus, int64_t* ctrl, const void* hx, const int32_t* picks,
-                 float* hout, int mode, int H, int I, int nlayers);
+                 float* hout, int maxtok, int maxpicks, int mode, int H, int I, int nlayers);
 /* Layer li (tier_add_layer, ft_tier_ext.cpp:60-101): ptrs int64 [E][3] host addresses of each expert's gate, up and
  * down trellis (tiles [K/16][N/16][96 B], as the GPU reads them); scales fp16 in host memory, per expert:
  * suh_g [E][H], svh_g [E][I], suh_u [E][H], svh_u [E][I], suh_d [E][I], svh_d [E][H]. The memory stays the
@@ -302,9 +306,12 @@ int mm_tier_add_layer(int li, int E, const int64_t* ptrs, const void* suh_g, con
 int mm_tier_set_limit(float limit);
 int mm_tier_set_mode(int mode);
 /* Start / stop the serving thread (tier_start, tier_stop, ft_tier_ext.cpp:161-175): it waits for ctrl[0] to move,
- * computes sum over the picks of token t of w * expert(x_t) into hout rows 0 .. tokens-1 (every row written),
- * then stores ctrl[1] = ctrl[0] with release ordering. mm_tier_shutdown also stops the workers and frees the
- * tier (mm_tier_init may then be called again). */
+ * copies the job's x rows and picks, computes sum over the picks of token t of w * expert(x_t) into hout rows
+ * 0 .. tokens-1 (every row written), then stores ctrl[1] = ctrl[0] with release ordering. If ctrl[0] moved on
+ * while the job was being copied (the combine gave up on it and the split published the next job over it), the
+ * job is dropped uncomputed (hout untouched) and counted as stale; it is still answered, and the next job is
+ * served. mm_tier_shutdown also stops the workers and frees the tier (mm_tier_init may then be called again);
+ * the mailbox and the expert homes must stay allocated until it returns. */
 int mm_tier_start(int cpu0);
 int mm_tier_stop(void);
 int mm_tier_shutdown(void);
@@ -312,7 +319,9 @@ int mm_tier_shutdown(void);
  * [m][H] (fp16-valued), sel int32 [m][k] (entries outside [0, E) skipped), w fp32 [m][k] -> out fp32 [m][H];
  * mode as for mm_tier_init (-1: the tier's mode). */
 int mm_tier_forward(int li, const float* x, int m, const int32_t* sel, const float* w, int k, float* out, int mode);
-/* out int64 [5]: jobs served, picks computed, tokens, jobs without picks, busy nanoseconds (tier_stats). */
+/* out int64 [MM_TIER_NSTATS]: jobs answered, picks computed, tokens, jobs without picks, busy nanoseconds
+ * (tier_stats), jobs rejected (larger than the mailbox, or an unknown layer), stale jobs dropped. */
+#define MM_TIER_NSTATS 7
 int mm_tier_stats(int64_t* out);
 
 #ifdef __cplusplus

@@ -137,6 +137,7 @@ def test_mailbox_worker_serves_jobs(tier):
     picks = np.zeros((T * k + 3, 3), np.int32)
     hout = np.full((T, H), np.nan, np.float32)
     mb = {k_: a.ctypes.data for k_, a in (("ctrl", ctrl), ("hx", hx), ("picks", picks), ("hout", hout))}
+    mb.update(maxtok=T, maxpicks=picks.shape[0])
     tier.init(H, I, 2, mailbox=mb, threads=3, cpus=sorted(os.sched_getaffinity(0))[:3], mode=0)
     tier.set_limit(10.0)
     tier.add_layer(1, ptrs=ptrs, scales=sc)
@@ -174,4 +175,47 @@ def test_mailbox_worker_serves_jobs(tier):
         picks[p] = (t, e, np.float32(wt).view(np.int32))
     job(3, len(rows))
     assert np.array_equal(hout, want)
+    # jobs larger than the mailbox (tokens, then picks) and one naming a layer never added: answered, not
+    # computed, the hout rows zeroed, counted as rejected
+    for seq, (li, bsz, npk) in enumerate(((1, T + 1, 4), (1, T, picks.shape[0] + 1), (0, T, 4)), start=4):
+        hout[:] = 1.0
+        ctrl[2], ctrl[3], ctrl[4] = li, bsz, npk
+        ctrl[0] = seq
+        t0 = time.time()
+        while ctrl[1] != seq:
+            assert time.time() - t0 < 20, "the worker did not answer"
+            time.sleep(1e-4)
+        assert np.count_nonzero(hout) == 0
+    s = tier.stats()
+    assert s["jobs"] == 6 and s["rejected"] == 3 and s["stale"] == 0
     tier.stop()
+
+
+def test_tier_holds_the_memory_its_workers_read(tier):
+    """The mailbox's owner is held while the tier is up (HostBuffer.free refuses it) and released by shutdown."""
+    from mi355moe.hostmem import HostBuffer
+    owner = object.__new__(HostBuffer)        # the bookkeeping only: no pinned allocation on a CPU-only host
+    owner.holders, owner.ptr, owner.nbytes = 0, None, 0
+    H, I, T = 512, 256, 2
+    ctrl = np.zeros(16, np.int64)
+    hx = np.zeros((T, H), np.float16)
+    picks = np.zeros((8, 3), np.int32)
+    hout = np.zeros((T, H), np.float32)
+    mb = {k_: a.ctypes.data for k_, a in (("ctrl", ctrl), ("hx", hx), ("picks", picks), ("hout", hout))}
+    mb.update(maxtok=T, maxpicks=8, owner=owner)
+    tier.init(H, I, 1, mailbox=mb, threads=2, cpus=sorted(os.sched_getaffinity(0))[:2])
+    assert owner.holders == 1
+    with pytest.raises(RuntimeError):
+        owner.free()
+    tier.shutdown()
+    assert owner.holders == 0
+    owner.free()                              # nothing allocated: a no-op once released
+
+
+def test_mailbox_needs_its_capacity(tier):
+    from mi355moe import _lib  # noqa: F401  (the library loads)
+    ctrl = np.zeros(16, np.int64)
+    buf = np.zeros(4096, np.float32)
+    mb = {"ctrl": ctrl.ctypes.data, "hx": buf.ctypes.data, "picks": buf.ctypes.data, "hout": buf.ctypes.data}
+    with pytest.raises(RuntimeError, match="capacities"):
+        tier.init(512, 256, 1, mailbox=mb, threads=1, cpus=[])
