@@ -6,7 +6,8 @@
 // device variable, so the entry point never passes it to a kernel or a copy: on the first call on a device (with
 // that device current) it asks the runtime for the device's own address of the array with hipGetSymbolAddress
 // and keeps it per device; every launch then gets that address. Each device that loads the library holds its own
-// copy of the array until the process ends. Every call on one device shares that device's array, which keeps
+// copy of the array until the process ends. That first call must therefore run outside graph capture; the
+// calls after it only launch kernels and can be captured. Every call on one device shares that device's array, which keeps
 // the previous call's contents: mm_moe_decode's launches write every workspace location before they read it,
 // so nothing needs clearing, but calls that overlap on one device (two streams, two threads) race.
 #include <mutex>

@@ -50,6 +50,25 @@ class Checkpoint:
             with safe_open(fn, "pt") as h:
                 for k in h.keys():
                     self.where[k] = fn
+        self._index()
+
+    def _index(self):
+        # every key under its unprefixed name (from a "layers." that starts the key or follows a "."), the first
+        # key of the checkpoint winning, and the routed experts present per layer: one pass over the keys, so a
+        # lookup costs a dict probe whatever the prefix
+        self._bare = {}
+        self._experts = {}
+        pat = re.compile(r"^layers\.(\d+)\.ffn\.experts\.(\d+)\.w1\.trellis$")
+        for k in self.where:
+            i = k.find("layers.")
+            while i >= 0:
+                if i == 0 or k[i - 1] == ".":
+                    bare = k[i:]
+                    self._bare.setdefault(bare, k)
+                    m = pat.match(bare)
+                    if m:
+                        self._experts.setdefault(int(m.group(1)), set()).add(int(m.group(2)))
+                i = k.find("layers.", i + 1)
 
     def keys(self):
         return self.where.keys()
@@ -65,17 +84,16 @@ class Checkpoint:
         base = f"layers.{layer}.ffn.experts.{e}.{w}.{part}"
         if base in self.where:
             return base
-        for k in self.where:
-            if k.endswith("." + base):
-                return k
-        raise KeyError(f"checkpoint has no tensor {base}")
+        k = self._bare.get(base)
+        if k is None:
+            raise KeyError(f"checkpoint has no tensor {base}")
+        return k
 
     def expert_tensor(self, layer, e, w, part):
         return self.get(self._key(layer, e, w, part))
 
     def num_experts(self, layer):
-        pat = re.compile(r"(?:^|\.)layers\." + str(int(layer)) + r"\.ffn\.experts\.(\d+)\.w1\.trellis$")
-        ids = {int(m.group(1)) for k in self.where for m in [pat.search(k)] if m}
+        ids = self._experts.get(int(layer), set())
         if not ids:
             raise KeyError(f"checkpoint has no experts for layer {layer}")
         if ids != set(range(max(ids) + 1)):

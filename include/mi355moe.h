@@ -167,7 +167,9 @@ int mm_moe_decode(const mm_layer_t* layer, const void* x, int x_dtype, int resca
  * of MM_NOALLOC_SCRATCH_BYTES per device, and the call allocates nothing. A call whose workspace
  * (mm_gemv_workspace(T * topk, E, H, I)) exceeds that size fails with MM_ERR_ARG: at most 62 routes per call at
  * H 4096 / I 2048 (T = 6 at top-8 plus a shared expert), 52 at H 5120 / I 2304. All calls on one device
- * share its array: calls that overlap on one device (concurrent streams or threads) race. */
+ * share its array: calls that overlap on one device (concurrent streams or threads) race. The first call on a
+ * device looks up the array's device address (hipGetSymbolAddress) and must run outside graph capture; later
+ * calls may be captured. */
 int mm_moe_decode_noalloc(const mm_layer_t* layer, const void* x, int x_dtype, int rescale, int T, int topk,
                           const int64_t* ids, const float* w, int max_rows, float* out, mm_stream_t stream);
 

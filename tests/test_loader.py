@@ -60,3 +60,22 @@ def test_refuses_mcg_codebook_and_bad_shapes(tmp_path):
     save_file(t, bad)
     with pytest.raises(ValueError):
         loader.load_layer(bad, 0, device="cpu")
+
+
+def test_prefixed_key_lookup_is_indexed():
+    """A full-size key set with a prefix (40 layers x 384 experts x 9 tensors): every lookup is a dict probe, so
+    all of one layer's expert lookups take well under a second."""
+    import time
+    from mi355moe.loader import Checkpoint
+    ck = object.__new__(Checkpoint)
+    ck.where = {f"model.layers.{L}.ffn.experts.{e}.{w}.{p}": "f" for L in range(40) for e in range(384)
+                for w in ("w1", "w3", "w2") for p in ("trellis", "suh", "svh")}
+    ck.where["model.layers.0.self_attn.q_proj.weight"] = "f"
+    ck._index()
+    t0 = time.perf_counter()
+    for e in range(384):
+        for w in ("w1", "w3", "w2"):
+            for p in ("trellis", "suh", "svh"):
+                assert ck._key(39, e, w, p) == f"model.layers.39.ffn.experts.{e}.{w}.{p}"
+    assert time.perf_counter() - t0 < 1.0
+    assert ck.num_experts(39) == 384
