@@ -110,7 +110,10 @@ def cpu_child(spec):
     """One reference CPU-tier pool (the pool starts once per process): times the requested tasks and prints one
     JSON line. Tasks: "config0" (one layer at T = 1: top-8 of 384 + the shared expert), "layer" (layer 0 of the
     decode step: T = 4, top-8 + shared), "jobs" (the reference's tier job shapes at the served DSV41 shape, random
-    experts of a 64-expert layer, x ~ N(0, 0.35), weights 0.15, as experimental/b70-tier/repro/smt_bench.py)."""
+    experts of a 64-expert layer, x ~ N(0, 0.35), weights 0.15, as experimental/b70-tier/repro/smt_bench.py),
+    "prefill" (the 16,384-token skewed layer: one timed moe_forward over a stratified quarter of the experts,
+    every 4th in descending route count, each with all of its routes; the time is scaled by all routes over the
+    sampled routes)."""
     import numpy as np
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle as O
@@ -150,6 +153,12 @@ def cpu_child(spec):
     DH, DI, DE = 5120, 2304, 64
     if "jobs" in tasks:
         add_layer(1, DE, DH, DI, 1000, range(DE))
+    if "prefill" in tasks:
+        TP = 16384
+        pids, pw = workload.skewed_routing(TP, K, E, seed=2000)
+        pcounts = np.bincount(pids.ravel(), minlength=E)
+        samp = np.argsort(-pcounts, kind="stable")[::4]
+        add_layer(2, E, H, I, 1000, samp)
     cpus = spec["cpus"]
     carr = (ctypes.c_int * len(cpus))(*cpus)
     R.ref_pool_start(int(spec["threads"]), carr, len(cpus))
@@ -209,6 +218,30 @@ def cpu_child(spec):
             res.append({"task": f"job m{m}k{k}", "shape": "H 5120 / I 2304", "tokens": m, "experts_per_token": k,
                         "mode": "auto", "mode_used": md, "p50_ms": round(ts[len(ts) // 2] * 1e3, 4),
                         "p90_ms": round(ts[int(len(ts) * 0.9)] * 1e3, 4), "timed_jobs": len(ts), "warmup_jobs": 50})
+    if "prefill" in tasks:
+        mask = np.isin(pids, samp)
+        tt, jj = np.nonzero(mask)
+        xp = np.random.default_rng(7).normal(0, 1, (TP, H)).astype(np.float16).astype(np.float32)
+        tok = tt.astype(np.int32)
+        exp = pids[tt, jj].astype(np.int32)
+        wt = pw[tt, jj].astype(np.float32)
+        outp = np.zeros((TP, H), np.float32)
+        # warm-up: the first 64 tokens' sampled picks (pool and workspaces up)
+        wm = tok < 64
+        w_tok, w_exp, w_wt = (np.ascontiguousarray(a[wm]) for a in (tok, exp, wt))   # held across the call
+        R.ref_moe_forward(2, P(xp), 64, P(w_tok), P(w_exp), P(w_wt), int(w_tok.size), P(outp), -1)
+        t0 = time.perf_counter()
+        md = R.ref_moe_forward(2, P(xp), TP, P(tok), P(exp), P(wt), int(tok.size), P(outp), -1)
+        dt = time.perf_counter() - t0
+        if md < 0:
+            raise RuntimeError("reference CPU tier refused the call")
+        scale = pids.size / tok.size
+        fat = pcounts > 32
+        flops = 2.0 * pcounts[fat].sum() * 3 * H * I
+        res.append({"task": "prefill16k", "tokens": TP, "mode": "auto", "mode_used": {0: "AFFINE", 1: "EXACT", 2: "I16"}[md],
+                    "sampled_experts": int(samp.size), "sampled_routes": int(tok.size), "routes": int(pids.size),
+                    "sample_s": round(dt, 3), "layer_s_scaled": round(dt * scale, 3),
+                    "tok_s": round(TP / (dt * scale), 1), "tflops": round(flops / (dt * scale) / 1e12, 3)})
     print(json.dumps({"threads": spec["threads"], "cpus": cpus, "results": res}), flush=True)
 
 
@@ -222,7 +255,7 @@ def cpu_baseline(L=40, T=4):
         return None
     topo = host_topology()
     sets = [{"label": "every physical core of the GPU's NUMA node", "threads": len(topo["node_physical_cpus"]),
-             "cpus": topo["node_physical_cpus"], "tasks": ["config0", "layer", "jobs"], "modes": [-1, 1],
+             "cpus": topo["node_physical_cpus"], "tasks": ["config0", "layer", "jobs", "prefill"], "modes": [-1, 1],
              "budget_s": 20.0},
             {"label": "22 threads (the reference's DSV41_CT_THREADS)", "threads": 22, "cpus": topo["allowed"],
              "tasks": ["config0", "layer"], "modes": [-1], "budget_s": 8.0}]
@@ -243,6 +276,7 @@ def cpu_baseline(L=40, T=4):
     if not runs:
         return None
     main = next((x for x in runs[0]["results"] if x["task"] == "layer" and x["mode"] == "auto"), None)
+    pre = next((x for x in runs[0]["results"] if x["task"] == "prefill16k"), None)
     topo_out = {k: topo[k] for k in ("cpus_allowed", "sockets", "physical_cores", "threads_per_core", "numa_nodes",
                                      "gpu_numa_node", "gpu_numa_node_raw")}
     return {"value": round(T / (L * main["p50_ms"] * 1e-3), 3), "unit": "tok/s", "cores": runs[0]["threads"],
@@ -250,7 +284,12 @@ def cpu_baseline(L=40, T=4):
             "sample": f"layer 0 of the step ({main['experts']} experts, T={T}) on the reference CPU tier "
                       f"(ft_core.h moe_forward, auto mode = {main['mode_used']}), {main['timed_jobs']} timed jobs "
                       f"after 50 warm-up, p50 {main['p50_ms']:.3f} ms (p90 {main['p90_ms']:.3f}), scaled to {L} layers",
-            "topology": topo_out, "runs": runs}
+            "topology": topo_out, "runs": runs,
+            "prefill16k": None if pre is None else dict(pre, cores=runs[0]["threads"], kind="reference",
+                                                          sample=f"one moe_forward over {pre['sampled_experts']} of 384 "
+                                                                 f"experts (every 4th by route count, all their "
+                                                                 f"routes: {pre['sampled_routes']} of {pre['routes']}), "
+                                                                 f"time scaled by routes")}
 
 
 # ------------------------------------------------------------------------------------------ GPU legs
@@ -407,6 +446,37 @@ def bench_prefill(store, E, H, I, k, reps, tokens=16384, cap=32):
             "mfma_util_layer": round(flops / (t_layer * 1e-3) / peak, 4),
             "mfma_util_grouped_gemm": round(flops / (t_grouped * 1e-3) / peak, 4),
             "mfma_peak_tflops": MFMA_PEAK_TFLOPS, "dtype": "fp16 MFMA, fp32 accumulation", "reps": reps}
+
+
+def bench_router(dev, E, H, k, reps=20):
+    """The router (logits x G^T in fp32 from bf16 x and fp32 G ~ N(0, 0.02), top-k, softmax of the picks) at the
+    decode (T = 4) and prefill (T = 16,384) sizes."""
+    import numpy as np
+    import torch
+    from mi355moe import _lib, workload
+    G = torch.from_numpy(np.random.default_rng(5).normal(0, 0.02, (E, H)).astype(np.float32)).to(dev)
+    out = {}
+    for T in (4, 16384):
+        x = torch.from_numpy(workload.activations(T, H, seed=7)).to(dev).to(torch.bfloat16)
+        ids = torch.empty((T, k), dtype=torch.int64, device=dev)
+        w = torch.empty((T, k), dtype=torch.float32, device=dev)
+        logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+
+        def call():
+            _lib.call("mm_router_topk", x.data_ptr(), T, H, G.data_ptr(), E, k, logits.data_ptr(), ids.data_ptr(),
+                      w.data_ptr(), _lib.stream_ptr())
+        call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        out[f"t{T}"] = {"ms": round(ms, 4), "fp32_tflops": round(2.0 * T * E * H / (ms * 1e-3) / 1e12, 2)}
+    out["workload"] = f"router top-{k} of {E} experts, H {H}: bf16 x, fp32 gate, fp32 logits and softmax"
+    return out
 
 
 def bench_split(calls=10000, per_graph=100):
@@ -785,6 +855,24 @@ def main():
         f"{d_gbs:.0f} GB/s; step {step_gbs:.0f} GB/s")
     d1 = decode_step(stores, E, H, I, K_TOP, 1, L, args.steps, args.warmup, roofline=False)
     ms1 = d1["ms_step"]
+    # the same steps with EXACT weights (every decoded weight rounded to fp16, as the oracle and the reference's
+    # reconstructed GPU weights are) instead of the AFFINE codebook evaluation
+    for st in stores:
+        st.exact, st._c = True, None
+    d4x = decode_step(stores, E, H, I, K_TOP, T, L, args.steps, args.warmup, roofline=True)
+    d1x = decode_step(stores, E, H, I, K_TOP, 1, L, args.steps, args.warmup, roofline=False)
+    for st in stores:
+        st.exact, st._c = False, None
+    exact = {"ms_per_step": round(d4x["ms_step"], 4), "tok_s": round(T / (d4x["ms_step"] * 1e-3), 2),
+             "hbm_gbs": round(d4x["step_bytes"] / (d4x["ms_step"] * 1e-3) / 1e9, 1),
+             "gate_up_kernel_us": round(float(d4x["t_gu"]) * 1e3, 2),
+             "gate_up_kernel_gbs": round(d4x["bytes_gu"] / (d4x["t_gu"] * 1e-3) / 1e9, 1),
+             "t1_ms_per_step": round(d1x["ms_step"], 4), "t1_tok_s": round(1 / (d1x["ms_step"] * 1e-3), 2)}
+    log(f"decode EXACT: {exact}")
+    router = None
+    if not args.no_prefill:
+        router = bench_router(dev, E, H, K_TOP)
+        log(f"router: {router}")
     prefill = None
     if not args.no_prefill:
         log("prefill: 16384-token layer")
@@ -848,6 +936,9 @@ def main():
         "decode_t1": {"ms_per_step": round(ms1, 4), "tok_s": round(1 / (ms1 * 1e-3), 2),
                       "hbm_gbs": round(d1["step_bytes"] / (ms1 * 1e-3) / 1e9, 1)},
     }
+    res["decode_exact"] = exact
+    if router is not None:
+        res["router"] = router
     if peaks is not None:
         res["peaks"] = peaks
         res["roofline"]["frac_of_measured_read"] = round(gu_gbs / peaks["hbm_read_gbs"], 4)

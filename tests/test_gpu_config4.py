@@ -167,3 +167,104 @@ def test_capacity_limited_cache_at_benchmark_shape(dev, monkeypatch):
          exl3.FAT_EXPERT_THRESHOLD) = saved[:5]
         exl3._DMA_STATE.clear()
         exl3._DMA_STATE.update(saved[5])
+
+
+def _host_picks():
+    """The picks of the last published host job: (layer, [(token, expert)]), read from the pinned mailbox."""
+    from mi355moe import ct_vllm
+    S = ct_vllm.S
+    mail = S["mail"]
+    ctrl = mail.array(np.int64, (16,), 0)
+    picks = mail.array(np.int32, (S["maxpicks"], 3), S["picks"] - mail.ptr)
+    n = int(ctrl[4])
+    return int(ctrl[2]), [(int(t), int(e)) for t, e in picks[:n, :2]]
+
+
+def test_capacity_limited_cache_with_host_tier_past_drift(dev, monkeypatch):
+    """The capacity-limited cache with the host tier serving the split's share of the misses (the benchmark's
+    default), for 80 decode steps: past the ranking drift at step 64 and the replan after it. Every replan equals
+    the oracle planner and leaves the tables equal to the residency; layer 0's output at steps 20 and 70, whose
+    host share the tier computed from the pinned home rows, matches the oracle (GPU picks with fp16 weights, host
+    picks with fp32 weights)."""
+    import torch
+    from mi355moe import cache, ct_vllm, exl3, workload
+    from mi355moe import tier as host_tier
+    from mi355moe.hostmem import HostBuffer
+    from mi355moe.store import ExpertStore
+
+    H, I, E, K, T, L, NH, SLOTS = 4096, 2048, 384, 8, 4, 40, 4, 709
+    env = {"DSV41_CT_LAYERS": str(L), "DSV41_EC_SLOTS": str(SLOTS), "DSV41_EC_EVERY": "16", "DSV41_EC_ADMIT": "48",
+           "DSV41_EC_DECAY": "0.9", "DSV41_EC_HYST": "1.0", "DSV41_EC_WARMUP": "16", "DSV41_EC_ASYNC": "1",
+           "DSV41_EC_PREFILL_TOKENS": "512", "DSV41_EC_REWARM_AFTER": "4", "DSV41_EC_ELASTIC": "1",
+           "DSV41_EC_MARGIN_MB": "1500", "DSV41_CPU_TIER": "1", "DSV41_CT_FORCE_N": "6", "DSV41_CT_THREADS": "8"}
+    for k, v in env.items():
+        monkeypatch.setenv(k, v)
+    ct_vllm.reset()
+    try:
+        rows = cache.ExpertRows(H, I)
+        bufs = [HostBuffer(E * rows.row_bytes) for _ in range(NH)]
+        ct_vllm.install(exl3)
+        method = exl3.Exl3MoEMethod()
+        stores = []
+        for l in range(L):
+            st = ExpertStore(E, H, I, device=dev, limit=10.0, host_home=cache.HostHome(E, H, I, buffer=bufs[l % NH]))
+            st.synthesize(1000 + l, trellis=l < NH)
+            method.process_weights_after_loading(st)
+            stores.append(st)
+        hbm0 = ExpertStore(E, H, I, device=dev, limit=10.0).synthesize(1000)
+        torch.cuda.synchronize()
+        c = ct_vllm.EC["cache"]
+        assert c is not None and ct_vllm.S["started"] and ct_vllm.S["cpu_tier"] and host_tier.serving()
+        print(f"config-4 cache with the host tier: self-test {ct_vllm.S['selftest']}", flush=True)
+        assert ct_vllm.S["selftest"]["max_rel_vs_gpu"] < 2e-2
+        oracle = OracleLayer(hbm0, 1000, cache=False)
+        rng = np.random.default_rng(2000)
+        chk = np.random.default_rng(1)
+        perms = [np.random.default_rng(2000 + l).permutation(E) for l in range(L)]
+        x = _t(workload.activations(T, H, seed=7), dev).to(torch.bfloat16)
+        x16 = x.half().cpu().numpy().astype(np.float32)
+        ec = None
+        replans = 0
+        for step in range(80):
+            if step % 64 == 0 and step:
+                for l in range(L):
+                    perms[l] = workload.drift(perms[l], rng)
+            routes = [workload.zipf_ids(T, K, E, rng, perms[l]) for l in range(L)]
+            ct_vllm.before_step(T)
+            for l in range(L):
+                ids, w = _t(routes[l][0], dev), _t(routes[l][1], dev)
+                out = exl3.apply_exl3_fused_moe(x, ids, w, stores[l], None, None, 10.0)
+                if l == 0 and step in (20, 70):
+                    torch.cuda.synchronize()
+                    li, hp = _host_picks()
+                    assert li == 0 and hp, f"step {step}: no host share on layer 0"
+                    host = np.zeros((T, K), bool)
+                    rid, rw = routes[0]
+                    for t, e in hp:
+                        host[t] |= rid[t] == e
+                    ref = oracle.forward(x16, rid, np.where(host, rw, rw.astype(np.float16).astype(np.float32)))
+                    ok, m = within_tolerance(out.cpu().numpy(), ref)
+                    print(f"step {step}: layer 0 with {len(hp)} host picks vs oracle {m}", flush=True)
+                    assert ok, m
+            replan = not c.released and (c.step_no + 1) % c.every == 0 and c.step_no + 1 >= c.warmup
+            counts = torch.stack([s.counts for s in stores]).cpu().numpy().copy() if replan else None
+            ct_vllm.ec_step()
+            torch.cuda.synchronize()
+            if replan:
+                if ec is None:
+                    ec = ECOracle(L, E, c.N, admit=48, decay=0.9, hyst=1.0)
+                ec.step(counts)
+                assert [(i, s) for i, s in c.where.items()] == ec.resident
+                assert c.free == ec.free and np.array_equal(c.score.reshape(-1), np.array(ec.score))
+                _check_placement(c, stores, bufs, NH, chk)
+                replans += 1
+                print(f"step {step}: replan {replans} checked, {len(c.where)} resident, "
+                      f"{ct_vllm.summary()['hit_rate']} hit rate", flush=True)
+        s = ct_vllm.summary()
+        hs = host_tier.stats()
+        print(f"summary {s}, tier {hs}", flush=True)
+        assert replans == 5 and c.admits == 240
+        assert s["timeouts"] == 0 and s["cpu_experts"] > 0 and hs["rejected"] == 0
+    finally:
+        ct_vllm.uninstall(exl3)
+        ct_vllm.reset()

@@ -217,3 +217,40 @@ def test_router_ties_pick_the_lower_expert(dev):
             assert list(gi[t]) == want, (t, list(gi[t]), want)
             z = np.exp(lg[t, want].astype(np.float64) - lg[t, want].max())
             assert np.allclose(gw[t], z / z.sum(), rtol=1e-5, atol=1e-6)
+
+
+def test_router_at_prefill_size(dev):
+    """The router at T = 16,384 (the prefill chunk): on 256 sampled rows the logits and picks equal the oracle's
+    (as at decode sizes); on every row the picks are k distinct experts in descending logit order whose logits
+    are at least the row's (k+1)-th largest, and the weights are the softmax of the picked logits."""
+    import torch
+    from mi355moe import _lib, workload
+    T, H, E, k = 16384, 4096, 384, 8
+    x = workload.activations(T, H, seed=16384)
+    G = np.random.default_rng(5).normal(0, 0.02, (E, H)).astype(np.float32)
+    xb = _t((x.view(np.uint32) >> 16).astype(np.uint16), dev)
+    Gd = _t(G, dev)
+    ids = torch.empty((T, k), dtype=torch.int64, device=dev)
+    w = torch.empty((T, k), dtype=torch.float32, device=dev)
+    logits = torch.empty((T, E), dtype=torch.float32, device=dev)
+    print(f"router T={T}", flush=True)
+    _lib.call("mm_router_topk", xb.data_ptr(), T, H, Gd.data_ptr(), E, k, logits.data_ptr(), ids.data_ptr(), w.data_ptr(),
+              _lib.stream_ptr())
+    torch.cuda.synchronize()
+    sel = logits.gather(1, ids)
+    kth = logits.topk(k + 1, dim=1).values[:, k:k + 1]
+    assert bool((ids >= 0).all()) and bool((ids < E).all())
+    assert bool((ids.sort(dim=1).values.diff(dim=1) > 0).all()), "picks not distinct"
+    assert bool((sel >= kth).all()), "a pick below the row's top k"
+    assert bool((sel[:, :-1] >= sel[:, 1:]).all()), "picks not in descending logit order"
+    assert torch.allclose(w, torch.softmax(sel.double(), dim=1).float(), rtol=1e-5, atol=1e-6)
+    rows = np.sort(np.random.default_rng(1).choice(T, 256, replace=False))
+    # the oracle's inputs are the bf16 values the kernel reads
+    xs = (x[rows].view(np.uint32) & 0xFFFF0000).view(np.float32)
+    rid, rw, rl = O.router(xs, G, k)
+    lg, gi = logits.cpu().numpy()[rows], ids.cpu().numpy()[rows]
+    assert np.allclose(lg, rl, rtol=0, atol=5e-5)
+    for t in range(rows.size):
+        if not np.array_equal(gi[t], rid[t]):
+            srt = np.sort(rl[t])[::-1]
+            assert np.min(np.abs(np.diff(srt[: k + 1]))) < 1e-5, t
