@@ -641,7 +641,8 @@ def bench_cache(args):
                        "DSV41_EC_ADMIT": "48", "DSV41_EC_DECAY": "0.9", "DSV41_EC_HYST": "1.0",
                        "DSV41_EC_WARMUP": str(args.ec_warmup), "DSV41_EC_ASYNC": "1",
                        "DSV41_EC_PREFILL_TOKENS": "512", "DSV41_EC_REWARM_AFTER": "4", "DSV41_EC_ELASTIC": "1",
-                       "DSV41_EC_MARGIN_MB": "1500", "DSV41_CPU_TIER": "1" if args.cpu_tier else "0"})
+                       "DSV41_EC_MARGIN_MB": "1500", "DSV41_CPU_TIER": "1" if args.cpu_tier else "0",
+                       "DSV41_CT_HYB_MAX": str(args.hyb_tokens) if args.cpu_tier else "0"})
     exl3._EXL3_HOST_DMA_MODE, exl3._DMA_B, exl3._DMA_NS, exl3._DMA_MIN_TOKENS = 1, 8, 8, 513
     exl3.FAT_EXPERT_THRESHOLD = 32
     rows = cache.ExpertRows(H, I)
@@ -744,6 +745,36 @@ def bench_cache(args):
             log(f"cache: step {step}/{total_steps} decode {dt * 1e3:.1f} ms {ct_vllm.summary()}")
     total_s = time.perf_counter() - t_all
     st = ct_vllm.S["stats"].tolist()
+    # a lone prefill step of hyb_tokens tokens (every layer's experts staged: the cache is released first), with
+    # the host tier taking each layer's trailing staging batches (the hybrid tail) and without it
+    hybrid = None
+    if args.cpu_tier and args.hyb_tokens > 0:
+        TH = args.hyb_tokens
+        hr = workload.zipf_ids(TH, K, E, np.random.default_rng(4000), np.arange(E))
+        xh = torch.from_numpy(np.random.default_rng(4001).normal(0, 1, (TH, H)).astype(np.float32)).to(dev).to(torch.bfloat16)
+        hid, hw = torch.from_numpy(hr[0]).to(dev), torch.from_numpy(hr[1]).to(dev)
+        perm_d = [torch.from_numpy(p).to(dev) for p in perms]
+        hybrid = {"tokens": TH, "runs": []}
+        for rep, use in enumerate((True, False, True, False)):
+            ct_vllm.S["hyb_max"] = TH if use else 0
+            ct_vllm.before_step(TH, solo=True)
+            tail0 = sum(int(s_._exl3_dma.get("tail_skipped", 0)) for s_ in stores)
+            torch.cuda.synchronize()
+            ts = time.perf_counter()
+            run_layers(xh, lambda l: (perm_d[l][hid], hw), TH)
+            torch.cuda.synchronize()
+            dt = time.perf_counter() - ts
+            ct_vllm.ec_step()
+            tail = sum(int(s_._exl3_dma.get("tail_skipped", 0)) for s_ in stores) - tail0
+            hybrid["runs"].append({"host_tail": use, "s": round(dt, 3), "tok_s": round(TH / dt, 1),
+                                   "tail_batches": tail})
+            log(f"cache: {TH}-token chunk, host tail {use}: {dt:.3f}s, {tail} tail batches over {L} layers")
+        ct_vllm.S["hyb_max"] = TH
+        w_ = [r["s"] for r in hybrid["runs"] if r["host_tail"]]
+        wo_ = [r["s"] for r in hybrid["runs"] if not r["host_tail"]]
+        hybrid.update(s_with_tail=round(min(w_), 3), s_without_tail=round(min(wo_), 3),
+                      speedup=round(min(wo_) / min(w_), 3), cost=dict(ct_vllm.S["hyb_cost"]),
+                      summary=ct_vllm.summary()["hybrid"])
     if hit0 is None:                      # every step was a warm-up step
         hit0 = st
     hits, misses = st[0] - hit0[0], st[1] - hit0[1]
@@ -769,7 +800,7 @@ def bench_cache(args):
                            max(stats["decode_s"] + stats["prefill_s"], 1e-9), 2),
         "prefill_chunks": stats["prefill_chunks"], "prefill_s": round(stats["prefill_s"], 3),
         "cpu_tier": bool(args.cpu_tier), "host_experts": summ["cpu_experts"], "host_jobs": summ["host_jobs"],
-        "host_timeouts": summ["timeouts"], "policy": policy,
+        "host_timeouts": summ["timeouts"], "policy": policy, "hybrid_prefill": hybrid,
         "ec": ct_vllm.ec_summary(), "wall_s": round(total_s, 1),
     }
     ct_vllm.uninstall(exl3)
@@ -814,6 +845,9 @@ def main():
                     help="cache leg: every decode miss read over PCIe by the GPU (default: the host tier serves the "
                          "share of the misses the split's cost model gives it, as the reference serves this "
                          "configuration)")
+    ap.add_argument("--hyb-tokens", type=int, default=2048,
+                    help="cache leg: the lone prefill step timed with and without the host tier's tail batches "
+                         "(DSV41_CT_HYB_MAX; 0 = not timed)")
     ap.add_argument("--cpu-child", default=None, help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_child is not None:

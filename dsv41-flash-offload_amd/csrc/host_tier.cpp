@@ -256,50 +256,46 @@ struct Rows
     Rows at(int t) const { return { xt + t * xstride, xstride, xs + t * sstride, sstride, y + t * ystride, ystride }; }
 };
 
-// y[t][0..127] (raw sums, before the output transform) of column block cb of matrix m for MT tokens. EXACT:
-// fp16-rounded weights; else the centred AFFINE codes.
-template <int MT, bool EXACT>
-static void gemv_block(const Mat& m, int cb, const Rows& R)
+// The decode constants of one GEMV.
+struct DecodeConsts
 {
-    const int NT = m.N / 16, KT = m.K / 16;
-    const __m512i vmask = _mm512_set1_epi32(0xffff), vmul = _mm512_set1_epi32((int)MUL1);
-    const __m512i vones = _mm512_set1_epi8(1);
-    const __m512i vbase = _mm512_set1_epi32(EXACT ? 1024 : 1024 - CENTER);
-    const __m512 vkinv = _mm512_set1_ps(kinv()), vkbias = _mm512_set1_ps(kbias());
-    __m512 acc[MT][8];
-    for (int t = 0; t < MT; ++t)
-        for (int j = 0; j < 8; ++j) acc[t][j] = _mm512_setzero_ps();
-    const uint8_t* base = m.tr + (size_t)cb * 8 * TILE_BYTES;
-    const Tables& TAB = tab();
-    for (int tk = 0; tk < KT; ++tk)
+    __m512i vmask, vmul, vones, vbase;
+    __m512 vkinv, vkbias;
+    template <bool EXACT>
+    static DecodeConsts make()
     {
-        const uint8_t* row = base + (size_t)tk * NT * TILE_BYTES;
-        if (tk + 4 < KT)
-        {
-            const uint8_t* pf = row + (size_t)4 * NT * TILE_BYTES;
-            for (int o = 0; o < 8 * TILE_BYTES; o += 64) _mm_prefetch((const char*)(pf + o), _MM_HINT_T0);
-        }
-        for (int j = 0; j < 8; ++j)
-        {
-            const uint8_t* tile = row + j * TILE_BYTES;
-            const __m512i wa = _mm512_loadu_si512(tile);
-            const __m512i wb = _mm512_castsi256_si512(_mm256_loadu_si256((const __m256i*)(tile + 64)));
-            for (int r = 0; r < 16; ++r)
-            {
-                const __m512i lo = _mm512_permutex2var_epi32(wa, _mm512_load_si512(TAB.lo[r]), wb);
-                const __m512i hi = _mm512_permutex2var_epi32(wa, _mm512_load_si512(TAB.hi[r]), wb);
-                const __m512i st = _mm512_and_si512(_mm512_shrdv_epi32(lo, hi, _mm512_load_si512(TAB.sh[r])), vmask);
-                const __m512i p = _mm512_mullo_epi32(st, vmul);
-                const __m512i code = _mm512_dpbusd_epi32(vbase, p, vones);
-                __m512 w = _mm512_cvtepi32_ps(code);
-                if constexpr (EXACT)
-                    w = _mm512_cvtph_ps(_mm512_cvtps_ph(_mm512_fmadd_ps(w, vkinv, vkbias),
-                                                        _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
-                const int k = tk * 16 + r;
-                for (int t = 0; t < MT; ++t) acc[t][j] = _mm512_fmadd_ps(_mm512_set1_ps(R.xt[t * R.xstride + k]), w, acc[t][j]);
-            }
-        }
+        return { _mm512_set1_epi32(0xffff), _mm512_set1_epi32((int)MUL1), _mm512_set1_epi8(1),
+                 _mm512_set1_epi32(EXACT ? 1024 : 1024 - CENTER), _mm512_set1_ps(kinv()), _mm512_set1_ps(kbias()) };
     }
+};
+
+// Weights of row r, columns 0 .. 15 of the tile held in wa (dwords 0 .. 15) and wb (dwords 16 .. 23). EXACT:
+// fp16-rounded weights; else the centred AFFINE codes.
+template <bool EXACT>
+static inline __m512 decode_row(__m512i wa, __m512i wb, int r, const Tables& TAB, const DecodeConsts& C)
+{
+    const __m512i lo = _mm512_permutex2var_epi32(wa, _mm512_load_si512(TAB.lo[r]), wb);
+    const __m512i hi = _mm512_permutex2var_epi32(wa, _mm512_load_si512(TAB.hi[r]), wb);
+    const __m512i st = _mm512_and_si512(_mm512_shrdv_epi32(lo, hi, _mm512_load_si512(TAB.sh[r])), C.vmask);
+    const __m512i p = _mm512_mullo_epi32(st, C.vmul);
+    const __m512i code = _mm512_dpbusd_epi32(C.vbase, p, C.vones);
+    __m512 w = _mm512_cvtepi32_ps(code);
+    if constexpr (EXACT)
+        w = _mm512_cvtph_ps(_mm512_cvtps_ph(_mm512_fmadd_ps(w, C.vkinv, C.vkbias),
+                                            _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+    return w;
+}
+
+static inline void prefetch_rows(const uint8_t* row)
+{
+    for (int o = 0; o < 8 * TILE_BYTES; o += 64) _mm_prefetch((const char*)(row + o), _MM_HINT_T0);
+}
+
+// The raw sums of MT tokens (in registers) -> y rows: EXACT as they are, AFFINE fixed up per output.
+template <int MT, bool EXACT>
+static inline void store_rows(__m512 (&acc)[MT][8], const Rows& R)
+{
+    const __m512 vkinv = _mm512_set1_ps(kinv());
     for (int t = 0; t < MT; ++t)
     {
         if constexpr (EXACT)
@@ -314,9 +310,125 @@ static void gemv_block(const Mat& m, int cb, const Rows& R)
     }
 }
 
+// y[t][0..127] (raw sums, before the output transform) of column block cb of matrix m for MT tokens, each
+// weight decoded in registers and used at once.
+template <int MT, bool EXACT>
+static void gemv_block(const Mat& m, int cb, const Rows& R)
+{
+    const int NT = m.N / 16, KT = m.K / 16;
+    const DecodeConsts C = DecodeConsts::make<EXACT>();
+    __m512 acc[MT][8];
+    for (int t = 0; t < MT; ++t)
+        for (int j = 0; j < 8; ++j) acc[t][j] = _mm512_setzero_ps();
+    const uint8_t* base = m.tr + (size_t)cb * 8 * TILE_BYTES;
+    const Tables& TAB = tab();
+    for (int tk = 0; tk < KT; ++tk)
+    {
+        const uint8_t* row = base + (size_t)tk * NT * TILE_BYTES;
+        if (tk + 4 < KT) prefetch_rows(row + (size_t)4 * NT * TILE_BYTES);
+        for (int j = 0; j < 8; ++j)
+        {
+            const uint8_t* tile = row + j * TILE_BYTES;
+            const __m512i wa = _mm512_loadu_si512(tile);
+            const __m512i wb = _mm512_castsi256_si512(_mm256_loadu_si256((const __m256i*)(tile + 64)));
+            for (int r = 0; r < 16; ++r)
+            {
+                const __m512 w = decode_row<EXACT>(wa, wb, r, TAB, C);
+                const int k = tk * 16 + r;
+                for (int t = 0; t < MT; ++t) acc[t][j] = _mm512_fmadd_ps(_mm512_set1_ps(R.xt[t * R.xstride + k]), w, acc[t][j]);
+            }
+        }
+    }
+    store_rows<MT, EXACT>(acc, R);
+}
+
+// The same sums for any number of tokens (an expert with many rows, as a prefill tail job has): the weights of
+// CHUNK_TR tile rows are decoded once into an L1 buffer, then every group of up to MAX_MT tokens runs over the
+// chunk with its sums in registers, kept between chunks in a per-thread buffer. Each output's fma chain runs in
+// ascending k as in gemv_block, so the results are bit-identical to it.
+constexpr int CHUNK_TR = 2;
+
+template <int MT, bool EXACT>
+static inline void chunk_pass(const float* W, int k0, float* accbuf, const Rows& R)
+{
+    __m512 acc[MT][8];
+    for (int t = 0; t < MT; ++t)
+        for (int j = 0; j < 8; ++j) acc[t][j] = _mm512_load_ps(accbuf + t * 128 + 16 * j);
+    for (int k = 0; k < CHUNK_TR * 16; ++k)
+    {
+        __m512 xb[MT];
+        for (int t = 0; t < MT; ++t) xb[t] = _mm512_set1_ps(R.xt[t * R.xstride + k0 + k]);
+        for (int j = 0; j < 8; ++j)
+        {
+            const __m512 w = _mm512_load_ps(W + k * 128 + 16 * j);
+            for (int t = 0; t < MT; ++t) acc[t][j] = _mm512_fmadd_ps(xb[t], w, acc[t][j]);
+        }
+    }
+    for (int t = 0; t < MT; ++t)
+        for (int j = 0; j < 8; ++j) _mm512_store_ps(accbuf + t * 128 + 16 * j, acc[t][j]);
+}
+
+template <bool EXACT>
+static void gemv_many(const Mat& m, int cb, int nt, const Rows& R)
+{
+    thread_local std::vector<float> accv;
+    alignas(64) static thread_local float W[CHUNK_TR * 16 * 128];
+    const size_t need = (size_t)((nt + MAX_MT - 1) / MAX_MT) * MAX_MT * 128;
+    if (accv.size() < need + 16) accv.resize(need + 16);
+    float* accbuf = reinterpret_cast<float*>(((uintptr_t)accv.data() + 63) & ~(uintptr_t)63);
+    memset(accbuf, 0, need * sizeof(float));
+    const int NT = m.N / 16, KT = m.K / 16;
+    const DecodeConsts C = DecodeConsts::make<EXACT>();
+    const uint8_t* base = m.tr + (size_t)cb * 8 * TILE_BYTES;
+    const Tables& TAB = tab();
+    for (int tk0 = 0; tk0 < KT; tk0 += CHUNK_TR)
+    {
+        for (int q = 0; q < CHUNK_TR; ++q)
+        {
+            const uint8_t* row = base + (size_t)(tk0 + q) * NT * TILE_BYTES;
+            if (tk0 + q + 4 < KT) prefetch_rows(row + (size_t)4 * NT * TILE_BYTES);
+            for (int j = 0; j < 8; ++j)
+            {
+                const uint8_t* tile = row + j * TILE_BYTES;
+                const __m512i wa = _mm512_loadu_si512(tile);
+                const __m512i wb = _mm512_castsi256_si512(_mm256_loadu_si256((const __m256i*)(tile + 64)));
+                for (int r = 0; r < 16; ++r) _mm512_store_ps(W + (q * 16 + r) * 128 + 16 * j, decode_row<EXACT>(wa, wb, r, TAB, C));
+            }
+        }
+        const int k0 = tk0 * 16;
+        for (int t0 = 0; t0 < nt; t0 += MAX_MT)
+        {
+            const int mt = nt - t0 < MAX_MT ? nt - t0 : MAX_MT;
+            float* ab = accbuf + (size_t)t0 * 128;
+            if (mt == 3) chunk_pass<3, EXACT>(W, k0, ab, R.at(t0));
+            else if (mt == 2) chunk_pass<2, EXACT>(W, k0, ab, R.at(t0));
+            else chunk_pass<1, EXACT>(W, k0, ab, R.at(t0));
+        }
+    }
+    for (int t0 = 0; t0 < nt; t0 += MAX_MT)
+    {
+        const int mt = nt - t0 < MAX_MT ? nt - t0 : MAX_MT;
+        __m512 acc[MAX_MT][8];
+        for (int t = 0; t < mt; ++t)
+            for (int j = 0; j < 8; ++j) acc[t][j] = _mm512_load_ps(accbuf + (size_t)(t0 + t) * 128 + 16 * j);
+        if (mt == 3) store_rows<3, EXACT>(acc, R.at(t0));
+        else if (mt == 2) store_rows<2, EXACT>(reinterpret_cast<__m512(&)[2][8]>(acc), R.at(t0));
+        else store_rows<1, EXACT>(reinterpret_cast<__m512(&)[1][8]>(acc), R.at(t0));
+    }
+}
+
+// Tokens past MANY_MIN take the chunked path (one decode for all of them); fewer run gemv_block, decoding per
+// group of MAX_MT.
+constexpr int MANY_MIN = 4;
+
 template <bool EXACT>
 static void gemv_tokens(const Mat& m, int cb, int nt, const Rows& R)
 {
+    if (nt >= MANY_MIN)
+    {
+        gemv_many<EXACT>(m, cb, nt, R);
+        return;
+    }
     for (int t0 = 0; t0 < nt; t0 += MAX_MT)
     {
         const int mt = nt - t0 < MAX_MT ? nt - t0 : MAX_MT;

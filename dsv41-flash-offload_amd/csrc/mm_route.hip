@@ -110,6 +110,53 @@ __global__ __launch_bounds__(256) void k_router_logits(const uint16_t* __restric
         }
 }
 
+// Decode-sized router logits: one wave per expert streams its gate row (16-byte loads) against up to RT_TB tokens
+// at a time (8-byte bf16 loads; the rows of a few tokens stay in L2 for every wave), lane partials in fp32, then a
+// wave sum. A launch of 64 x 64 tiles would give a 4-token call only E / 64 workgroups.
+constexpr int RT_TB = 16;
+constexpr int RT_MAX_T = 64;
+
+__global__ __launch_bounds__(256) void k_router_gemv(const uint16_t* __restrict__ x, const float* __restrict__ G,
+                                                     float* __restrict__ logits, int T, int H, int E)
+{
+    const int lane = threadIdx.x & 63;
+    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int t0 = blockIdx.y * RT_TB;
+    if (e >= E) return;                                    // the whole wave
+    const int nt = min(RT_TB, T - t0);
+    float acc[RT_TB];
+#pragma unroll
+    for (int t = 0; t < RT_TB; ++t) acc[t] = 0.0f;
+    const float4* g = reinterpret_cast<const float4*>(G + (size_t)e * H);
+    auto bf = [](uint32_t b) { return __builtin_bit_cast(float, b << 16); };
+    for (int h = lane * 4; h < H; h += 256)
+    {
+        const float4 gv = g[h >> 2];
+#pragma unroll
+        for (int t = 0; t < RT_TB; ++t)
+            if (t < nt)
+            {
+                const uint2 xr = *reinterpret_cast<const uint2*>(x + (size_t)(t0 + t) * H + h);
+                acc[t] = fmaf(bf(xr.x & 0xffffu), gv.x, acc[t]);
+                acc[t] = fmaf(bf(xr.x >> 16), gv.y, acc[t]);
+                acc[t] = fmaf(bf(xr.y & 0xffffu), gv.z, acc[t]);
+                acc[t] = fmaf(bf(xr.y >> 16), gv.w, acc[t]);
+            }
+    }
+#pragma unroll
+    for (int t = 0; t < RT_TB; ++t)
+    {
+        float v = acc[t];
+        v += xor_lane<32>(v);
+        v += xor_lane<16>(v);
+        v += xor_lane<8>(v);
+        v += xor_lane<4>(v);
+        v += xor_lane<2>(v);
+        v += xor_lane<1>(v);
+        if (lane == 0 && t < nt) logits[(size_t)(t0 + t) * E + e] = v;
+    }
+}
+
 // One wave per token: k rounds of a wave-wide argmax (ties to the lower index), then softmax over the picks.
 __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int T, int E, int k,
                                                      int64_t* __restrict__ ids, float* __restrict__ w)
@@ -732,8 +779,12 @@ int mm_router_topk(const void* x_bf16, int T, int H, const float* gate, int E, i
     MM_CHECK_ARG(E > 0 && E <= 1024 && k > 0 && k <= 32 && k <= E, "mm_router_topk: need 0 < k <= 32, k <= E <= 1024");
     MM_CHECK_ARG(x_bf16 && gate && ids && w && logits, "mm_router_topk: null pointer (logits workspace is required)");
     if (T == 0) return MM_OK;
-    dim3 g1((E + 63) / 64, (T + 63) / 64);
-    hipLaunchKernelGGL(k_router_logits, g1, dim3(256), 0, S(stream), (const uint16_t*)x_bf16, gate, logits, T, H, E);
+    if (T <= RT_MAX_T && H % 256 == 0 && ((uintptr_t)x_bf16 & 7) == 0 && ((uintptr_t)gate & 15) == 0)
+        hipLaunchKernelGGL(k_router_gemv, dim3((E + 3) / 4, (T + RT_TB - 1) / RT_TB), dim3(256), 0, S(stream),
+                           (const uint16_t*)x_bf16, gate, logits, T, H, E);
+    else
+        hipLaunchKernelGGL(k_router_logits, dim3((E + 63) / 64, (T + 63) / 64), dim3(256), 0, S(stream),
+                           (const uint16_t*)x_bf16, gate, logits, T, H, E);
     hipLaunchKernelGGL(k_router_topk, dim3((T + 3) / 4), dim3(256), 0, S(stream), logits, T, E, k, ids, w);
     return check_launch("mm_router_topk");
 }

@@ -24,6 +24,13 @@ to the host: the split's cost model (ct/ft_tier_cu_v.cu:35-62) chooses how many 
 cores compute from their pinned home rows while the GPU reads the rest zero-copy over PCIe and computes its
 share; the combine then adds the host partial (bounded wait, DSV41_CT_TIMEOUT_S). Without it the policy's
 force_n is 0 and every routed expert runs on the GPU.
+
+Hybrid prefill tail (ct/ct_vllm.py:163-225; DSV41_CT_HYB_MAX, 0 = off): a lone step of maxbsz < T <= HYB_MAX
+tokens on a layer with staged experts gives the host tier the trailing staging batches (_hyb_tail's cost model:
+host time per expert against copy time per expert), so the copy engine streams fewer experts while the host
+cores compute the tail: the split marks the tail experts as misses (a slot table with -1 for them only) and
+sends every one of their picks to the host, the staged prefill skips those batches, and the combine adds the
+host partial.
 """
 import importlib
 import json
@@ -49,12 +56,14 @@ def _init(layer):
     dev = layer._exl3_ptrs["gate_trellis"].device
     H = layer.H
     maxbsz = int(os.environ.get("DSV41_CT_MAXBSZ", "32"))
-    S.update(H=H, I=layer.I, dev=dev, maxbsz=maxbsz, maxpicks=8 * maxbsz)
-    # host mailbox (ct_vllm.py:62-65), pinned and device-mapped: ctrl int64 [16] | hx fp16 [maxbsz * H] |
-    # picks int32 [maxpicks * 3] | hout fp32 [maxbsz * H] (the host worker's partial, read by mm_combine_host)
-    o_hx, o_pk = 128, 128 + maxbsz * H * 2
+    hyb = int(os.environ.get("DSV41_CT_HYB_MAX", "0"))        # hybrid DMA + host-tail range (maxbsz, hyb]; 0 = off
+    buf = max(maxbsz, hyb)
+    S.update(H=H, I=layer.I, dev=dev, maxbsz=maxbsz, maxpicks=8 * buf, hyb_max=hyb, buf=buf)
+    # host mailbox (ct_vllm.py:58-65), pinned and device-mapped: ctrl int64 [16] | hx fp16 [buf * H] |
+    # picks int32 [maxpicks * 3] | hout fp32 [buf * H] (the host worker's partial, read by mm_combine_host)
+    o_hx, o_pk = 128, 128 + buf * H * 2
     o_out = (o_pk + S["maxpicks"] * 12 + 255) // 256 * 256
-    S["mail"] = HostBuffer(o_out + maxbsz * H * 4)
+    S["mail"] = HostBuffer(o_out + buf * H * 4)
     S["mail"].array(np.uint8)[:] = 0
     S["ctrl"] = S["mail"].data_ptr(0)
     S["hx"] = S["mail"].data_ptr(o_hx)
@@ -69,13 +78,20 @@ def _init(layer):
     S["pol"] = torch.tensor([_f("DSV41_CT_TZC", 0.58), _f("DSV41_CT_THIT", 0.03), _f("DSV41_CT_A", 0.11),
                              _f("DSV41_CT_B", 0.16), _f("DSV41_CT_TOK", 0.2), _f("DSV41_CT_MAXN", 64), force, 0.0, 0.0],
                             dtype=torch.float32, device=dev)
+    # hybrid: every miss to the host (force_n = all), and the x rows copied by the copy engine (ct_vllm.py:75-78);
+    # the "misses" are exactly the tail experts (the tail's slot table)
+    S["pol_hyb"] = torch.tensor([0.54, 0.0, 0.0, 0.0, 0.0, 4096.0, 4096.0, 0.0, 1.0], dtype=torch.float32, device=dev)
+    S["stats_hyb"] = torch.zeros(8, dtype=torch.int64, device=dev)
+    S["hyb_n"] = 0
+    S["hyb_cost"] = {"c0": _f("DSV41_HYB_C0", 0.24), "c1": _f("DSV41_HYB_C1", 0.085), "dma": _f("DSV41_HYB_DMA", 0.54),
+                     "tok_us": _f("DSV41_HYB_TOK_US", 6.0), "max_batches": int(_f("DSV41_HYB_MAX_BATCHES", 24))}
     S["timeout_ns"] = int(_f("DSV41_CT_TIMEOUT_S", 2) * 1e9)
     S["sel"] = torch.empty(S["maxpicks"], dtype=torch.long, device=dev)
     S["w"] = torch.empty(S["maxpicks"], dtype=torch.float32, device=dev)
     S["nlayers"] = int(os.environ.get("DSV41_CT_LAYERS", "40"))
     if S["cpu_tier"]:
         _tier.init(H, layer.I, S["nlayers"], mailbox={"ctrl": S["ctrl"], "hx": S["hx"], "picks": S["picks"],
-                                                        "hout": S["hout"], "maxtok": S["maxbsz"],
+                                                        "hout": S["hout"], "maxtok": buf,
                                                         "maxpicks": S["maxpicks"], "owner": S["mail"]})
         S["limit"] = _f("DSV41_CT_LIMIT", 10.0)
         _tier.set_limit(S["limit"] if S["limit"] > 0 else 0.0)
@@ -175,19 +191,64 @@ def calibrate(layer=None, experts=8):
             ts.append(time.perf_counter() - t0)
         return float(np.median(ts[3:])) * 1e3
 
+    def cpu_rows_t(rows):
+        # `rows` tokens, each routed to every one of the experts: ms per expert
+        sel = np.tile(np.array(cold, np.int32), (rows, 1))
+        ww = np.full(sel.shape, 1.0 / len(cold), np.float32)
+        xf = (torch.randn(rows, S["H"]) * 0.35).half().float().numpy()
+        ts = []
+        for r in range(5):
+            t0 = time.perf_counter()
+            _tier.forward(layer._ct["li"], xf, sel, ww)
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts[1:])) * 1e3 / len(cold)
+
+    def cpu_tok_t(T):
+        # the per-token part of a job (every output row written) with no picks: ms per token
+        sel = np.full((T, 1), -1, np.int32)
+        xf = np.zeros((T, S["H"]), np.float32)
+        ts = []
+        for r in range(5):
+            t0 = time.perf_counter()
+            _tier.forward(layer._ct["li"], xf, sel, np.zeros((T, 1), np.float32))
+            ts.append(time.perf_counter() - t0)
+        return float(np.median(ts[1:])) * 1e3 / T
+
     zc = gpu_t(cold) / len(cold)
     serving = _tier.serving()
     if serving:                     # synchronous host forwards need the mailbox worker stopped
         _tier.stop()
     try:
         c1, cn = cpu_t(cold[:1]), cpu_t(cold)
+        hyb = S.get("hyb_max", 0) > 0
+        if hyb:
+            r1, rr = cpu_rows_t(1), cpu_rows_t(32)
+            tok = cpu_tok_t(2048)
     finally:
         if serving:
             _tier.start()
     b = max((cn - c1) / max(1, len(cold) - 1), 1e-3)
     a = max(c1 - b, 0.0)
     set_policy(tzc=zc, thit=zc / 400.0, a=a, b=b)
-    return {"tzc": zc, "thit": zc / 400.0, "a": a, "b": b}
+    res = {"tzc": zc, "thit": zc / 400.0, "a": a, "b": b}
+    if hyb:
+        # copy time of one expert row through the staging copy stream (pinned home -> HBM)
+        rows_b = cache.ExpertRows(S["H"], S["I"]).row_bytes
+        dst = torch.empty(len(cold) * rows_b, dtype=torch.uint8, device=S["dev"])
+        cs = _lib.copy_stream(S["dev"], _lib.COPY_STAGING)
+        copies = [(dst.data_ptr() + i * rows_b, layer.host_home.row(e), rows_b) for i, e in enumerate(cold)]
+        cache.stage_copy(copies, cs)
+        cs.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(cs)
+        cache.stage_copy(copies, cs)
+        e1.record(cs)
+        cs.synchronize()
+        dma = e0.elapsed_time(e1) / len(cold)
+        del dst
+        S["hyb_cost"].update(c0=r1, c1=max((rr - r1) / 31.0, 0.0), dma=dma, tok_us=tok * 1e3)
+        res["hybrid"] = dict(S["hyb_cost"])
+    return res
 
 
 def start(**ec_args):
@@ -204,12 +265,80 @@ def start(**ec_args):
     S["started"] = True
 
 
+def _hyb_tail(layer, T, k):
+    """Trailing staging batches the host tier takes for a T-token step (ct_vllm.py:163-178): the host time of
+    n experts, n (C0 + C1 (rows - 1)) ms at rows = k T / E routes per expert, against the copy time of the rest,
+    DMA ms per expert, after a per-token input cost TOK_US; at most MAX_BATCHES, and at least the NS batches the
+    copy engine starts with stay staged. Returns (batches, the tail's experts)."""
+    if getattr(layer, "_exl3_dma", None) is None:
+        return 0, []
+    batches = exl3._dma_batches(layer)
+    nb = len(batches)
+    if nb == 0:
+        return 0, []
+    c = S["hyb_cost"]
+    staged = sum(len(b) for b in batches)
+    rows = k * T / layer.E
+    c_cpu = c["c0"] + c["c1"] * max(0.0, rows - 1)
+    fixed = c["tok_us"] * T / 1000.0
+    n_cpu = max(0.0, (staged * c["dma"] - fixed) / (c["dma"] + c_cpu))
+    kc = int(n_cpu // exl3._DMA_B)
+    kc = max(0, min(kc, nb - exl3._DMA_NS, c["max_batches"]))
+    return kc, [e for b in batches[nb - kc:] for e in b]
+
+
+def _hybrid(x2d, ids, weights, layer, inners, limit, kc, tail):
+    """One hybrid step (ct_vllm.py:186-213): the tail's experts to the host tier, the rest staged."""
+    ct = layer._ct
+    T = x2d.shape[0]
+    dev = S["dev"]
+    orig = _ORIG.get("fused", exl3.apply_exl3_fused_moe)
+    key = (kc, tuple(tail))
+    fake = ct.setdefault("hyb_slot", {}).get(key)
+    if fake is None:
+        f = np.zeros(ct["E"], np.int32)
+        f[tail] = -1
+        fake = torch.from_numpy(f).to(dev)
+        ct["hyb_slot"] = {key: fake}            # the tail changes with the cache's residency: keep the latest
+    n = ids.numel()
+    so, wo = S["sel"][:n], S["w"][:n]
+    z = x2d if (x2d.dtype == torch.half and x2d.is_contiguous()) else x2d.half().contiguous()
+    # the x rows to the mailbox on the copy engine, on this stream, before the split publishes (pol[8] = 1)
+    cache.stage_copy([(S["hx"], z.data_ptr(), z.numel() * 2)], torch.cuda.current_stream(dev))
+    cnt = ct.get("hyb_cnt")
+    if cnt is None:
+        cnt = ct["hyb_cnt"] = torch.zeros(ct["E"], dtype=torch.int32, device=dev)
+    idc = ids.contiguous().long()
+    wc = weights.contiguous().float()
+    _lib.call("mm_split", idc.data_ptr(), wc.data_ptr(), z.data_ptr(), n, T, S["H"], ct["E"], fake.data_ptr(),
+              ct["score"].data_ptr(), S["pol_hyb"].data_ptr(), S["ctrl"], S["hx"], S["picks"], S["seqc"].data_ptr(),
+              ct["li"], so.data_ptr(), wo.data_ptr(), S["dflag"].data_ptr(), S["stats_hyb"].data_ptr(),
+              cnt.data_ptr(), None, None, None, _lib.stream_ptr())
+    layer._hyb_tail = kc
+    try:
+        out = orig(x2d, so.view(ids.shape), wo.view(weights.shape).to(weights.dtype), layer, inners, None, limit)
+    finally:
+        layer._hyb_tail = 0
+    _lib.call("mm_combine_host", out.data_ptr(), out.numel(), S["dflag"].data_ptr(), S["ctrl"], S["hout"],
+              S["stats_hyb"].data_ptr(), S["timeout_ns"], _lib.stream_ptr())
+    S["hyb_n"] += 1
+    S["hyb_last"] = {"tokens": T, "batches": kc, "experts": len(tail)}
+    return out
+
+
 def _fused(x2d, ids, weights, layer, inners, expert_map, limit):
-    """Split / fused MoE / combine for decode-sized calls of tier layers; everything else goes to the plugin's
-    own entry unchanged (ct_vllm.py:214-223)."""
+    """Split / fused MoE / combine for decode-sized calls of tier layers, the hybrid tail for lone prefill steps
+    up to DSV41_CT_HYB_MAX tokens; everything else goes to the plugin's own entry unchanged
+    (ct_vllm.py:181-223)."""
     ct = getattr(layer, "_ct", None)
     T = x2d.shape[0]
     orig = _ORIG.get("fused", exl3.apply_exl3_fused_moe)
+    if (ct is not None and S["started"] and S["cpu_tier"] and expert_map is None and S.get("hyb_max", 0)
+            and S["maxbsz"] < T <= S["hyb_max"] and S.get("solo", True) and ids.numel() <= S["maxpicks"]
+            and inners is None and not torch.cuda.is_current_stream_capturing()):
+        kc, tail = _hyb_tail(layer, T, ids.reshape(T, -1).shape[1])
+        if kc > 0:
+            return _hybrid(x2d, ids, weights, layer, inners, limit, kc, tail)
     if ct is None or not S["started"] or T > S["maxbsz"] or expert_map is not None or ids.numel() > S["maxpicks"]:
         return orig(x2d, ids, weights, layer, inners, expert_map, limit)
     n = ids.numel()
@@ -266,15 +395,21 @@ def summary():
     st = S["stats"].tolist()
     calls = max(1, st[3])
     h = _tier.stats() if S["cpu_tier"] else {"jobs": 0, "busy_ns": 0}
+    hy = S["stats_hyb"].tolist()
+    hyb = {"calls": hy[3], "host_experts": hy[2], "timeouts": hy[6], "last": S.get("hyb_last")} if hy[3] else None
     return {"calls": st[3], "hits": st[0], "misses": st[1], "cpu_experts": st[2], "cpu_per_call": round(st[2] / calls, 3),
+            "hybrid": hyb,
             "gpu_wait_ms": round(st[4] / 1e6 / max(1, st[5]), 4), "timeouts": st[6], "host_jobs": h["jobs"],
             "host_busy_ms": round(h["busy_ns"] / 1e6 / max(1, h["jobs"]), 4), "selftest": S["selftest"],
             "hit_rate": round(st[0] / max(1, st[0] + st[1]), 4), "ec": ec_summary()}
 
 
-def before_step(ntok):
+def before_step(ntok, solo=None):
     """Before an engine step of `ntok` scheduled tokens: release the cache before prefill-sized steps (elastic
-    cache). ec_step() follows the step."""
+    cache); `solo` (one request in the step, when known) gates the hybrid prefill tail, which the reference runs
+    for a lone request only (ct_vllm.py:525). ec_step() follows the step."""
+    if solo is not None:
+        S["solo"] = bool(solo)
     c = EC["cache"]
     if c is None:
         return
@@ -305,7 +440,9 @@ def install_step_hook(modules=RUNNER_MODULES):
         def execute_model(self, *a, _o=orig, **k):
             try:
                 so = a[0] if a else k.get("scheduler_output")
-                before_step(int(getattr(so, "total_num_scheduled_tokens", 0) or 0))
+                reqs = getattr(so, "num_scheduled_tokens", None)
+                before_step(int(getattr(so, "total_num_scheduled_tokens", 0) or 0),
+                            solo=(len(reqs) <= 1) if isinstance(reqs, dict) else None)
             except Exception:
                 S["hook_errors"] = S.get("hook_errors", 0) + 1
             r = _o(self, *a, **k)

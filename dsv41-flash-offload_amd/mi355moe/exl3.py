@@ -213,9 +213,16 @@ def _dma_prefill(x2d, ids, w16, layer, limit, dev):
     counts_d = routes["counts"][:E]
     ws, need = _fat_ws(dev, n, T, E, layer.H, layer.I)
     batches = _dma_batches(layer)
+    # a hybrid step's trailing batches belong to the host tier (its routes arrive masked): neither copied nor
+    # computed here (runtime/patch_dma_prefetch.py:21)
+    tail = int(getattr(layer, "_hyb_tail", 0) or 0)
+    if tail > 0:
+        batches = batches[:max(0, len(batches) - tail)]
+        D["tail_skipped"] = D.get("tail_skipped", 0) + tail
+    skip_e = {e for b in _dma_batches(layer)[len(batches):] for e in b} if tail > 0 else set()
     staged_e = {e for b in batches for e in b}
     masks = np.ones((len(batches) + 1, E), np.uint8)
-    masks[0, [e for e in range(E) if e not in staged_e]] = 0          # row 0: the HBM-resident experts
+    masks[0, [e for e in range(E) if e not in staged_e and e not in skip_e]] = 0   # row 0: the HBM-resident experts
     items = np.zeros((max(len(batches), 1), _DMA_B, 5), np.int64)
     items[:, :, 0] = -1
     pool = st["slots"]
@@ -245,7 +252,7 @@ def _dma_prefill(x2d, ids, w16, layer, limit, dev):
             D["prefetched"] += 1
         else:
             events[j] = _dma_issue(layer, j % _DMA_NS, batches[j], dev)
-    if len(staged_e) < E:
+    if len(staged_e) + len(skip_e) < E:
         run(L, 0)
     if batches:
         tabs = _dma_tables(layer)

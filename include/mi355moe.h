@@ -54,7 +54,9 @@ int mm_host_free(void* ptr);
 /* Router top-k (vLLM FusedMoE semantics at the boundary patches/vllm-exl3-host-dma.patch:496-507):
  * logits[t][e] = sum_h x[t][h] * gate[e][h] (x bf16 [T][H], gate fp32 [E][H], fp32 sums);
  * ids[t][:k] = the k largest logits (ties -> lower expert id), w[t][:k] = softmax over those k logits.
- * logits may be NULL. Requires E <= 1024, k <= 32. */
+ * logits fp32 [T][E] is written too (it is the kernels' workspace: required). Requires E <= 1024, k <= 32.
+ * Up to 64 tokens (H a multiple of 256) one wave per expert sums lane partials; larger calls sum each logit in
+ * ascending h: the last bits of a logit may differ between the two. */
 int mm_router_topk(const void* x_bf16, int T, int H, const float* gate, int E, int k, float* logits, int64_t* ids,
                    float* w, mm_stream_t stream);
 

@@ -219,3 +219,27 @@ def test_mailbox_needs_its_capacity(tier):
     mb = {"ctrl": ctrl.ctypes.data, "hx": buf.ctypes.data, "picks": buf.ctypes.data, "hout": buf.ctypes.data}
     with pytest.raises(RuntimeError, match="capacities"):
         tier.init(512, 256, 1, mailbox=mb, threads=1, cpus=[])
+
+
+@pytest.mark.parametrize("mode", [1, 0])
+def test_many_rows_per_expert_bitwise_equal_to_single_rows(tier, mode):
+    """Experts with many rows (a prefill tail job: 40 tokens over 6 experts, every expert 20-40 rows) take the
+    chunked GEMV that decodes each weight once for all rows; every output equals the same token computed alone
+    (the per-token path) bit for bit, in EXACT and in AFFINE mode."""
+    H, I, E, T, k = 512, 256, 6, 40, 4
+    seed = 99
+    ptrs, sc, keep = _layer(seed, E, H, I)
+    tier.init(H, I, 1, threads=4, cpus=sorted(os.sched_getaffinity(0))[:4])
+    tier.set_limit(10.0)
+    tier.add_layer(0, ptrs=ptrs, scales=sc)
+    rng = np.random.default_rng(5)
+    sel = np.stack([rng.permutation(E)[:k] for _ in range(T)]).astype(np.int32)
+    w = rng.uniform(0.1, 1.0, (T, k)).astype(np.float32)
+    x = rng.normal(0, 1, (T, H)).astype(np.float16).astype(np.float32)
+    got = tier.forward(0, x, sel, w, mode)
+    for t in range(T):
+        one = tier.forward(0, x[t:t + 1], sel[t:t + 1], w[t:t + 1], mode)
+        assert np.array_equal(got[t], one[0]), t
+    ref = _oracle(seed, sc, x, sel, w, H, I, 10.0)
+    mx, mean = O.tolerance_metrics(got, ref)
+    assert mx <= 2e-2 and mean <= 2e-3, (mx, mean)

@@ -119,3 +119,34 @@ def test_step_hook_releases_before_prefill_steps_and_steps_after(monkeypatch):
     finally:
         ct_vllm.EC["cache"] = None
         ct_vllm.reset()
+
+
+def test_hybrid_tail_cost_model_known_answers():
+    """_hyb_tail with the reference's default constants (ct/ct_vllm.py:163-178: C0 0.24, C1 0.085, DMA 0.54,
+    6 us per token, at most 24 batches): 384 cold experts in 48 batches of 8, NS = 8 slots, top-8. Hand-computed:
+    T = 2048: rows 42.67, host 0.24 + 0.085 x 41.67 = 3.782 ms per expert, n = (384 x 0.54 - 12.288) / 4.322 =
+    45.1 experts -> 5 batches; T = 600: rows 12.5, host 1.2175, n = (207.36 - 3.6) / 1.7575 = 115.9 -> 14 batches;
+    T = 513 with a cap of 10 -> 10; a cold set of 70 experts (9 batches): T = 2048 gives (37.8 - 12.288) / 4.322 =
+    5.9 experts -> 0 batches, T = 600 gives (37.8 - 3.6) / 1.7575 = 19.5 -> 2, capped at 9 - 8 = 1."""
+    import numpy as np
+    from mi355moe import ct_vllm, exl3
+    saved = (exl3._DMA_B, exl3._DMA_NS)
+    exl3._DMA_B, exl3._DMA_NS = 8, 8
+    ct_vllm.reset()
+    try:
+        ct_vllm.S["hyb_cost"] = {"c0": 0.24, "c1": 0.085, "dma": 0.54, "tok_us": 6.0, "max_batches": 24}
+        lay = types.SimpleNamespace(E=384, slot_host=np.full(384, -1, np.int32), _exl3_dma={})
+        kc, tail = ct_vllm._hyb_tail(lay, 2048, 8)
+        assert kc == 5 and tail == list(range(384 - 40, 384))
+        assert ct_vllm._hyb_tail(lay, 600, 8)[0] == 14
+        ct_vllm.S["hyb_cost"]["max_batches"] = 10
+        assert ct_vllm._hyb_tail(lay, 513, 8)[0] == 10
+        lay.slot_host[70:] = 0                       # only experts 0 .. 69 are cold: 9 batches
+        assert ct_vllm._hyb_tail(lay, 2048, 8) == (0, [])
+        kc, tail = ct_vllm._hyb_tail(lay, 600, 8)
+        assert kc == 1 and tail == list(range(64, 70))
+        lay.slot_host[:] = 0                         # nothing staged: no tail
+        assert ct_vllm._hyb_tail(lay, 2048, 8) == (0, [])
+    finally:
+        exl3._DMA_B, exl3._DMA_NS = saved
+        ct_vllm.reset()
