@@ -156,6 +156,69 @@ def test_decode_chain_three_layers(dev):
             prev = outs[l]
 
 
+def test_decode_chain_forty_layers(dev):
+    """The benchmark's 40-layer decode step at T = 4 (40 x 385 experts resident, Zipf routing per layer, each layer
+    rescaling its input): the step captured in one graph and replayed gives every layer's output bit for bit as the
+    eager chain; at every layer the fp16 input built from the previous output equals the oracle's chain step bit
+    for bit; layers 0, 13, 26 and 39 match the oracle on their own input."""
+    import torch
+    from mi355moe import _lib, workload
+    from mi355moe.moe import DecodeRunner
+    H, I, E, T, K, L = 4096, 2048, 384, 4, 8, 40
+    print("decode chain of 40 layers: stores", flush=True)
+    stores = [make_store(E + 1, H, I, 1000 + l, device=dev) for l in range(L)]
+    routes = [workload.zipf_routing(T, K, E, seed=2000 + l) for l in range(L)]
+    runners = []
+    for l in range(L):
+        R = DecodeRunner(E, H, I, T, K, device=dev)
+        R.set_routes(_t(routes[l][0], dev), _t(routes[l][1], dev))
+        runners.append(R)
+    x0 = _t(workload.activations(T, H, seed=7), dev)
+    outs = [torch.empty((T, H), dtype=torch.float32, device=dev) for _ in range(L)]
+
+    def step():
+        src = x0
+        for l in range(L):
+            src = runners[l].layer(stores[l], x=src, out=outs[l], rescale=True)
+
+    step()
+    torch.cuda.synchronize()
+    eager = [o.clone() for o in outs]
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            step()
+    torch.cuda.current_stream().wait_stream(side)
+    for o in outs:
+        o.fill_(float("nan"))
+    torch.cuda.synchronize()
+    for r in range(2):
+        print(f"decode chain of 40 layers: graph replay {r}", flush=True)
+        g.replay()
+        torch.cuda.synchronize()
+        for l in range(L):
+            assert torch.equal(outs[l], eager[l]), f"replay {r}: layer {l} differs from the eager chain"
+    prev = x0.cpu().numpy()
+    for l in range(L):
+        x16 = torch.empty((T, H), dtype=torch.float16, device=dev)
+        src = x0 if l == 0 else eager[l - 1]
+        _lib.call("mm_prepare_input", src.data_ptr(), T, H, 1, None, x16.data_ptr(), _lib.stream_ptr())
+        torch.cuda.synchronize()
+        got = x16.cpu().numpy().astype(np.float32)
+        assert np.array_equal(got, O.prepare_input(prev, rescale=True)), f"layer {l}: chain step differs"
+        if l in (0, 13, 26, 39):
+            ids = np.concatenate([routes[l][0], np.full((T, 1), E)], 1)
+            wts = np.concatenate([routes[l][1], np.ones((T, 1), np.float32)], 1)
+            ref = OracleLayer(stores[l], 1000 + l, cache=False).forward(got, ids, wts)
+            ok, m = within_tolerance(eager[l].cpu().numpy(), ref)
+            print(f"layer {l} on its own input vs oracle: {m}", flush=True)
+            assert ok, (l, m)
+        prev = eager[l].cpu().numpy()
+    del g
+
+
 @pytest.mark.parametrize("T", [1, 4])
 def test_dsv41_shape_decode(dev, T):
     """The served DSV41 expert shape: H 5120, I 2304, top-6 over 384 routed experts + 1 shared, on the decode
