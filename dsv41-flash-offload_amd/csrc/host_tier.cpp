@@ -18,7 +18,11 @@
 // (VNNI) that adds the four bytes onto the constant. EXACT rounds KINV * code + KBIAS to fp16 per weight (the
 // reference's EXACT expert and the GPU's fp16 weights); AFFINE (the default) accumulates sum_k x_k (code_k - 1534)
 // per column and forms KINV * S + (KBIAS + 1534 KINV) * sum_k x_k once per output (ft_core.h:267-293's AFFINE
-// evaluation; the codes are centred so the fp32 sum carries less of the common offset).
+// evaluation; the codes are centred so the fp32 sum carries less of the common offset). I16 (ft_core.h:315-415)
+// quantises each 128-block of transformed inputs to int16 (|x| <= 16383 with one fp32 scale per block) and sums
+// bytesum * x exactly in int32 per block (VNNI vpdpwssd over row pairs), scaled into fp32 once per block; the
+// output is KINV * S + (1024 KINV + KBIAS) * sum of the dequantised inputs. The automatic mode takes I16 for jobs
+// whose experts have at most two rows each and AFFINE otherwise, as the reference's tier does.
 #include <immintrin.h>
 #include <pthread.h>
 #include <sched.h>
@@ -222,6 +226,30 @@ static float prep_input(const float* x, const uint16_t* suh, int K, float* xt)
     return s;
 }
 
+// I16 inputs (ft_core.h:393-411): each 128-block of xt as int16 with scale amax / 16383 (1 for an all-zero block),
+// rounded to nearest even after a multiply by the reciprocal; returns the sum of the dequantised values, block by
+// block in fp32 (the fix-up's input sum).
+static float quant_i16(const float* xt, int K, int16_t* xq, float* qs)
+{
+    float s = 0.0f;
+    for (int b = 0; b < K; b += 128)
+    {
+        float amax = 0.0f;
+        for (int i = 0; i < 128; ++i) amax = std::max(amax, std::fabs(xt[b + i]));
+        const float sc = amax > 0.0f ? amax / 16383.0f : 1.0f, rs = 1.0f / sc;
+        long si = 0;
+        for (int i = 0; i < 128; ++i)
+        {
+            const int v = (int)std::nearbyint(xt[b + i] * rs);
+            xq[b + i] = (int16_t)v;
+            si += v;
+        }
+        qs[b / 128] = sc;
+        s += (float)si * sc;
+    }
+    return s;
+}
+
 // y = r16(FWHT(r16(y)) * HAD * svh) on one 128-block in place (ft_core.h:104-110).
 static void out_block(float* y, const uint16_t* svh)
 {
@@ -284,6 +312,15 @@ static inline __m512 decode_row(__m512i wa, __m512i wb, int r, const Tables& TAB
         w = _mm512_cvtph_ps(_mm512_cvtps_ph(_mm512_fmadd_ps(w, C.vkinv, C.vkbias),
                                             _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
     return w;
+}
+
+// Byte sums (code - 1024) of row r, columns 0 .. 15, as int32.
+static inline __m512i byte_sums(__m512i wa, __m512i wb, int r, const Tables& TAB, const DecodeConsts& C)
+{
+    const __m512i lo = _mm512_permutex2var_epi32(wa, _mm512_load_si512(TAB.lo[r]), wb);
+    const __m512i hi = _mm512_permutex2var_epi32(wa, _mm512_load_si512(TAB.hi[r]), wb);
+    const __m512i st = _mm512_and_si512(_mm512_shrdv_epi32(lo, hi, _mm512_load_si512(TAB.sh[r])), C.vmask);
+    return _mm512_dpbusd_epi32(_mm512_setzero_si512(), _mm512_mullo_epi32(st, C.vmul), C.vones);
 }
 
 static inline void prefetch_rows(const uint8_t* row)
@@ -438,6 +475,95 @@ static void gemv_tokens(const Mat& m, int cb, int nt, const Rows& R)
     }
 }
 
+// I16 sums of column block cb for MT tokens: int16 inputs xq[t] (row pairs read as one dword), block scales
+// qs[t], input sums xs[t]; per tile row pair the two rows' byte sums are packed into the halves of each dword and
+// one vpdpwssd per token adds both products; every 8 tile rows (one 128-block) the int32 sums are scaled into fp32.
+struct RowsI16
+{
+    const int16_t* xq;
+    size_t xstride;
+    const float* qs;
+    size_t qstride;
+    const float* xs;
+    size_t sstride;
+    float* y;
+    size_t ystride;
+    RowsI16 at(int t) const
+    {
+        return { xq + t * xstride, xstride, qs + t * qstride, qstride, xs + t * sstride, sstride, y + t * ystride, ystride };
+    }
+};
+
+template <int MT>
+static void gemv_block_i16(const Mat& m, int cb, const RowsI16& R)
+{
+    const int NT = m.N / 16, KT = m.K / 16;
+    const DecodeConsts C = DecodeConsts::make<false>();
+    const __m512i zero = _mm512_setzero_si512();
+    __m512i acc[MT][8];
+    alignas(64) float accf[MT][8][16];
+    for (int t = 0; t < MT; ++t)
+        for (int j = 0; j < 8; ++j)
+        {
+            acc[t][j] = zero;
+            _mm512_store_ps(accf[t][j], _mm512_setzero_ps());
+        }
+    const uint8_t* base = m.tr + (size_t)cb * 8 * TILE_BYTES;
+    const Tables& TAB = tab();
+    for (int tk = 0; tk < KT; ++tk)
+    {
+        const uint8_t* row = base + (size_t)tk * NT * TILE_BYTES;
+        if (tk + 4 < KT) prefetch_rows(row + (size_t)4 * NT * TILE_BYTES);
+        for (int j = 0; j < 8; ++j)
+        {
+            const uint8_t* tile = row + j * TILE_BYTES;
+            const __m512i wa = _mm512_loadu_si512(tile);
+            const __m512i wb = _mm512_castsi256_si512(_mm256_loadu_si256((const __m256i*)(tile + 64)));
+            for (int r = 0; r < 16; r += 2)
+            {
+                const __m512i b0 = byte_sums(wa, wb, r, TAB, C), b1 = byte_sums(wa, wb, r + 1, TAB, C);
+                const __m512i pair = _mm512_or_si512(b0, _mm512_slli_epi32(b1, 16));
+                const int k = tk * 16 + r;
+                for (int t = 0; t < MT; ++t)
+                {
+                    int32_t xp;
+                    memcpy(&xp, R.xq + t * R.xstride + k, 4);
+                    acc[t][j] = _mm512_dpwssd_epi32(acc[t][j], pair, _mm512_set1_epi32(xp));
+                }
+            }
+        }
+        if ((tk & 7) == 7)
+            for (int t = 0; t < MT; ++t)
+            {
+                const __m512 sc = _mm512_set1_ps(R.qs[t * R.qstride + (tk >> 3)]);
+                for (int j = 0; j < 8; ++j)
+                {
+                    _mm512_store_ps(accf[t][j], _mm512_fmadd_ps(_mm512_cvtepi32_ps(acc[t][j]), sc, _mm512_load_ps(accf[t][j])));
+                    acc[t][j] = zero;
+                }
+            }
+    }
+    const __m512 vkinv = _mm512_set1_ps(kinv());
+    const float caff = (float)(1024.0 * (double)kinv() + (double)kbias());       // -3.453125, exact
+    for (int t = 0; t < MT; ++t)
+    {
+        const __m512 off = _mm512_set1_ps(caff * R.xs[t * R.sstride]);
+        for (int j = 0; j < 8; ++j)
+            _mm512_storeu_ps(R.y + t * R.ystride + 16 * j, _mm512_fmadd_ps(vkinv, _mm512_load_ps(accf[t][j]), off));
+    }
+}
+
+static void gemv_tokens_i16(const Mat& m, int cb, int nt, const RowsI16& R)
+{
+    for (int t0 = 0; t0 < nt; t0 += MAX_MT)
+    {
+        const int mt = nt - t0 < MAX_MT ? nt - t0 : MAX_MT;
+        if (mt == 3) gemv_block_i16<3>(m, cb, R.at(t0));
+        else if (mt == 2) gemv_block_i16<2>(m, cb, R.at(t0));
+        else gemv_block_i16<1>(m, cb, R.at(t0));
+    }
+}
+
 // ------------------------------------------------------------------------------------------------ a job
 
 // The picks of one call grouped by expert: expert g's tokens are tok[first[g] .. first[g + 1]) (pick order).
@@ -456,6 +582,9 @@ struct Job
     std::vector<int> cnt, slot, fill, tfill;      // grouping scratch
     // per group entry (expert e, token t): transformed inputs and intermediate rows
     std::vector<float> xt, xs, gu, xd, xds, yd;
+    // I16 mode: int16 inputs and block scales of the gate/up inputs and of the down inputs
+    std::vector<int16_t> xq, xdq;
+    std::vector<float> qs, qds;
     float* out = nullptr;                   // [T][H]
 };
 
@@ -472,6 +601,14 @@ static void ph_input(void* c, int u)          // u = group entry
     float* xt = J.xt.data() + (size_t)u * 2 * J.H;
     J.xs[2 * u + 0] = prep_input(x, E.g.suh, J.H, xt);
     J.xs[2 * u + 1] = prep_input(x, E.u.suh, J.H, xt + J.H);
+    if (J.mode == 2)
+    {
+        const int nb = J.H / 128;
+        int16_t* xq = J.xq.data() + (size_t)u * 2 * J.H;
+        float* qs = J.qs.data() + (size_t)u * 2 * nb;
+        J.xs[2 * u + 0] = quant_i16(xt, J.H, xq, qs);
+        J.xs[2 * u + 1] = quant_i16(xt + J.H, J.H, xq + J.H, qs + nb);
+    }
 }
 
 static void ph_gateup(void* c, int u)         // u = (group, matrix, column block of I)
@@ -485,7 +622,15 @@ static void ph_gateup(void* c, int u)         // u = (group, matrix, column bloc
     const Rows R = { J.xt.data() + (size_t)f * 2 * J.H + (size_t)mm * J.H, (size_t)2 * J.H,
                      J.xs.data() + 2 * (size_t)f + mm, 2,
                      J.gu.data() + (size_t)f * 2 * J.I + (size_t)mm * J.I + cb * 128, (size_t)2 * J.I };
-    if (J.mode == 1) gemv_tokens<true>(M, cb, nt, R);
+    if (J.mode == 2)
+    {
+        const int nb = J.H / 128;
+        const RowsI16 Q = { J.xq.data() + (size_t)f * 2 * J.H + (size_t)mm * J.H, (size_t)2 * J.H,
+                            J.qs.data() + (size_t)f * 2 * nb + (size_t)mm * nb, (size_t)2 * nb, R.xs, R.sstride, R.y,
+                            R.ystride };
+        gemv_tokens_i16(M, cb, nt, Q);
+    }
+    else if (J.mode == 1) gemv_tokens<true>(M, cb, nt, R);
     else gemv_tokens<false>(M, cb, nt, R);
     for (int t = 0; t < nt; ++t) out_block(R.y + t * R.ystride, M.svh + cb * 128);
 }
@@ -498,6 +643,9 @@ static void ph_act(void* c, int u)            // u = group entry: SwiGLU (in pla
     const float* uu = gg + J.I;
     for (int i = 0; i < J.I; ++i) gg[i] = r16(act_gu(gg[i], uu[i], J.limit));
     J.xds[u] = prep_input(gg, E.d.suh, J.I, J.xd.data() + (size_t)u * J.I);
+    if (J.mode == 2)
+        J.xds[u] = quant_i16(J.xd.data() + (size_t)u * J.I, J.I, J.xdq.data() + (size_t)u * J.I,
+                             J.qds.data() + (size_t)u * (J.I / 128));
 }
 
 static void ph_down(void* c, int u)           // u = (group, column block of H)
@@ -509,7 +657,14 @@ static void ph_down(void* c, int u)           // u = (group, column block of H)
     const int f = J.first[g], nt = J.first[g + 1] - f;
     const Rows R = { J.xd.data() + (size_t)f * J.I, (size_t)J.I, J.xds.data() + f, 1,
                      J.yd.data() + (size_t)f * J.H + cb * 128, (size_t)J.H };
-    if (J.mode == 1) gemv_tokens<true>(M, cb, nt, R);
+    if (J.mode == 2)
+    {
+        const int nb = J.I / 128;
+        const RowsI16 Q = { J.xdq.data() + (size_t)f * J.I, (size_t)J.I, J.qds.data() + (size_t)f * nb, (size_t)nb,
+                            R.xs, R.sstride, R.y, R.ystride };
+        gemv_tokens_i16(M, cb, nt, Q);
+    }
+    else if (J.mode == 1) gemv_tokens<true>(M, cb, nt, R);
     else gemv_tokens<false>(M, cb, nt, R);
     for (int t = 0; t < nt; ++t) out_block(R.y + t * R.ystride, M.svh + cb * 128);
 }
@@ -540,7 +695,6 @@ static void run_picks(Pool& pool, const Layer& L, int H, int I, const float* x, 
     J.H = H;
     J.I = I;
     J.T = T;
-    J.mode = mode;
     J.limit = limit;
     J.x = x;
     J.out = out;
@@ -558,6 +712,11 @@ static void run_picks(Pool& pool, const Layer& L, int H, int I, const float* x, 
             J.first.push_back(J.first.back() + J.cnt[e]);
         }
     const int ng = (int)J.gexp.size();
+    // mode: 0 AFFINE, 1 EXACT, 2 I16; automatic (-1): I16 if no expert has more than two rows, else AFFINE
+    // (ft_tier_ext.cpp:130-132)
+    int maxm = 0;
+    for (int e : J.gexp) maxm = std::max(maxm, J.cnt[e]);
+    J.mode = mode >= 0 ? mode : (maxm <= 2 ? 2 : 0);
     J.tok.assign(np, 0);
     J.wt.assign(np, 0.0f);
     J.pick_of.assign(np, 0);
@@ -581,6 +740,13 @@ static void run_picks(Pool& pool, const Layer& L, int H, int I, const float* x, 
     J.xd.resize((size_t)np * I);
     J.xds.resize((size_t)np);
     J.yd.resize((size_t)np * H);
+    if (J.mode == 2)
+    {
+        J.xq.resize((size_t)np * 2 * H);
+        J.qs.resize((size_t)np * 2 * (H / 128));
+        J.xdq.resize((size_t)np * I);
+        J.qds.resize((size_t)np * (I / 128));
+    }
     if (np)
     {
         pool.run(ph_input, &J, np);
@@ -621,8 +787,8 @@ struct Tier
 
 static Tier* g_tier = nullptr;
 
-// mode: 0 AFFINE, 1 EXACT, -1 auto (AFFINE)
-static int eff_mode(int m) { return m == 1 ? 1 : 0; }
+// mode: 0 AFFINE, 1 EXACT, 2 I16, -1 automatic (resolved per job in run_picks); anything else is automatic
+static int eff_mode(int m) { return m >= 0 && m <= 2 ? m : -1; }
 
 // The mailbox's x rows fp16 -> fp32. The words are read as relaxed atomics: the publisher may rewrite them while
 // they are read (after a timed-out job), which the sequence check after the copy detects.

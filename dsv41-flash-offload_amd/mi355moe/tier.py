@@ -9,7 +9,9 @@ kernels/cpu_avx2/ft_tier_ext.cpp:36-231, driven from ct/ct_vllm.py:56-87,143-152
   add_layer(li, layer)                a layer with a pinned host home (ExpertStore): its home rows and host copies
                                       of its scales
   start() / stop() / shutdown()       the serving thread
-  forward(li, x, sel, w, mode)        synchronous forward (tests, the tier's self-check and calibration)
+  forward(li, x, sel, w, mode)        synchronous forward (tests, the tier's self-check and calibration); mode 0
+                                      AFFINE, 1 EXACT, 2 I16, -1 automatic (I16 when no expert has more than two
+                                      rows, else AFFINE)
   stats()                             jobs, picks, tokens, empty jobs, busy ns, rejected and stale jobs
 
 Host memory the workers read (the mailbox, the layers' pinned expert homes) is held while the tier is up: the

@@ -294,8 +294,9 @@ int mm_prepare_input(const float* x, int T, int H, int rescale, void* x_bf16, vo
  * memory the GPU maps, e.g. mm_host_alloc); they may be NULL (and the capacities 0) when only mm_tier_forward is
  * used. A published job with more than maxtok tokens or maxpicks picks, or naming a layer never added, is not
  * computed: the serving thread zeroes the hout rows that exist, answers it, and counts it as rejected (the
- * reference's worker trusts ctrl[3] and ctrl[4]). mode: 1 EXACT (fp16-rounded weights), 0 AFFINE, -1 automatic
- * (AFFINE; the reference's automatic choice of its int16 path is not built). H a multiple of 512, I of 128.
+ * reference's worker trusts ctrl[3] and ctrl[4]). mode: 1 EXACT (fp16-rounded weights), 0 AFFINE, 2 I16 (int16
+ * inputs per 128-block, exact int32 block sums), -1 automatic (I16 for a job whose experts have at most two rows
+ * each, else AFFINE: the reference's choice, ft_tier_ext.cpp:130-132). H a multiple of 512, I of 128.
  * The first call registers a process exit handler that stops the serving thread and the workers before memory
  * released at exit (the mailbox, the expert homes) can go away. */
 int mm_tier_init(int threads, const int* cpus, int ncpus, int64_t* ctrl, const void* hx, const int32_t* picks,

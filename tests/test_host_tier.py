@@ -54,11 +54,11 @@ def _oracle(seed, scales, x, sel, w, H, I, limit):
     return out
 
 
-@pytest.mark.parametrize("mode", [1, 0])
+@pytest.mark.parametrize("mode", [1, 0, 2])
 @pytest.mark.parametrize("H,I,E,T,k", [(512, 256, 6, 5, 3), (1024, 384, 9, 9, 4)])
 def test_forward_matches_oracle(tier, mode, H, I, E, T, k):
-    """EXACT (mode 1) and AFFINE (mode 0) against the oracle's EXACT expert; groups of 1 to 9 tokens per expert
-    (GEMV passes of 3), masked picks, clamp on."""
+    """EXACT (mode 1), AFFINE (mode 0) and I16 (mode 2) against the oracle's EXACT expert; groups of 1 to 9 tokens
+    per expert (GEMV passes of 3), masked picks, clamp on."""
     seed = 900 + H
     ptrs, sc, keep = _layer(seed, E, H, I)
     tier.init(H, I, 1, threads=4, cpus=sorted(os.sched_getaffinity(0))[:4])
@@ -98,7 +98,9 @@ def test_forward_matches_reference_golden_expert(tier):
 
 def test_forward_matches_reference_tier_modes(tier):
     """The reference's CPU tier on a T=4 layer (6 experts, 12 picks): EXACT against its EXACT output, AFFINE
-    against its AFFINE output."""
+    against its AFFINE output, I16 against its I16 output, each within the parity tolerance (I16's int16 inputs
+    and block scales follow the reference's quantisation, so I16 is closer to the reference's I16 output than to
+    its AFFINE output)."""
     g = np.load(os.path.join(os.path.dirname(__file__), "golden", "tier_t4.npz"))
     H, I, E = int(g["H"]), int(g["I"]), int(g["E"])
     seed = int(g["layer_seed"])
@@ -118,11 +120,15 @@ def test_forward_matches_reference_tier_modes(tier):
     for t, e, wt in zip(g["tok"], g["exp"], g["w"]):
         sel[t, fill[t]], w[t, fill[t]] = e, wt
         fill[t] += 1
-    for mode in (1, 0):
+    for mode in (1, 0, 2):
         got = tier.forward(0, g["x"], sel, w, mode)
         mx, mean = O.tolerance_metrics(got, g[f"out_mode{mode}"].astype(np.float64))
         print(f"mode {mode} vs the reference tier: {mx:.2e} {mean:.2e}")
         assert mx <= 2e-2 and mean <= 2e-3, (mode, mx, mean)
+        if mode == 2:
+            _, m0 = O.tolerance_metrics(got, g["out_mode0"].astype(np.float64))
+            print(f"mode 2 vs the reference tier's AFFINE output: {m0:.2e}")
+            assert mean < m0, (mean, m0)
 
 
 def test_mailbox_worker_serves_jobs(tier):
@@ -243,3 +249,22 @@ def test_many_rows_per_expert_bitwise_equal_to_single_rows(tier, mode):
     ref = _oracle(seed, sc, x, sel, w, H, I, 10.0)
     mx, mean = O.tolerance_metrics(got, ref)
     assert mx <= 2e-2 and mean <= 2e-3, (mx, mean)
+
+
+def test_automatic_mode_selection(tier):
+    """The automatic mode (the reference's ft_tier_ext.cpp:130-132): a job whose experts have at most two rows each
+    is computed in I16 (bit for bit equal to mode 2), a job with an expert of three rows in AFFINE (mode 0)."""
+    H, I, E = 512, 256, 8
+    seed = 321
+    ptrs, sc, keep = _layer(seed, E, H, I)
+    tier.init(H, I, 1, threads=4, cpus=sorted(os.sched_getaffinity(0))[:4])
+    tier.set_limit(10.0)
+    tier.add_layer(0, ptrs=ptrs, scales=sc)
+    rng = np.random.default_rng(3)
+    x = rng.normal(0, 1, (3, H)).astype(np.float16).astype(np.float32)
+    w = rng.uniform(0.1, 1.0, (3, 2)).astype(np.float32)
+    two = np.array([[0, 1], [1, 2], [3, 4]], np.int32)           # expert 1 has two rows
+    three = np.array([[0, 1], [1, 2], [1, 4]], np.int32)         # expert 1 has three rows
+    assert np.array_equal(tier.forward(0, x, two, w, -1), tier.forward(0, x, two, w, 2))
+    assert np.array_equal(tier.forward(0, x, three, w, -1), tier.forward(0, x, three, w, 0))
+    assert not np.array_equal(tier.forward(0, x, two, w, 2), tier.forward(0, x, two, w, 0))
