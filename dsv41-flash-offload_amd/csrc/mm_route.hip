@@ -157,6 +157,118 @@ __global__ __launch_bounds__(256) void k_router_gemv(const uint16_t* __restrict_
     }
 }
 
+// Prefill-sized router logits on MFMA (v_mfma_f32_16x16x32_bf16). The fp32 gate is split exactly into three bf16
+// parts, g = g1 + g2 + g3: g1 is g with its low 16 bits cleared (its top 8 significant bits), g2 the same of the
+// exact remainder g - g1, and g3 = g - g1 - g2, which has at most 8 significant bits; each product of a bf16 input
+// with a part is exact in fp32, so the MFMA's fp32 accumulation is the only rounding, as in an fp32 dot product
+// (in another order). A workgroup computes 64 tokens x 128 experts: per 32-row step the input tile and the gate
+// tile (split into the three bf16 planes on the way into LDS) are staged, the next step's loads are in flight
+// during the multiplies; wave (wm, wn) takes tokens 32 wm .. + 31 and experts 64 wn .. + 63 (2 x 4 tiles x 3 parts).
+constexpr int RM_TM = 64, RM_TN = 128, RM_K = 32;
+constexpr int RM_ROW = 40;            // LDS row stride in bf16 (80 bytes: the 16 rows of an operand read hit 16 bank groups)
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float rm_f4_t __attribute__((ext_vector_type(4)));
+
+__global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict__ x, const float* __restrict__ G,
+                                                     float* __restrict__ logits, int T, int H, int E)
+{
+    __shared__ __align__(16) uint16_t xs[RM_TM * RM_ROW];
+    __shared__ __align__(16) uint16_t gs[3][RM_TN * RM_ROW];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int t0 = blockIdx.y * RM_TM, e0 = blockIdx.x * RM_TN;
+    const int wm = wave >> 1, wn = wave & 1;
+    // this thread's loads of a step: one 16-byte chunk of the input tile (64 rows x 4 chunks), four of the gate tile
+    // (128 rows x 8 chunks of 4 floats); rows past T or E load zeros
+    const int xr = tid >> 2, xq = tid & 3;
+    const bool xin = t0 + xr < T;
+    const uint16_t* xp = x + (size_t)min(t0 + xr, T - 1) * H + 8 * xq;
+    int gr[4], gq[4];
+    bool gin[4];
+    const float* gp[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+    {
+        const int c = tid + 256 * j;
+        gr[j] = c >> 3;
+        gq[j] = c & 7;
+        gin[j] = e0 + gr[j] < E;
+        gp[j] = G + (size_t)min(e0 + gr[j], E - 1) * H + 4 * gq[j];
+    }
+    uint4 xv;
+    float4 gv[4];
+    auto load = [&](int k0) {
+        xv = xin ? *reinterpret_cast<const uint4*>(xp + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) gv[j] = gin[j] ? *reinterpret_cast<const float4*>(gp[j] + k0) : make_float4(0, 0, 0, 0);
+    };
+    auto split = [](float g, uint32_t& a, uint32_t& b, uint32_t& c) {
+        const uint32_t h1 = __float_as_uint(g) & 0xffff0000u;
+        const float r1 = g - __uint_as_float(h1);
+        const uint32_t h2 = __float_as_uint(r1) & 0xffff0000u;
+        const float r2 = r1 - __uint_as_float(h2);
+        a = h1 >> 16;
+        b = h2 >> 16;
+        c = __float_as_uint(r2) >> 16;
+    };
+    rm_f4_t acc[2][4];
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = rm_f4_t{ 0.f, 0.f, 0.f, 0.f };
+    const int S = H / RM_K;
+    load(0);
+    for (int s = 0; s < S; ++s)
+    {
+        __syncthreads();                                       // the previous step's operand reads are done
+        *reinterpret_cast<uint4*>(&xs[xr * RM_ROW + 8 * xq]) = xv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            uint32_t a[4], b[4], c[4];
+            split(gv[j].x, a[0], b[0], c[0]);
+            split(gv[j].y, a[1], b[1], c[1]);
+            split(gv[j].z, a[2], b[2], c[2]);
+            split(gv[j].w, a[3], b[3], c[3]);
+            const int o = gr[j] * RM_ROW + 4 * gq[j];
+            *reinterpret_cast<uint2*>(&gs[0][o]) = make_uint2(a[0] | (a[1] << 16), a[2] | (a[3] << 16));
+            *reinterpret_cast<uint2*>(&gs[1][o]) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
+            *reinterpret_cast<uint2*>(&gs[2][o]) = make_uint2(c[0] | (c[1] << 16), c[2] | (c[3] << 16));
+        }
+        __syncthreads();
+        if (s + 1 < S) load((s + 1) * RM_K);
+        bf16x8_t A[2], B[3][4];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            A[i] = *reinterpret_cast<const bf16x8_t*>(&xs[(32 * wm + 16 * i + (lane & 15)) * RM_ROW + 8 * (lane >> 4)]);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                B[p][j] = *reinterpret_cast<const bf16x8_t*>(&gs[p][(64 * wn + 16 * j + (lane & 15)) * RM_ROW + 8 * (lane >> 4)]);
+#pragma unroll
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int i = 0; i < 2; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B[p][j], acc[i][j], 0, 0, 0);
+    }
+    // D: lane (column l & 15, group l >> 4) holds rows 4 g .. 4 g + 3 of its column of each tile
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+        {
+            const int e = e0 + 64 * wn + 16 * j + (lane & 15);
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+            {
+                const int t = t0 + 32 * wm + 16 * i + 4 * (lane >> 4) + r;
+                if (t < T && e < E) logits[(size_t)t * E + e] = acc[i][j][r];
+            }
+        }
+}
+
 // One wave per token: k rounds of a wave-wide argmax (ties to the lower index), then softmax over the picks.
 __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ logits, int T, int E, int k,
                                                      int64_t* __restrict__ ids, float* __restrict__ w)
@@ -782,6 +894,9 @@ int mm_router_topk(const void* x_bf16, int T, int H, const float* gate, int E, i
     if (T <= RT_MAX_T && H % 256 == 0 && ((uintptr_t)x_bf16 & 7) == 0 && ((uintptr_t)gate & 15) == 0)
         hipLaunchKernelGGL(k_router_gemv, dim3((E + 3) / 4, (T + RT_TB - 1) / RT_TB), dim3(256), 0, S(stream),
                            (const uint16_t*)x_bf16, gate, logits, T, H, E);
+    else if (H % RM_K == 0 && ((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)gate & 15) == 0)
+        hipLaunchKernelGGL(k_router_mfma, dim3((E + RM_TN - 1) / RM_TN, (T + RM_TM - 1) / RM_TM), dim3(256), 0,
+                           S(stream), (const uint16_t*)x_bf16, gate, logits, T, H, E);
     else
         hipLaunchKernelGGL(k_router_logits, dim3((E + 63) / 64, (T + 63) / 64), dim3(256), 0, S(stream),
                            (const uint16_t*)x_bf16, gate, logits, T, H, E);

@@ -55,8 +55,10 @@ int mm_host_free(void* ptr);
  * logits[t][e] = sum_h x[t][h] * gate[e][h] (x bf16 [T][H], gate fp32 [E][H], fp32 sums);
  * ids[t][:k] = the k largest logits (ties -> lower expert id), w[t][:k] = softmax over those k logits.
  * logits fp32 [T][E] is written too (it is the kernels' workspace: required). Requires E <= 1024, k <= 32.
- * Up to 64 tokens (H a multiple of 256) one wave per expert sums lane partials; larger calls sum each logit in
- * ascending h: the last bits of a logit may differ between the two. */
+ * Up to 64 tokens (H a multiple of 256) one wave per expert sums lane partials; larger calls (H a multiple of 32)
+ * run on bf16 MFMA with the fp32 gate split exactly into three bf16 parts, so every product is exact in fp32 and
+ * the fp32 accumulation (in the matrix cores' order) is the only rounding; other shapes sum each logit in
+ * ascending h. The last bits of a logit may differ between the paths. */
 int mm_router_topk(const void* x_bf16, int T, int H, const float* gate, int E, int k, float* logits, int64_t* ids,
                    float* w, mm_stream_t stream);
 
