@@ -4,11 +4,11 @@
 // 128x128 GEMM).
 //
 // Launches: mm_permute (sorted positions) -> k_fat_prep (transformed inputs per sorted position) -> k_fat_plan
-// (expert records and the two tile lists) -> k_fat<0, 8>, k_fat<0, 4> (gate/up) -> k_fat<1, 8>, k_fat<1, 4> (down)
-// -> k_fat_combine.
+// (expert records and the two tile lists) -> k_fat<0, 8>, k_fat16<0, 2> (gate/up) -> k_fat16<1, 4>, k_fat16<1, 2>
+// (down) -> k_fat_combine.
 //
-// A workgroup (8 waves, two per SIMD) owns a tile of 256 routes (sorted positions of one expert; 128 for an
-// expert's last <= 128 routes) x 256 output columns:
+// A workgroup (k_fat: 8 waves, two per SIMD; k_fat16: 16 waves, four per SIMD) owns a tile of 256 routes (sorted
+// positions of one expert; 128 for an expert's last <= 128 routes) x 256 output columns:
 //   gate/up (MODE 0): gate columns 128 c .. 128 c + 127 and the same up columns, so the epilogue holds both and
 //                     applies the output transforms, SwiGLU and the down-input transform of that 128-block (the
 //                     transforms act within 128-blocks);
@@ -30,6 +30,7 @@ constexpr int FT_SMALL = 128;       // routes per tile for an expert's remainder
 constexpr int FT_BN = 256;          // output columns per tile
 constexpr int FT_WAVES = 8;
 constexpr int FT_THREADS = 64 * FT_WAVES;
+constexpr int FT16_THREADS = 1024;   // the sixteen-wave form
 constexpr int FT_PA = 3;            // input ring stages (loads run FT_PA - 1 steps ahead)
 constexpr int FT_PT = 5;            // trellis steps in flight
 constexpr int FT_TS = FT_PT + 1;    // trellis ring slots
@@ -330,6 +331,137 @@ __device__ __forceinline__ int chunk_slot(int q, int r)
     else return q ^ (((r >> 1) ^ (r >> 2)) & 3);
 }
 
+// Epilogue of a fat tile from the transposed fp16 C tile in LDS (column c at c * CS halves, the raw GEMM outputs
+// rounded to fp16): gate/up (MODE 0) applies the output transforms, SwiGLU and the down-input transform of the
+// tile's 128-block and writes the down input in operand order; down (MODE 1) applies the output transform of its
+// two 128-blocks and writes per-route rows. The C tile is complete (the caller's barrier) when this runs.
+template <int MODE, int CS, bool YH, int NW = FT_WAVES>
+__device__ __forceinline__ void fat_tile_epilogue(const FatArgs& a, const uint16_t* C, int rows, int pos0, int e,
+                                                  int nu, int wave, int lane)
+{
+    // Transforms in the layout of fwht128_lane8: per pass a wave takes 8 rows; lane (rpair, q, g) = (lane >> 4,
+    // (lane >> 2) & 3, lane & 3) holds rows r0 + 2 rpair and r0 + 2 rpair + 1 (one dword of the transposed tile per
+    // column) of the 8 columns lane8_k(lane, i) of each 128-block, so each butterfly stage is in-lane or a DPP
+    // exchange within 16 lanes.
+    const Lane8Signs sg = lane8_signs(lane);
+    const int rpair = lane >> 4;
+    int kk[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) kk[i] = lane8_k(lane, i);
+    // column c at rows r, r + 1 (r even)
+    auto rows2 = [&](int c, int r, float& v0, float& v1) {
+        const uint32_t d = *reinterpret_cast<const uint32_t*>(C + (size_t)c * CS + r);
+        v0 = h2f((uint16_t)(d & 0xffffu));
+        v1 = h2f((uint16_t)(d >> 16));
+    };
+    if constexpr (MODE == 0)
+    {
+        const int c0 = nu * 128;
+        const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c0;
+        const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c0;
+        const uint16_t* sd = a.suh2 + (size_t)e * a.I + c0;
+        float sgv[8], suv[8], sdv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+        {
+            sgv[i] = h2f(svg[kk[i]]);
+            suv[i] = h2f(svu[kk[i]]);
+            sdv[i] = h2f(sd[kk[i]]);
+        }
+        // operand order: the lane's 8 elements are positions 32 q + 8 g .. + 7 of the block, v[i] at + i
+        const int od = c0 + 32 * ((lane >> 2) & 3) + 8 * (lane & 3);
+        for (int r0 = 8 * wave; r0 < rows; r0 += 8 * NW)
+        {
+            const int r = r0 + 2 * rpair;
+            float gv[2][8], uv[2][8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+            {
+                rows2(kk[i], r, gv[0][i], gv[1][i]);
+                rows2(128 + kk[i], r, uv[0][i], uv[1][i]);
+            }
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2)
+            {
+                // the tile holds fp16 values, so the output transform's first rounding is exact
+                fwht128_lane8(gv[h2], sg);
+                fwht128_lane8(uv[h2], sg);
+                float xv[8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i)
+                {
+                    const float gg = r16((gv[h2][i] * HAD) * sgv[i]);
+                    const float uu = r16((uv[h2][i] * HAD) * suv[i]);
+                    xv[i] = r16(act_gu(gg, uu, a.limit)) * sdv[i];
+                }
+                fwht128_lane8(xv, sg);
+                if (r + h2 < rows)
+                {
+                    uint4 o;
+                    o.x = (uint32_t)f2h(xv[0] * HAD) | ((uint32_t)f2h(xv[1] * HAD) << 16);
+                    o.y = (uint32_t)f2h(xv[2] * HAD) | ((uint32_t)f2h(xv[3] * HAD) << 16);
+                    o.z = (uint32_t)f2h(xv[4] * HAD) | ((uint32_t)f2h(xv[5] * HAD) << 16);
+                    o.w = (uint32_t)f2h(xv[6] * HAD) | ((uint32_t)f2h(xv[7] * HAD) << 16);
+                    *reinterpret_cast<uint4*>(a.xd + (size_t)(pos0 + r + h2) * a.I + od) = o;
+                }
+            }
+        }
+    }
+    else
+    {
+        float svv[2][8];
+#pragma unroll
+        for (int hb = 0; hb < 2; ++hb)
+        {
+            const uint16_t* sv = a.svh2 + (size_t)e * a.H + (2 * nu + hb) * 128;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) svv[hb][i] = h2f(sv[kk[i]]);
+        }
+        for (int r0 = 8 * wave; r0 < rows; r0 += 8 * NW)
+        {
+            const int r = r0 + 2 * rpair;
+            // output rows of the lane's two routes (a row past the tile's routes is not stored)
+            const int y0 = r < rows ? a.route_at[pos0 + r] : 0;
+            const int y1 = r + 1 < rows ? a.route_at[pos0 + r + 1] : 0;
+#pragma unroll
+            for (int hb = 0; hb < 2; ++hb)
+            {
+                const int c0 = (2 * nu + hb) * 128;
+                float yv[2][8];
+#pragma unroll
+                for (int i = 0; i < 8; ++i) rows2(hb * 128 + kk[i], r, yv[0][i], yv[1][i]);
+#pragma unroll
+                for (int h2 = 0; h2 < 2; ++h2)
+                {
+                    fwht128_lane8(yv[h2], sg);
+#pragma unroll
+                    for (int i = 0; i < 8; ++i) yv[h2][i] = r16((yv[h2][i] * HAD) * svv[hb][i]);
+                    if (r + h2 < rows)
+                    {
+                        const size_t yo = (size_t)(h2 ? y1 : y0) * a.H + c0;
+                        // elements 2 p, 2 p + 1 are adjacent columns kk[2 p], kk[2 p] + 1
+#pragma unroll
+                        for (int p2 = 0; p2 < 4; ++p2)
+                        {
+                            if constexpr (YH)
+                            {
+                                // the output transform rounded y to fp16: the half stores are exact
+                                const uint32_t w2 = (uint32_t)f2h(yv[h2][2 * p2]) | ((uint32_t)f2h(yv[h2][2 * p2 + 1]) << 16);
+                                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.Y) + yo + kk[2 * p2]) = w2;
+                            }
+                            else
+                            {
+                                *reinterpret_cast<float2*>(a.Y + yo + kk[2 * p2]) =
+                                    make_float2(yv[h2][2 * p2], yv[h2][2 * p2 + 1]);
+                            }
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
 // MB = 16-row blocks per row-wave: tiles of BM = 32 MB routes (256 or 128). 8 waves: wave (wm, wn) = (w >> 2,
 // w & 3) multiplies row blocks wm, wm + 2, wm + 4, ... (rows 16 (2 i + wm) .. + 15) by column tiles 4 wn .. 4 wn + 3
 // of 16, so in a tile with fewer routes the two waves of a SIMD keep about the same number of row blocks
@@ -575,127 +707,218 @@ __global__ __launch_bounds__(FT_THREADS, 1) void k_fat(FatArgs a)
             d[1] = (uint32_t)f2h(acc[i][j][2]) | ((uint32_t)f2h(acc[i][j][3]) << 16);
         }
     __syncthreads();
-    // Transforms in the layout of fwht128_lane8: per pass a wave takes 8 rows; lane (rpair, q, g) = (lane >> 4,
-    // (lane >> 2) & 3, lane & 3) holds rows r0 + 2 rpair and r0 + 2 rpair + 1 (one dword of the transposed tile per
-    // column) of the 8 columns lane8_k(lane, i) of each 128-block, so each butterfly stage is in-lane or a DPP
-    // exchange within 16 lanes.
-    const Lane8Signs sg = lane8_signs(lane);
-    const int rpair = lane >> 4;
-    int kk[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) kk[i] = lane8_k(lane, i);
-    // column c at rows r, r + 1 (r even)
-    auto rows2 = [&](int c, int r, float& v0, float& v1) {
-        const uint32_t d = *reinterpret_cast<const uint32_t*>(C + (size_t)c * CS + r);
-        v0 = h2f((uint16_t)(d & 0xffffu));
-        v1 = h2f((uint16_t)(d >> 16));
+    fat_tile_epilogue<MODE, CS, YH>(a, C, rows, pos0, e, nu, wave, lane);
+}
+
+// Sixteen-wave form of the tile (four waves per SIMD, 64 accumulators per lane): MBW = row blocks per wave, BM =
+// 64 MBW routes (256 or 128). Wave (wm, wn) = (w >> 2, w & 3) multiplies row blocks wm, wm + 4, ... (rows
+// 16 (4 i + wm) .. + 15) by column tiles 4 wn .. 4 wn + 3, so each SIMD (waves w, w + 4, w + 8, w + 12) holds
+// one column group over every row block of the tile. Inputs: buffer-to-LDS, two steps ahead in a three-stage ring,
+// input load li of a step (1 KB) issued by wave li % 16; trellis as k_fat (waves 0 .. 3); wave w decodes column
+// tile w & 7 of sub-block w >> 3 in both tile rows (one 16-byte store per lane and step).
+template <int MODE, int MBW, bool YH = false>
+__global__ __launch_bounds__(FT16_THREADS, 1) void k_fat16(FatArgs a)
+{
+    constexpr int NW = 16;
+    constexpr int BM = 64 * MBW;
+    constexpr int NA = MODE == 0 ? 2 : 1;
+    constexpr int SEG = NA * 64;
+    constexpr int A_STAGE = BM * SEG;
+    constexpr int NL = A_STAGE / 1024;                           // input loads of a step
+    constexpr int T_SLOT = 4 * 1024;
+    constexpr int B_BUF = 16 * 64 * 16;
+    constexpr int A_BYTES = FT_PA * A_STAGE, T_BYTES = FT_TS * T_SLOT;
+    constexpr int MAIN = A_BYTES + T_BYTES + 2 * B_BUF;
+    constexpr int CS = BM + 2;
+    constexpr int SMEM = MAIN > FT_BN * CS * 2 ? MAIN : FT_BN * CS * 2;
+    static_assert(SMEM <= 160 * 1024, "LDS");
+    static_assert(((CS / 2) & 1) == 1, "odd dword stride: conflict-free column reads");
+    static_assert(NL >= 4 && NL <= 2 * NW, "the trellis loaders also load inputs; at most two input loads per wave");
+    __shared__ __align__(16) uint8_t smem[SMEM];
+    uint8_t* Aring = smem;
+    uint8_t* Tring = smem + A_BYTES;
+    uint8_t* Bdec = smem + A_BYTES + T_BYTES;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int nact = min(a.nactive[0], a.max_active);
+    const int total = a.tile_off[nact];
+    const int work = total * a.nunits, per_xcd = (work + 7) >> 3;
+    const int L = (int)(blockIdx.x & 7) * per_xcd + (int)(blockIdx.x >> 3);
+    if ((int)(blockIdx.x >> 3) >= per_xcd || L >= work) return;
+    const int mt = L / a.nunits, nu = L % a.nunits;
+    int lo = 0, hi = nact - 1;
+    while (lo < hi)
+    {
+        const int mid = (lo + hi + 1) >> 1;
+        if (a.tile_off[mid] <= mt) lo = mid; else hi = mid - 1;
+    }
+    const ExpertRec* rp = a.rec + lo;
+    const int row0 = BM == FT_BIG ? (mt - a.tile_off[lo]) * BM : (a.big_off[lo + 1] - a.big_off[lo]) * FT_BIG;
+    const int rows = __builtin_amdgcn_readfirstlane(min(BM, rp->cnt - row0));
+    const int pos0 = __builtin_amdgcn_readfirstlane(rp->first + row0);
+    const int e = __builtin_amdgcn_readfirstlane(rp->e);
+    const int S = a.K / 32;
+
+    auto uniform_ptr = [](const void* p) {
+        const uint64_t v = (uint64_t)(uintptr_t)p;
+        const uint32_t l = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)v);
+        const uint32_t h = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(v >> 32));
+        return reinterpret_cast<void*>((uintptr_t)((uint64_t)l | ((uint64_t)h << 32)));
     };
-    if constexpr (MODE == 0)
+    const bool tloader = wave < 4;
+    const int tq = wave & 3;
+    const uint32_t row_bytes = (uint32_t)(a.N / 16) * 96, wbytes = (uint32_t)(a.K / 16) * row_bytes;
+    const void* wbase = (const void*)(uintptr_t)(MODE == 0 ? ((tq & 1) ? rp->w[1] : rp->w[0]) : rp->w[2]);
+    const __amdgpu_buffer_rsrc_t wres = __builtin_amdgcn_make_buffer_rsrc(uniform_ptr(wbase), (short)0, (int)wbytes,
+                                                                          0x00020000);
+    const uint32_t wcol = MODE == 0 ? (uint32_t)nu * 768 : (uint32_t)(2 * nu + (tq & 1)) * 768;
+    auto load_trellis = [&](int s) {
+        const uint32_t tr = (uint32_t)(2 * min(s, S - 1) + (tq >> 1));
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(wres, Tring + (size_t)(s % FT_TS) * T_SLOT + (size_t)tq * 1024, 12,
+                                                 tr * row_bytes + wcol + (uint32_t)lane * 12, 0, 0, 0);
+    };
+    const uint32_t a_row = (uint32_t)NA * a.K * 2;
+    const __amdgpu_buffer_rsrc_t ares = __builtin_amdgcn_make_buffer_rsrc(
+        uniform_ptr(a.xa + (size_t)pos0 * NA * a.K), (short)0, (int)((uint32_t)rows * a_row), 0x00020000);
+    // input load li = wave + 16 u of a step; this wave issues na of them (uniform)
+    const int na = wave < NL ? (wave + NW < NL ? 2 : 1) : 0;
+    auto load_input = [&](int s, int u) {
+        const int st = s % FT_PA;
+        const uint32_t ks = s < S ? (uint32_t)s * SEG : 0x40000000u;
+        const int li = wave + NW * u;
+        const int r = li * (1024 / SEG) + lane / (SEG / 16), slot = lane % (SEG / 16);
+        const uint32_t voff = (uint32_t)r * a_row + (uint32_t)chunk_slot<NA>(slot, r) * 16 + ks;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(ares, Aring + (size_t)st * A_STAGE + (size_t)li * 1024, 16, voff, 0, 0, 0);
+    };
+    auto load_inputs = [&](int s) {
+        if (na > 0) load_input(s, 0);
+        if (na > 1) load_input(s, 1);
+    };
+
+    const int col = lane & 15, g = lane >> 4;
+    const int i0 = 32 * (col & 7) + 8 * g + 4 * (col >> 3);
+    const int eb = 3 * i0 + 11;
+    const int blo = eb >> 5, bhi = (blo + 23) % 24;
+    const int llo = 4 * (blo / 3) + blo % 3, lhi = 4 * (bhi / 3) + bhi % 3;
+    const uint32_t sh = 31u - (uint32_t)(eb & 31);
+    const int db = wave >> 3, dc = wave & 7;
+    const uint32_t* tword = reinterpret_cast<const uint32_t*>(Tring + (size_t)db * 1024 + (size_t)dc * 128);
+    uint8_t* bdst = Bdec + ((size_t)(db * 8 + dc) * 64 + lane) * 16;
+    const int wm = wave >> 2, wn = wave & 3;
+    const uint8_t* bsrc = Bdec + ((size_t)(wn * 4) * 64 + lane) * 16;
+    int aoff[MBW];
+#pragma unroll
+    for (int i = 0; i < MBW; ++i)
     {
-        const int c0 = nu * 128;
-        const uint16_t* svg = a.svh13 + ((size_t)e * 2 + 0) * a.I + c0;
-        const uint16_t* svu = a.svh13 + ((size_t)e * 2 + 1) * a.I + c0;
-        const uint16_t* sd = a.suh2 + (size_t)e * a.I + c0;
-        float sgv[8], suv[8], sdv[8];
-#pragma unroll
-        for (int i = 0; i < 8; ++i)
-        {
-            sgv[i] = h2f(svg[kk[i]]);
-            suv[i] = h2f(svu[kk[i]]);
-            sdv[i] = h2f(sd[kk[i]]);
-        }
-        // operand order: the lane's 8 elements are positions 32 q + 8 g .. + 7 of the block, v[i] at + i
-        const int od = c0 + 32 * ((lane >> 2) & 3) + 8 * (lane & 3);
-        for (int r0 = 8 * wave; r0 < rows; r0 += 8 * FT_WAVES)
-        {
-            const int r = r0 + 2 * rpair;
-            float gv[2][8], uv[2][8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-            {
-                rows2(kk[i], r, gv[0][i], gv[1][i]);
-                rows2(128 + kk[i], r, uv[0][i], uv[1][i]);
-            }
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2)
-            {
-                // the tile holds fp16 values, so the output transform's first rounding is exact
-                fwht128_lane8(gv[h2], sg);
-                fwht128_lane8(uv[h2], sg);
-                float xv[8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i)
-                {
-                    const float gg = r16((gv[h2][i] * HAD) * sgv[i]);
-                    const float uu = r16((uv[h2][i] * HAD) * suv[i]);
-                    xv[i] = r16(act_gu(gg, uu, a.limit)) * sdv[i];
-                }
-                fwht128_lane8(xv, sg);
-                if (r + h2 < rows)
-                {
-                    uint4 o;
-                    o.x = (uint32_t)f2h(xv[0] * HAD) | ((uint32_t)f2h(xv[1] * HAD) << 16);
-                    o.y = (uint32_t)f2h(xv[2] * HAD) | ((uint32_t)f2h(xv[3] * HAD) << 16);
-                    o.z = (uint32_t)f2h(xv[4] * HAD) | ((uint32_t)f2h(xv[5] * HAD) << 16);
-                    o.w = (uint32_t)f2h(xv[6] * HAD) | ((uint32_t)f2h(xv[7] * HAD) << 16);
-                    *reinterpret_cast<uint4*>(a.xd + (size_t)(pos0 + r + h2) * a.I + od) = o;
-                }
-            }
-        }
+        const int r = 16 * (4 * i + wm) + col;
+        aoff[i] = r * SEG + chunk_slot<NA>((MODE == 0 ? (wn >> 1) : 0) * 4 + g, r) * 16;
     }
+    float4_t acc[MBW][4];
+#pragma unroll
+    for (int i = 0; i < MBW; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = float4_t{ 0.f, 0.f, 0.f, 0.f };
+
+    // Issue order per wave: inputs of step 0, [trellis of steps 0 .. FT_PT - 1], inputs of step 1, then in step s
+    // [the trellis of step s + FT_PT] and the inputs of step s + 2 ([..] = waves 0 .. 3). At the top of step s the
+    // wave's inputs of step s are complete once at most na (+ 1) loads are outstanding (what step s - 1 issued
+    // after them; step 0: more came after); the trellis of step s + 1 was issued before them.
+    auto wait_step = [&]() {
+        const int k = na + (tloader ? 1 : 0);
+        if (k >= 3) wait_vmcnt<3>();
+        else if (k == 2) wait_vmcnt<2>();
+        else if (k == 1) wait_vmcnt<1>();
+        else if (na == 0 && tloader) wait_vmcnt<FT_PT - 2>();
+    };
+    load_inputs(0);
+    asm volatile("" ::: "memory");
+    if (tloader)
+        for (int s = 0; s < FT_PT; ++s) load_trellis(s);
+    asm volatile("" ::: "memory");
+    load_inputs(1);
+    if (tloader)
+    {
+        if (na == 2) wait_vmcnt<2 + FT_PT - 1>();
+        else wait_vmcnt<1 + FT_PT - 1>();
+    }
+    lds_barrier();
+    {
+        const half4_t r0 = decode4<true>(tword[lhi], tword[llo], sh);
+        const half4_t r1 = decode4<true>(tword[512 + lhi], tword[512 + llo], sh);
+        *reinterpret_cast<half8_t*>(bdst) = half8_t{ r0[0], r0[1], r0[2], r0[3], r1[0], r1[1], r1[2], r1[3] };
+    }
+    const int nb16 = (rows + 15) >> 4;
+    const int nvb = max(0, min(MBW, (nb16 - wm + 3) >> 2));
+    auto main_loop = [&](auto part_tag) {
+        constexpr bool PART = decltype(part_tag)::value;
+        for (int s = 0; s < S; ++s)
+        {
+            wait_step();
+            lds_barrier();
+            if (tloader) load_trellis(s + FT_PT);
+            const uint32_t toff = (uint32_t)__builtin_amdgcn_readfirstlane(((s + 1) % FT_TS) * T_SLOT);
+            const uint8_t* thp = reinterpret_cast<const uint8_t*>(tword + lhi) + toff;
+            const uint8_t* tlp = reinterpret_cast<const uint8_t*>(tword + llo) + toff;
+            const uint32_t th0 = *reinterpret_cast<const uint32_t*>(thp), tl0 = *reinterpret_cast<const uint32_t*>(tlp);
+            const uint32_t th1 = *reinterpret_cast<const uint32_t*>(thp + 2048);
+            const uint32_t tl1 = *reinterpret_cast<const uint32_t*>(tlp + 2048);
+            const uint8_t* as = Aring + (size_t)(s % FT_PA) * A_STAGE;
+            const uint8_t* bs = bsrc + (size_t)(s & 1) * B_BUF;
+            uint8_t* bd = bdst + (size_t)((s + 1) & 1) * B_BUF;
+            half8_t B[4], A[MBW];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) B[j] = *reinterpret_cast<const half8_t*>(bs + j * 1024);
+#pragma unroll
+            for (int i = 0; i < MBW; ++i)
+                if (!PART || i < nvb) A[i] = *reinterpret_cast<const half8_t*>(as + aoff[i]);
+            const half4_t d0 = decode4<true>(th0, tl0, sh);
+#pragma unroll
+            for (int i = 0; i < MBW; ++i)
+            {
+                if (!PART || i < nvb)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(A[i], B[j], acc[i][j], 0, 0, 0);
+                if (i == 0) load_inputs(s + FT_PA - 1);
+                if (i == MBW / 2 - 1)
+                {
+                    const half4_t d1 = decode4<true>(th1, tl1, sh);
+                    *reinterpret_cast<half8_t*>(bd) = half8_t{ d0[0], d0[1], d0[2], d0[3], d1[0], d1[1], d1[2], d1[3] };
+                }
+            }
+            if constexpr (!PART)
+            {
+                __builtin_amdgcn_sched_group_barrier(0x0100, 4 + MBW + 4, 0);
+                __builtin_amdgcn_sched_group_barrier(0x0002, 8, 0);
+#pragma unroll
+                for (int k = 0; k < 4 * MBW; ++k)
+                {
+                    __builtin_amdgcn_sched_group_barrier(0x0008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x0002, 1, 0);
+                }
+            }
+        }
+    };
+    if (nvb == MBW)
+        main_loop(std::false_type{});
     else
-    {
-        float svv[2][8];
+        main_loop(std::true_type{});
+    wait_vmcnt<0>();
+    lds_barrier();
+
+    uint16_t* C = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
-        for (int hb = 0; hb < 2; ++hb)
+    for (int i = 0; i < MBW; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
         {
-            const uint16_t* sv = a.svh2 + (size_t)e * a.H + (2 * nu + hb) * 128;
-#pragma unroll
-            for (int i = 0; i < 8; ++i) svv[hb][i] = h2f(sv[kk[i]]);
+            const int c = (wn * 4 + j) * 16 + col, r = 16 * (4 * i + wm) + 4 * g;
+            uint32_t* d = reinterpret_cast<uint32_t*>(C + (size_t)c * CS + r);
+            d[0] = (uint32_t)f2h(acc[i][j][0]) | ((uint32_t)f2h(acc[i][j][1]) << 16);
+            d[1] = (uint32_t)f2h(acc[i][j][2]) | ((uint32_t)f2h(acc[i][j][3]) << 16);
         }
-        for (int r0 = 8 * wave; r0 < rows; r0 += 8 * FT_WAVES)
-        {
-            const int r = r0 + 2 * rpair;
-            // output rows of the lane's two routes (a row past the tile's routes is not stored)
-            const int y0 = r < rows ? a.route_at[pos0 + r] : 0;
-            const int y1 = r + 1 < rows ? a.route_at[pos0 + r + 1] : 0;
-#pragma unroll
-            for (int hb = 0; hb < 2; ++hb)
-            {
-                const int c0 = (2 * nu + hb) * 128;
-                float yv[2][8];
-#pragma unroll
-                for (int i = 0; i < 8; ++i) rows2(hb * 128 + kk[i], r, yv[0][i], yv[1][i]);
-#pragma unroll
-                for (int h2 = 0; h2 < 2; ++h2)
-                {
-                    fwht128_lane8(yv[h2], sg);
-#pragma unroll
-                    for (int i = 0; i < 8; ++i) yv[h2][i] = r16((yv[h2][i] * HAD) * svv[hb][i]);
-                    if (r + h2 < rows)
-                    {
-                        const size_t yo = (size_t)(h2 ? y1 : y0) * a.H + c0;
-                        // elements 2 p, 2 p + 1 are adjacent columns kk[2 p], kk[2 p] + 1
-#pragma unroll
-                        for (int p2 = 0; p2 < 4; ++p2)
-                        {
-                            if constexpr (YH)
-                            {
-                                // the output transform rounded y to fp16: the half stores are exact
-                                const uint32_t w2 = (uint32_t)f2h(yv[h2][2 * p2]) | ((uint32_t)f2h(yv[h2][2 * p2 + 1]) << 16);
-                                *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(a.Y) + yo + kk[2 * p2]) = w2;
-                            }
-                            else
-                            {
-                                *reinterpret_cast<float2*>(a.Y + yo + kk[2 * p2]) =
-                                    make_float2(yv[h2][2 * p2], yv[h2][2 * p2 + 1]);
-                            }
-                        }
-                    }
-                }
-            }
-        }
-    }
+    __syncthreads();
+    fat_tile_epilogue<MODE, CS, YH, NW>(a, C, rows, pos0, e, nu, wave, lane);
 }
 
 // Weighted combine of the fat routes: out[t] = (accumulate ? out[t] : 0) + sum_j w_j y_j over the routes j of
@@ -956,22 +1179,26 @@ static int fat_gemms(const mm_layer_t* L, int n, int cap, const FatWs& ws, hipSt
                L->H, L->I, L->H, L->I, L->I / 128, na, L->limit };
     FatArgs gs = g;
     gs.tile_off = ws.off_small;
-    if (max_big > 0) hipLaunchKernelGGL((k_fat<0, FT_BIG / 32>), grid(max_big, g.nunits), dim3(FT_THREADS), 0, s, g);
-    hipLaunchKernelGGL((k_fat<0, FT_SMALL / 32>), grid(max_small, g.nunits), dim3(FT_THREADS), 0, s, gs);
     FatArgs d = g;
     d.xa = ws.xd; d.K = L->I; d.N = L->H; d.nunits = L->H / 256;
     FatArgs ds = d;
     ds.tile_off = ws.off_small;
+    // gate/up: 256-route tiles on the 8-wave kernel, 128-route tiles and the down GEMM on the 16-wave kernel (same
+    // bits; measured on the 16k layer: gate/up 256-route tiles equal, 128-route tiles 97 against 111 us, down
+    // 2.76-2.85 against 2.92-2.94 ms)
+    if (max_big > 0) hipLaunchKernelGGL((k_fat<0, FT_BIG / 32>), grid(max_big, g.nunits), dim3(FT_THREADS), 0, s, g);
+    hipLaunchKernelGGL((k_fat16<0, FT_SMALL / 64>), grid(max_small, g.nunits), dim3(FT16_THREADS), 0, s, gs);
     if (yh)
     {
         if (max_big > 0)
-            hipLaunchKernelGGL((k_fat<1, FT_BIG / 32, true>), grid(max_big, d.nunits), dim3(FT_THREADS), 0, s, d);
-        hipLaunchKernelGGL((k_fat<1, FT_SMALL / 32, true>), grid(max_small, d.nunits), dim3(FT_THREADS), 0, s, ds);
+            hipLaunchKernelGGL((k_fat16<1, FT_BIG / 64, true>), grid(max_big, d.nunits), dim3(FT16_THREADS), 0, s, d);
+        hipLaunchKernelGGL((k_fat16<1, FT_SMALL / 64, true>), grid(max_small, d.nunits), dim3(FT16_THREADS), 0, s, ds);
     }
     else
     {
-        if (max_big > 0) hipLaunchKernelGGL((k_fat<1, FT_BIG / 32>), grid(max_big, d.nunits), dim3(FT_THREADS), 0, s, d);
-        hipLaunchKernelGGL((k_fat<1, FT_SMALL / 32>), grid(max_small, d.nunits), dim3(FT_THREADS), 0, s, ds);
+        if (max_big > 0)
+            hipLaunchKernelGGL((k_fat16<1, FT_BIG / 64>), grid(max_big, d.nunits), dim3(FT16_THREADS), 0, s, d);
+        hipLaunchKernelGGL((k_fat16<1, FT_SMALL / 64>), grid(max_small, d.nunits), dim3(FT16_THREADS), 0, s, ds);
     }
     return check_launch("fat path");
 }
