@@ -294,6 +294,43 @@ def cpu_baseline(L=40, T=4):
 
 # ------------------------------------------------------------------------------------------ GPU legs
 
+def start_cache_child(args):
+    """The capacity-limited cache leg runs in a child process of its own, started here before this process touches
+    the GPU: it waits on its stdin until the parent's GPU legs are done, then runs the leg and prints its JSON line.
+    A failure of the leg (an exception, a signal) then costs that leg only; the parent reports it and still prints
+    its line."""
+    cmd = [sys.executable, "-u", os.path.abspath(__file__), "--workload", "cache", "--cache-child",
+           "--slots", str(args.slots), "--cache-steps", str(args.cache_steps), "--chunk-every", str(args.chunk_every),
+           "--chunk-tokens", str(args.chunk_tokens), "--home-layers", str(args.home_layers),
+           "--ec-warmup", str(args.ec_warmup), "--cache-warmup", str(args.cache_warmup),
+           "--hyb-tokens", str(args.hyb_tokens)]
+    if not args.cpu_tier:
+        cmd.append("--no-cpu-tier")
+
+    def die_with_parent():                          # PR_SET_PDEATHSIG: the leg ends if this process does
+        import signal
+        ctypes.CDLL(None, use_errno=True).prctl(1, signal.SIGKILL, 0, 0, 0)
+    return subprocess.Popen(cmd, stdin=subprocess.PIPE, stdout=subprocess.PIPE, text=True, preexec_fn=die_with_parent)
+
+
+def run_cache_child(p, timeout_s=900):
+    """Releases the waiting cache-leg child and returns its "cache" object, or a record of how it failed."""
+    t0 = time.time()
+    try:
+        out, _ = p.communicate(input="go\n", timeout=timeout_s)
+    except subprocess.TimeoutExpired:
+        p.kill()
+        p.wait()
+        return {"error": f"timed out after {timeout_s} s", "process": "child"}
+    lines = [l for l in out.splitlines() if l.startswith("{")]
+    if p.returncode != 0 or not lines:
+        return {"error": f"child exited with status {p.returncode}", "process": "child",
+                "wall_s": round(time.time() - t0, 1)}
+    r = json.loads(lines[-1])["cache"]
+    r["process"] = "child"
+    return r
+
+
 def free_gpu():
     import torch
     gc.collect()
@@ -391,6 +428,32 @@ def decode_step(stores, E, H, I, K, T, L, steps, warmup, roofline):
 
         g_gu, g_d = kernel_graph(2), kernel_graph(8)
         res["t_gu"], res["t_d"] = time_graph(g_gu), time_graph(g_d)
+
+        # the same launches inside the step: the step's kernels launched eagerly, layer by layer in the step's order
+        # (route prep with the rescale, gate/up partial sums, epilogue, down partial sums, down epilogue, combine),
+        # with events recorded on the stream right before and after each gate/up launch
+        def eager_step(evs):
+            src = x0
+            for l in range(L):
+                R = runners[l]
+                R.experts(stores[l], x=src, phases=1, rescale=True)
+                if evs is not None:
+                    evs[l][0].record()
+                R.experts(stores[l], x=src, phases=2)
+                if evs is not None:
+                    evs[l][1].record()
+                R.experts(stores[l], x=src, phases=4 | 8 | 16)
+                src = R.combine(out=outs[l % 2])
+
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(L)]
+        eager_step(None)
+        torch.cuda.synchronize()
+        per = []
+        for _ in range(3):
+            eager_step(evs)
+            torch.cuda.synchronize()
+            per += [a.elapsed_time(b) for a, b in evs]
+        res["t_gu_in_step"] = float(np.mean(per))
         bgu = 2 * trellis_bytes(H, I) + 2 * H * 2          # gate/up partial kernel: trellis + suh13 per expert
         res["bytes_gu"] = float(np.mean([(u + 1) * bgu for u in uniq]))
         res["bytes_d"] = float(np.mean([(u + 1) * trellis_bytes(I, H) for u in uniq]))
@@ -849,16 +912,23 @@ def main():
                     help="cache leg: the lone prefill step timed with and without the host tier's tail batches "
                          "(DSV41_CT_HYB_MAX; 0 = not timed)")
     ap.add_argument("--cpu-child", default=None, help=argparse.SUPPRESS)
+    ap.add_argument("--cache-child", action="store_true", help=argparse.SUPPRESS)
     args = ap.parse_args()
     if args.cpu_child is not None:
         return cpu_child(args.cpu_child)
+    if args.cache_child and sys.stdin.readline().strip() != "go":
+        return                                      # the parent ended before releasing this leg
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(f"bench.py: measures one MI355X only (got --gpus {args.gpus}, WORLD_SIZE {world}); the multi-GPU "
               "expert-parallel design is documented but not built, so N > 1 is not run.", flush=True)
         sys.exit(2)
 
-    # the CPU baseline runs first, in child processes, before this process touches the GPU
+    # the cache leg's process starts (and waits) and the CPU baseline runs, in child processes, before this process
+    # touches the GPU
+    cache_child = None
+    if args.workload == "decode" and not args.no_cache and args.layers == 40:
+        cache_child = start_cache_child(args)
     cpu = None
     if args.workload == "decode" and not args.no_cpu_baseline:
         log("cpu baseline: reference CPU tier")
@@ -936,10 +1006,11 @@ def main():
         free_gpu()
 
     cache_res = None
-    if not args.no_cache and L == 40:
-        log(f"cache: capacity-limited configuration, {args.cache_steps} steps")
-        cache_res = bench_cache(args)
+    if cache_child is not None:
+        log(f"cache: capacity-limited configuration, {args.cache_steps} steps (child process)")
         free_gpu()
+        cache_res = run_cache_child(cache_child)
+        log(f"cache: {cache_res.get('error', 'done')}")
 
     res = {
         "metric": METRIC,
@@ -962,7 +1033,11 @@ def main():
                      "frac": round(gu_gbs / HBM_PEAK_GBS, 4), "traffic": traffic_bytes(L, T),
                      "kernel": "mm::k_partial<0> (gate/up decode GEMV partial sums)",
                      "avg_launch_us": round(float(d4["t_gu"]) * 1e3, 2),
-                     "bytes_per_launch": round(float(d4["bytes_gu"]), 1)},
+                     "bytes_per_launch": round(float(d4["bytes_gu"]), 1),
+                     "in_step": {"avg_launch_us": round(float(d4["t_gu_in_step"]) * 1e3, 2),
+                                 "achieved": round(d4["bytes_gu"] / (d4["t_gu_in_step"] * 1e-3) / 1e9, 1),
+                                 "frac": round(d4["bytes_gu"] / (d4["t_gu_in_step"] * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                                 "method": "the step launched eagerly, events around each layer's gate/up launch"}},
         "step_hbm": {"bytes_per_step": d4["step_bytes"], "achieved_gbs": round(step_gbs, 1),
                      "frac_of_peak": round(step_gbs / HBM_PEAK_GBS, 4),
                      "down_kernel_gbs": round(d_gbs, 1), "down_avg_launch_us": round(float(d4["t_d"]) * 1e3, 2)},
