@@ -110,41 +110,79 @@ __global__ __launch_bounds__(256) void k_router_logits(const uint16_t* __restric
         }
 }
 
-// Decode-sized router logits: one wave per expert streams its gate row (16-byte loads) against up to RT_TB tokens
-// at a time (8-byte bf16 loads; the rows of a few tokens stay in L2 for every wave), lane partials in fp32, then a
-// wave sum. A launch of 64 x 64 tiles would give a 4-token call only E / 64 workgroups.
-constexpr int RT_TB = 16;
+// Decode-sized router logits: one workgroup per expert (and TB tokens), its 4 waves take interleaved 256-element
+// chunks of the gate row (16-byte loads; chunk c by wave c % 4), four chunks' loads issued before any is used, the
+// x rows (8-byte bf16 loads of TB tokens; they stay in L2 for every expert) with them; lane partials in fp32, a
+// wave sum per token, then the 4 waves' sums added in wave order. A launch of 64 x 64 tiles would give a 4-token
+// call only E / 64 workgroups, and one wave per expert walking its row chunk by chunk waits a memory round trip per
+// chunk.
 constexpr int RT_MAX_T = 64;
 
+template <int TB>
 __global__ __launch_bounds__(256) void k_router_gemv(const uint16_t* __restrict__ x, const float* __restrict__ G,
                                                      float* __restrict__ logits, int T, int H, int E)
 {
-    const int lane = threadIdx.x & 63;
-    const int e = blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int t0 = blockIdx.y * RT_TB;
-    if (e >= E) return;                                    // the whole wave
-    const int nt = min(RT_TB, T - t0);
-    float acc[RT_TB];
+    __shared__ float part[4][TB];
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+    const int e = blockIdx.x;
+    const int t0 = blockIdx.y * TB;
+    const int nt = min(TB, T - t0);
+    const int nch = H / 256;
+    float acc[TB];
 #pragma unroll
-    for (int t = 0; t < RT_TB; ++t) acc[t] = 0.0f;
+    for (int t = 0; t < TB; ++t) acc[t] = 0.0f;
     const float4* g = reinterpret_cast<const float4*>(G + (size_t)e * H);
     auto bf = [](uint32_t b) { return __builtin_bit_cast(float, b << 16); };
-    for (int h = lane * 4; h < H; h += 256)
+    // tokens past nt read the last valid row (never stored), chunks past the row reload the last chunk (not added)
+    auto xrow = [&](int t, int c) {
+        return *reinterpret_cast<const uint2*>(x + (size_t)(t0 + min(t, nt - 1)) * H + (size_t)c * 256 + lane * 4);
+    };
+    for (int c0 = wv; c0 < nch; c0 += 16)
     {
-        const float4 gv = g[h >> 2];
+        float4 gv[4];
 #pragma unroll
-        for (int t = 0; t < RT_TB; ++t)
-            if (t < nt)
+        for (int u = 0; u < 4; ++u) gv[u] = g[(size_t)min(c0 + 4 * u, nch - 1) * 64 + lane];
+        if constexpr (TB <= 4)
+        {
+            uint2 xr[4][TB];
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+#pragma unroll
+                for (int t = 0; t < TB; ++t) xr[u][t] = xrow(t, min(c0 + 4 * u, nch - 1));
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
+                if (c0 + 4 * u < nch)
+#pragma unroll
+                    for (int t = 0; t < TB; ++t)
+                    {
+                        acc[t] = fmaf(bf(xr[u][t].x & 0xffffu), gv[u].x, acc[t]);
+                        acc[t] = fmaf(bf(xr[u][t].x >> 16), gv[u].y, acc[t]);
+                        acc[t] = fmaf(bf(xr[u][t].y & 0xffffu), gv[u].z, acc[t]);
+                        acc[t] = fmaf(bf(xr[u][t].y >> 16), gv[u].w, acc[t]);
+                    }
+        }
+        else
+        {
+#pragma unroll
+            for (int u = 0; u < 4; ++u)
             {
-                const uint2 xr = *reinterpret_cast<const uint2*>(x + (size_t)(t0 + t) * H + h);
-                acc[t] = fmaf(bf(xr.x & 0xffffu), gv.x, acc[t]);
-                acc[t] = fmaf(bf(xr.x >> 16), gv.y, acc[t]);
-                acc[t] = fmaf(bf(xr.y & 0xffffu), gv.z, acc[t]);
-                acc[t] = fmaf(bf(xr.y >> 16), gv.w, acc[t]);
+                uint2 xr[TB];
+#pragma unroll
+                for (int t = 0; t < TB; ++t) xr[t] = xrow(t, min(c0 + 4 * u, nch - 1));
+                if (c0 + 4 * u < nch)
+#pragma unroll
+                    for (int t = 0; t < TB; ++t)
+                    {
+                        acc[t] = fmaf(bf(xr[t].x & 0xffffu), gv[u].x, acc[t]);
+                        acc[t] = fmaf(bf(xr[t].x >> 16), gv[u].y, acc[t]);
+                        acc[t] = fmaf(bf(xr[t].y & 0xffffu), gv[u].z, acc[t]);
+                        acc[t] = fmaf(bf(xr[t].y >> 16), gv[u].w, acc[t]);
+                    }
             }
+        }
     }
 #pragma unroll
-    for (int t = 0; t < RT_TB; ++t)
+    for (int t = 0; t < TB; ++t)
     {
         float v = acc[t];
         v += xor_lane<32>(v);
@@ -153,8 +191,11 @@ __global__ __launch_bounds__(256) void k_router_gemv(const uint16_t* __restrict_
         v += xor_lane<4>(v);
         v += xor_lane<2>(v);
         v += xor_lane<1>(v);
-        if (lane == 0 && t < nt) logits[(size_t)(t0 + t) * E + e] = v;
+        if (lane == 0) part[wv][t] = v;
     }
+    __syncthreads();
+    if (wv == 0 && lane < nt)
+        logits[(size_t)(t0 + lane) * E + e] = ((part[0][lane] + part[1][lane]) + part[2][lane]) + part[3][lane];
 }
 
 // Prefill-sized router logits on MFMA (v_mfma_f32_16x16x32_bf16). The fp32 gate is split exactly into three bf16
@@ -319,6 +360,87 @@ __global__ __launch_bounds__(256) void k_router_topk(const float* __restrict__ l
             ids[(size_t)t * k + r] = sel_e[r];
             w[(size_t)t * k + r] = expf(sel_v[r] - m) / den;
         }
+    }
+}
+
+// Top-k for E <= 64 NV: each lane sorts its NV logits (experts lane + 64 i) once, descending by (value, lower
+// index), and keeps them as a queue; a round is a wave-wide max of the lanes' queue heads (6 exchange stages, ties
+// to the lower index) and the winning lane pops its head. Round r's pick is kept by lane r, so the softmax runs
+// on k lanes at once: exp(v - max) per lane, a wave sum, and each lane writes its id and weight. Same picks, order
+// and weights as k_router_topk.
+template <int NV>
+__global__ __launch_bounds__(256) void k_router_topk_q(const float* __restrict__ logits, int T, int E, int k,
+                                                       int64_t* __restrict__ ids, float* __restrict__ w)
+{
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= T) return;
+    const float* row = logits + (size_t)t * E;
+    float qv[NV];
+    int qe[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+    {
+        const int e = lane + 64 * i;
+        qv[i] = e < E ? row[e] : -INFINITY;
+        qe[i] = e < E ? e : 0x7fffffff;
+    }
+    // insertion sort of the lane's NV entries: (a before b) iff a.v > b.v or (equal and a.e < b.e)
+#pragma unroll
+    for (int i = 1; i < NV; ++i)
+#pragma unroll
+        for (int j = i; j > 0; --j)
+        {
+            const bool sw = qv[j] > qv[j - 1] || (qv[j] == qv[j - 1] && qe[j] < qe[j - 1]);
+            const float tv = qv[j];
+            const int te = qe[j];
+            qv[j] = sw ? qv[j - 1] : tv;
+            qe[j] = sw ? qe[j - 1] : te;
+            qv[j - 1] = sw ? tv : qv[j - 1];
+            qe[j - 1] = sw ? te : qe[j - 1];
+        }
+    float myv = -INFINITY;
+    int mye = 0;
+    for (int r = 0; r < k; ++r)
+    {
+        float bv = qv[0];
+        int be = qe[0];
+        auto pick = [&](float ov, int oe) {
+            if (ov > bv || (ov == bv && oe < be)) { bv = ov; be = oe; }
+        };
+        pick(xor_lane<32>(bv), xor_lane_i<32>(be));
+        pick(xor_lane<16>(bv), xor_lane_i<16>(be));
+        pick(xor_lane<8>(bv), xor_lane_i<8>(be));
+        pick(xor_lane<4>(bv), xor_lane_i<4>(be));
+        pick(xor_lane<2>(bv), xor_lane_i<2>(be));
+        pick(xor_lane<1>(bv), xor_lane_i<1>(be));
+        if (be == qe[0])                                  // this lane's head won: pop it
+        {
+#pragma unroll
+            for (int i = 0; i + 1 < NV; ++i)
+            {
+                qv[i] = qv[i + 1];
+                qe[i] = qe[i + 1];
+            }
+            qv[NV - 1] = -INFINITY;
+            qe[NV - 1] = 0x7fffffff;
+        }
+        if (lane == r)
+        {
+            myv = bv;
+            mye = be;
+        }
+    }
+    // the first pick is the row's maximum; lanes k .. 63 contribute 0 to the sum
+    const float m = __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, myv)));
+    const float z = lane < k ? expf(myv - m) : 0.0f;
+    // den = ((0 + z_0) + z_1) + ... in pick order, on every lane
+    float den = 0.0f;
+    for (int r = 0; r < k; ++r) den += __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, z), r));
+    if (lane < k)
+    {
+        ids[(size_t)t * k + lane] = mye;
+        w[(size_t)t * k + lane] = z / den;
     }
 }
 
@@ -891,16 +1013,24 @@ int mm_router_topk(const void* x_bf16, int T, int H, const float* gate, int E, i
     MM_CHECK_ARG(E > 0 && E <= 1024 && k > 0 && k <= 32 && k <= E, "mm_router_topk: need 0 < k <= 32, k <= E <= 1024");
     MM_CHECK_ARG(x_bf16 && gate && ids && w && logits, "mm_router_topk: null pointer (logits workspace is required)");
     if (T == 0) return MM_OK;
-    if (T <= RT_MAX_T && H % 256 == 0 && ((uintptr_t)x_bf16 & 7) == 0 && ((uintptr_t)gate & 15) == 0)
-        hipLaunchKernelGGL(k_router_gemv, dim3((E + 3) / 4, (T + RT_TB - 1) / RT_TB), dim3(256), 0, S(stream),
-                           (const uint16_t*)x_bf16, gate, logits, T, H, E);
+    if (T <= 4 && H % 256 == 0 && ((uintptr_t)x_bf16 & 7) == 0 && ((uintptr_t)gate & 15) == 0)
+        hipLaunchKernelGGL(k_router_gemv<4>, dim3(E, 1), dim3(256), 0, S(stream), (const uint16_t*)x_bf16, gate,
+                           logits, T, H, E);
+    else if (T <= RT_MAX_T && H % 256 == 0 && ((uintptr_t)x_bf16 & 7) == 0 && ((uintptr_t)gate & 15) == 0)
+        hipLaunchKernelGGL(k_router_gemv<16>, dim3(E, (T + 15) / 16), dim3(256), 0, S(stream), (const uint16_t*)x_bf16,
+                           gate, logits, T, H, E);
     else if (H % RM_K == 0 && ((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)gate & 15) == 0)
         hipLaunchKernelGGL(k_router_mfma, dim3((E + RM_TN - 1) / RM_TN, (T + RM_TM - 1) / RM_TM), dim3(256), 0,
                            S(stream), (const uint16_t*)x_bf16, gate, logits, T, H, E);
     else
         hipLaunchKernelGGL(k_router_logits, dim3((E + 63) / 64, (T + 63) / 64), dim3(256), 0, S(stream),
                            (const uint16_t*)x_bf16, gate, logits, T, H, E);
-    hipLaunchKernelGGL(k_router_topk, dim3((T + 3) / 4), dim3(256), 0, S(stream), logits, T, E, k, ids, w);
+    if (E <= 384)
+        hipLaunchKernelGGL(k_router_topk_q<6>, dim3((T + 3) / 4), dim3(256), 0, S(stream), logits, T, E, k, ids, w);
+    else if (E <= 512)
+        hipLaunchKernelGGL(k_router_topk_q<8>, dim3((T + 3) / 4), dim3(256), 0, S(stream), logits, T, E, k, ids, w);
+    else
+        hipLaunchKernelGGL(k_router_topk, dim3((T + 3) / 4), dim3(256), 0, S(stream), logits, T, E, k, ids, w);
     return check_launch("mm_router_topk");
 }
 
