@@ -162,11 +162,13 @@ def test_combine_matches_oracle(dev, T, k):
     assert np.array_equal(out.cpu().numpy(), ref)     # same fp32 fma chain in ascending j
 
 
-@pytest.mark.parametrize("T", [1, 4, 300])
-def test_router_matches_oracle(dev, T):
+@pytest.mark.parametrize("T,H,E,k", [(1, 4096, 384, 8), (4, 4096, 384, 8), (16, 4096, 384, 8), (64, 5120, 384, 6),
+                                     (300, 4096, 384, 8), (4, 4096, 512, 8), (4, 2048, 1024, 8)])
+def test_router_matches_oracle(dev, T, H, E, k):
+    """Decode sizes (up to 4 tokens per workgroup, then 16), the DSV41 shape, an MFMA-sized call, and the top-k
+    forms for up to 384, 512 and 1024 experts."""
     import torch
     from mi355moe import _lib, workload
-    H, E, k = 4096, 384, 8
     x = workload.activations(T, H, seed=T)
     G = np.random.default_rng(5).normal(0, 0.02, (E, H)).astype(np.float32)
     xb = _t((x.view(np.uint32) >> 16).astype(np.uint16), dev)
@@ -174,7 +176,7 @@ def test_router_matches_oracle(dev, T):
     ids = torch.empty((T, k), dtype=torch.int64, device=dev)
     w = torch.empty((T, k), dtype=torch.float32, device=dev)
     logits = torch.empty((T, E), dtype=torch.float32, device=dev)
-    print(f"router T={T}", flush=True)
+    print(f"router T={T} H={H} E={E} k={k}", flush=True)
     _lib.call("mm_router_topk", xb.data_ptr(), T, H, Gd.data_ptr(), E, k, logits.data_ptr(), ids.data_ptr(), w.data_ptr(),
               _lib.stream_ptr())
     torch.cuda.synchronize()
