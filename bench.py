@@ -708,7 +708,7 @@ def bench_cache(args):
     slots of 8 experts. Routing Zipf(1.1) per layer, the ranking reshuffled by 5 % every 64 steps."""
     import numpy as np
     import torch
-    from mi355moe import _lib, cache, ct_vllm, exl3, workload
+    from mi355moe import _lib, cache, ct_vllm, exl3, tier, workload
     from mi355moe.hostmem import HostBuffer
     from mi355moe.store import ExpertStore
 
@@ -779,6 +779,10 @@ def bench_cache(args):
         return src
 
     stats = {"decode_steps": 0, "decode_s": 0.0, "prefill_chunks": 0, "prefill_s": 0.0}
+
+    def tier_busy():                      # the host tier's cumulative busy time (ns), 0 without the tier
+        return tier.stats()["busy_ns"] if args.cpu_tier else 0
+    busy0 = None
     x0 = torch.from_numpy(workload.activations(T, H, seed=7)).to(dev).to(torch.bfloat16)
     total_steps = args.cache_steps
     step = 0
@@ -818,11 +822,13 @@ def bench_cache(args):
             stats["decode_steps"] += 1
             if hit0 is None:
                 hit0 = ct_vllm.S["stats"].tolist()
+                busy0 = tier_busy()
         step += 1
         if step % 32 == 0:
             log(f"cache: step {step}/{total_steps} decode {dt * 1e3:.1f} ms {ct_vllm.summary()}")
     total_s = time.perf_counter() - t_all
     st = ct_vllm.S["stats"].tolist()
+    busy_ms = (tier_busy() - busy0) * 1e-6 if busy0 is not None else 0.0
     # a lone prefill step of hyb_tokens tokens (every layer's experts staged: the cache is released first), with
     # the host tier taking each layer's trailing staging batches (the hybrid tail) and without it
     hybrid = None
@@ -878,7 +884,9 @@ def bench_cache(args):
                            max(stats["decode_s"] + stats["prefill_s"], 1e-9), 2),
         "prefill_chunks": stats["prefill_chunks"], "prefill_s": round(stats["prefill_s"], 3),
         "cpu_tier": bool(args.cpu_tier), "host_experts": summ["cpu_experts"], "host_jobs": summ["host_jobs"],
-        "host_timeouts": summ["timeouts"], "policy": policy, "hybrid_prefill": hybrid,
+        "host_timeouts": summ["timeouts"],
+        "host_busy_ms_per_step": round(busy_ms / max(1, stats["decode_steps"]), 3),
+        "policy": policy, "hybrid_prefill": hybrid,
         "ec": ct_vllm.ec_summary(), "wall_s": round(total_s, 1),
     }
     ct_vllm.uninstall(exl3)
