@@ -388,26 +388,12 @@ def decode_step(stores, E, H, I, K, T, L, steps, warmup, roofline):
     with torch.cuda.graph(graph):
         final = step()
     torch.cuda.synchronize()
-    for _ in range(warmup):
-        graph.replay()
-    torch.cuda.synchronize()
-    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    t_start = time.perf_counter()
-    ev0.record()
-    for _ in range(steps):
-        graph.replay()
-    ev1.record()
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - t_start
-    ms_step = ev0.elapsed_time(ev1) / steps
-    out_rms = float(final.float().pow(2).mean().sqrt())
-    step_bytes = float(sum((u + 1) * expert_bytes(H, I) for u in uniq))
-    res = {"ms_step": ms_step, "ms_wall": wall * 1e3 / steps, "uniq": uniq, "step_bytes": step_bytes,
-           "out_rms": out_rms}
-    log(f"decode {H}/{I} T={T} top-{K}: step {ms_step:.3f} ms (wall {res['ms_wall']:.3f} ms), "
-        f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s, final output rms {out_rms:.4f}")
+    res = {}
     if roofline:
-        # every runner's workspace holds its layer's routing records from the step replays above
+        # Kernel-level timings first (every runner's workspace holds its layer's routing records from the eager pass
+        # above). Each is taken at the GPU's steady clocks: from idle, this load runs about 20 % slower for its first
+        # 30 ms or so while the clocks ramp up, so a graph is replayed untimed for at least 60 ms before its timed
+        # replays. As a side effect the step below is also timed at steady clocks.
         def kernel_graph(phase):
             g = torch.cuda.CUDAGraph()
             with torch.cuda.graph(g):
@@ -415,10 +401,16 @@ def decode_step(stores, E, H, I, K, T, L, steps, warmup, roofline):
                     runners[l].experts(stores[l], x=outs[0], phases=phase)
             return g
 
-        def time_graph(g, reps=5):
-            g.replay()
-            torch.cuda.synchronize()
+        def time_graph(g, warm_ms=60.0, reps=20):
             e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            spent = 0.0
+            while spent < warm_ms:
+                e0.record()
+                for _ in range(5):
+                    g.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                spent += e0.elapsed_time(e1)
             e0.record()
             for _ in range(reps):
                 g.replay()
@@ -458,6 +450,24 @@ def decode_step(stores, E, H, I, K, T, L, steps, warmup, roofline):
         res["bytes_gu"] = float(np.mean([(u + 1) * bgu for u in uniq]))
         res["bytes_d"] = float(np.mean([(u + 1) * trellis_bytes(I, H) for u in uniq]))
         del g_gu, g_d
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t_start = time.perf_counter()
+    ev0.record()
+    for _ in range(steps):
+        graph.replay()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t_start
+    ms_step = ev0.elapsed_time(ev1) / steps
+    out_rms = float(final.float().pow(2).mean().sqrt())
+    step_bytes = float(sum((u + 1) * expert_bytes(H, I) for u in uniq))
+    res.update({"ms_step": ms_step, "ms_wall": wall * 1e3 / steps, "uniq": uniq, "step_bytes": step_bytes,
+                "out_rms": out_rms})
+    log(f"decode {H}/{I} T={T} top-{K}: step {ms_step:.3f} ms (wall {res['ms_wall']:.3f} ms), "
+        f"{step_bytes / (ms_step * 1e-3) / 1e9:.0f} GB/s, final output rms {out_rms:.4f}")
     del graph
     return res
 
