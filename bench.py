@@ -498,10 +498,16 @@ def bench_prefill(store, E, H, I, k, reps, tokens=16384, cap=32):
         _lib.call("mm_grouped_gemm", store.mm_layer(), x.data_ptr(), _lib.DTYPE_BF16, tokens, k, idd.data_ptr(), cap,
                   Y.data_ptr(), ws.data_ptr(), wsb, _lib.stream_ptr())
 
-    def timed(fn):
-        fn()
-        torch.cuda.synchronize()
+    def timed(fn, warm_ms=60.0):
+        # untimed calls for at least warm_ms first, so the timed ones run at the GPU's steady clocks
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        spent = 0.0
+        while spent < warm_ms:
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            spent += e0.elapsed_time(e1)
         e0.record()
         for _ in range(reps):
             fn()
