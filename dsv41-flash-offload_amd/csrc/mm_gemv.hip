@@ -827,20 +827,34 @@ static Ws carve(void* base, int n, int npos, int E, int H, int I)
     return w;
 }
 
-// Waves of one partial launch: the whole GPU once (WAVES_PER_CU per CU), a multiple of 8 workgroups.
-static int partial_waves()
+// Waves of one partial launch: the whole GPU once (WAVES_PER_CU per CU, a multiple of 8 workgroups), or half of
+// that (three waves per SIMD) when the call's segments would otherwise be cut into more than 12 pieces each
+// even with every route on an expert of its own (nseg_max = min(n, E) x matrices x column blocks): at one token
+// and top-8 + 1 the 288 segments of a launch would take 21 pieces each, which the epilogues add in round trips
+// of 24 loads; with half the waves they take 10-11, added in one round trip of 12, and the partial kernels run
+// as fast with three waves per SIMD on runs twice as long (one-token step 4 % shorter). The partial kernel
+// finds its wave count from its grid, and the epilogues are given the same value.
+static int partial_waves(int64_t nseg_max)
 {
-    static int waves = 0;
-    if (!waves)
+    static int full = 0;
+    if (!full)
     {
         int dev = 0, cus = 0;
         if (hipGetDevice(&dev) != hipSuccess ||
             hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
             cus = 256;
         const int blocks = ((cus * WAVES_PER_CU / GV_WAVES) + 7) & ~7;
-        waves = blocks * GV_WAVES;
+        full = blocks * GV_WAVES;
     }
-    return waves;
+    if ((int64_t)full > 12 * nseg_max)
+        return (((full / GV_WAVES) / 2 + 7) & ~7) * GV_WAVES;
+    return full;
+}
+// the segment bound of a partial launch of mode 0 (gate/up) or 1 (down) over n routes
+static int64_t seg_max(const mm_layer_t* L, int n, int mode)
+{
+    const int64_t na = n < L->E ? n : L->E;
+    return mode == 0 ? na * 2 * (L->I / GV_COLS) : na * (L->H / GV_COLS);
 }
 
 static int check_common(const mm_layer_t* L, const void* x, int x_dtype, int T, int n, int topk, const int64_t* ids,
@@ -892,7 +906,7 @@ static void launch_partial(const mm_layer_t* L, const Ws& w, int npos, hipStream
     const int K = MODE == 0 ? L->H : L->I, N = MODE == 0 ? L->I : L->H;
     PartArgs p{ w.rec, w.counts, MODE == 0 ? w.xa : w.xd, MODE == 0 ? w.part_gu : w.part_d, npos, K, N, N / GV_COLS,
                 piece_cap(npos) };
-    const dim3 grid(partial_waves() / GV_WAVES), block(GV_THREADS);
+    const dim3 grid(partial_waves(seg_max(L, npos, MODE)) / GV_WAVES), block(GV_THREADS);
     if (L->flags & MM_LAYER_EXACT)
         hipLaunchKernelGGL((k_partial<MODE, true>), grid, block, 0, s, p);
     else
@@ -902,7 +916,7 @@ static void launch_partial(const mm_layer_t* L, const Ws& w, int npos, hipStream
 static void launch_gu_epilogue(const mm_layer_t* L, const Ws& w, int npos, hipStream_t s)
 {
     GuEpiArgs g{ w.part_gu, w.xsum, w.counts, w.e_at, w.ai_at, L->svh13, L->suh2, w.xd, w.xdsum, npos, L->H, L->I,
-                 prep_blocks(L->H), partial_waves(), piece_cap(npos), (L->flags & MM_LAYER_EXACT) ? 0 : 1, L->limit };
+                 prep_blocks(L->H), partial_waves(seg_max(L, npos, 0)), piece_cap(npos), (L->flags & MM_LAYER_EXACT) ? 0 : 1, L->limit };
     hipLaunchKernelGGL(k_gu_epilogue, dim3((npos * (L->I / GV_COLS) + 3) / 4), dim3(256), 0, s, g);
 }
 
@@ -910,7 +924,7 @@ static DEpiArgs down_args(const mm_layer_t* L, const Ws& w, int npos, int topk, 
                           float* Y, float* out, int accumulate)
 {
     return DEpiArgs{ w.part_d, w.xdsum, w.counts, w.pos_of, w.route_at, w.e_at, w.ai_at, w.ai_of, ids, wt, L->svh2, Y, out, npos, L->H,
-                     L->I, topk, partial_waves(), piece_cap(npos), (L->flags & MM_LAYER_EXACT) ? 0 : 1, accumulate };
+                     L->I, topk, partial_waves(seg_max(L, npos, 1)), piece_cap(npos), (L->flags & MM_LAYER_EXACT) ? 0 : 1, accumulate };
 }
 
 // One decode layer (mm_moe_decode) on a caller-provided workspace; `who` names the entry point in errors.
