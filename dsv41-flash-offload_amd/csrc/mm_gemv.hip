@@ -39,6 +39,7 @@ static_assert(GV_RING % 2 == 0, "row pairs");
 constexpr int ROW_BYTES = 8 * 96;     // one tile row of a segment
 constexpr int WAVES_PER_CU = 24;      // partial kernels: 6 workgroups of 4 waves per CU (<= 80 VGPRs, 16 KB LDS)
 constexpr int PREP_ROWS = 512;        // input rows per route-prep workgroup
+constexpr int SS_LOADS = 16;          // route prep: row elements per thread loaded at once for the rescale
 constexpr int MAX_TOPK = 16;
 
 // Rows of a partial launch: nseg segments of KT tile rows each (KT a multiple of 8), in segment order, cut into
@@ -84,8 +85,8 @@ __device__ __forceinline__ int seg_pieces(const RowSplit& s, int seg, int KT)
 
 // Every load that does not depend on another is issued before the first barrier, with no branch in between (the
 // route's id, all ids for the position, the token row for the rescale, this wave's block of it; the loads that need
-// the expert follow with clamped indices), and the routing counts and the row's sum of squares share one
-// reduction, so the kernel costs about two memory round trips. XD = the input's element type.
+// the expert follow with clamped indices, before the row's sum of squares is formed), and the routing counts and
+// the row's sum of squares share one reduction, so the kernel costs about two memory round trips. XD = the input's element type.
 template <int XD>
 __device__ __forceinline__ float load_x_t(const void* x, size_t i)
 {
@@ -127,17 +128,12 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
 #pragma unroll
         for (int k = 0; k < 4; ++k) act[k] = a.active[min(tid + 256 * k, a.E - 1)];
     }
+    // the row for its sum of squares: h = tid + 256 j, the first SS_LOADS of them issued here with the other first
+    // loads (rows up to 256 SS_LOADS elements in one round trip), summed below in the same order
+    float xr[SS_LOADS];
     if (a.rescale)
-        // the row's sum of squares, h = tid, tid + 256, ... in order; eight loads in flight before they are used
-        for (int hb = tid; hb < a.H; hb += 256 * 8)
-        {
-            float v[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) v[k] = load_x_t<XD>(a.x, row + min(hb + 256 * k, a.H - 1));
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (hb + 256 * k < a.H) ss = fmaf(v[k], v[k], ss);
-        }
+        for (int j = 0; j < SS_LOADS; ++j) xr[j] = load_x_t<XD>(a.x, row + min(tid + 256 * j, a.H - 1));
     const bool valid = perm ? idx < nvalid_perm : (e64 >= 0 && e64 < a.E);
     const int e = valid ? (int)e64 : -1;
     const int ec = valid ? e : 0;               // an expert in range for the loads
@@ -152,6 +148,17 @@ __global__ __launch_bounds__(256) void k_route_prep(PrepArgs a)
         wt0 = a.wtab0[e];
         wt1 = a.wtab1[e];
         wt2 = a.wtab2[e];
+    }
+    if (a.rescale)
+    {
+#pragma unroll
+        for (int j = 0; j < SS_LOADS; ++j)
+            if (tid + 256 * j < a.H) ss = fmaf(xr[j], xr[j], ss);
+        for (int h = tid + 256 * SS_LOADS; h < a.H; h += 256)
+        {
+            const float v = load_x_t<XD>(a.x, row + h);
+            ss = fmaf(v, v, ss);
+        }
     }
     if (tid < 32) s_bm[tid] = 0;
     if (tid == 0) s_ai = -1;
