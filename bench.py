@@ -326,7 +326,10 @@ def run_cache_child(p, timeout_s=900):
     if p.returncode != 0 or not lines:
         return {"error": f"child exited with status {p.returncode}", "process": "child",
                 "wall_s": round(time.time() - t0, 1)}
-    r = json.loads(lines[-1])["cache"]
+    try:
+        r = json.loads(lines[-1])["cache"]
+    except (ValueError, KeyError, TypeError) as ex:
+        return {"error": f"unreadable child output: {ex!r}", "process": "child"}
     r["process"] = "child"
     return r
 
