@@ -108,6 +108,29 @@ def test_full_shape_layer_with_shared_expert(dev, T, exact):
     assert ok, m
 
 
+@pytest.mark.parametrize("T,k", [(1, 14), (2, 7)])
+def test_full_shape_either_side_of_the_wave_count_switch(dev, T, k):
+    """The partial launches take three waves per SIMD when a full launch would cut every segment into more than 12
+    pieces: 15 routes (14 + the shared expert, at most 480 segments per launch) fall below the switch and 16 (two
+    tokens of 7 + 1, 512) above it; both against the oracle at the benchmark shape."""
+    import torch
+    from mi355moe import moe, workload
+    H, I, E = 4096, 2048, 384
+    seed = 1100 + T
+    st = make_store(E + 1, H, I, seed, device=dev)
+    ids, w = workload.zipf_routing(T, k, E, seed=2100 + T)
+    x16 = workload.activations(T, H, seed=8).astype(np.float16)
+    print(f"wave-count switch T={T} k={k}", flush=True)
+    out = moe.moe_forward(st, _t(x16, dev), _t(ids, dev), _t(w, dev), shared_expert=E)
+    torch.cuda.synchronize()
+    ids_ext = np.concatenate([ids, np.full((T, 1), E)], 1)
+    w_ext = np.concatenate([w, np.ones((T, 1), np.float32)], 1)
+    ref = OracleLayer(st, seed).forward(x16.astype(np.float32), ids_ext, w_ext)
+    ok, m = within_tolerance(out.cpu().numpy(), ref)
+    print("tolerance metrics", m, flush=True)
+    assert ok, m
+
+
 def test_deterministic_and_runner_matches(dev):
     import torch
     from mi355moe import moe, workload
