@@ -206,7 +206,11 @@ __global__ __launch_bounds__(256) void k_router_gemv(const uint16_t* __restrict_
 // tile (split into the three bf16 planes on the way into LDS) are staged, the next step's loads are in flight
 // during the multiplies; wave (wm, wn) takes tokens 32 wm .. + 31 and experts 64 wn .. + 63 (2 x 4 tiles x 3 parts).
 constexpr int RM_TM = 64, RM_TN = 128, RM_K = 32;
-constexpr int RM_ROW = 40;            // LDS row stride in bf16 (80 bytes: the 16 rows of an operand read hit 16 bank groups)
+constexpr int RM_ROW = 32;            // LDS row: 32 bf16 = four 16-byte chunks, chunk q of row r stored at q ^ ((r >> 2) & 3)
+// The swizzle puts the 16 rows of an operand read (one chunk each) and the 16 chunks of four rows that 16 lanes
+// write in 16 distinct 16-byte bank groups (the padded 80-byte rows read conflict-free but wrote with conflicts:
+// 36 % of the kernel's LDS cycles).
+__device__ __forceinline__ int rm_at(int r, int q) { return r * RM_ROW + 8 * (q ^ ((r >> 2) & 3)); }
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float rm_f4_t __attribute__((ext_vector_type(4)));
 
@@ -261,7 +265,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
     for (int s = 0; s < S; ++s)
     {
         __syncthreads();                                       // the previous step's operand reads are done
-        *reinterpret_cast<uint4*>(&xs[xr * RM_ROW + 8 * xq]) = xv;
+        *reinterpret_cast<uint4*>(&xs[rm_at(xr, xq)]) = xv;
 #pragma unroll
         for (int j = 0; j < 4; ++j)
         {
@@ -270,7 +274,7 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
             split(gv[j].y, a[1], b[1], c[1]);
             split(gv[j].z, a[2], b[2], c[2]);
             split(gv[j].w, a[3], b[3], c[3]);
-            const int o = gr[j] * RM_ROW + 4 * gq[j];
+            const int o = rm_at(gr[j], gq[j] >> 1) + 4 * (gq[j] & 1);
             *reinterpret_cast<uint2*>(&gs[0][o]) = make_uint2(a[0] | (a[1] << 16), a[2] | (a[3] << 16));
             *reinterpret_cast<uint2*>(&gs[1][o]) = make_uint2(b[0] | (b[1] << 16), b[2] | (b[3] << 16));
             *reinterpret_cast<uint2*>(&gs[2][o]) = make_uint2(c[0] | (c[1] << 16), c[2] | (c[3] << 16));
@@ -280,12 +284,12 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
         bf16x8_t A[2], B[3][4];
 #pragma unroll
         for (int i = 0; i < 2; ++i)
-            A[i] = *reinterpret_cast<const bf16x8_t*>(&xs[(32 * wm + 16 * i + (lane & 15)) * RM_ROW + 8 * (lane >> 4)]);
+            A[i] = *reinterpret_cast<const bf16x8_t*>(&xs[rm_at(32 * wm + 16 * i + (lane & 15), lane >> 4)]);
 #pragma unroll
         for (int p = 0; p < 3; ++p)
 #pragma unroll
             for (int j = 0; j < 4; ++j)
-                B[p][j] = *reinterpret_cast<const bf16x8_t*>(&gs[p][(64 * wn + 16 * j + (lane & 15)) * RM_ROW + 8 * (lane >> 4)]);
+                B[p][j] = *reinterpret_cast<const bf16x8_t*>(&gs[p][rm_at(64 * wn + 16 * j + (lane & 15), lane >> 4)]);
 #pragma unroll
         for (int p = 0; p < 3; ++p)
 #pragma unroll
