@@ -202,10 +202,13 @@ __global__ __launch_bounds__(256) void k_router_gemv(const uint16_t* __restrict_
 // parts, g = g1 + g2 + g3: g1 is g with its low 16 bits cleared (its top 8 significant bits), g2 the same of the
 // exact remainder g - g1, and g3 = g - g1 - g2, which has at most 8 significant bits; each product of a bf16 input
 // with a part is exact in fp32, so the MFMA's fp32 accumulation is the only rounding, as in an fp32 dot product
-// (in another order). A workgroup computes 64 tokens x 128 experts: per 32-row step the input tile and the gate
-// tile (split into the three bf16 planes on the way into LDS) are staged, the next step's loads are in flight
-// during the multiplies; wave (wm, wn) takes tokens 32 wm .. + 31 and experts 64 wn .. + 63 (2 x 4 tiles x 3 parts).
-constexpr int RM_TM = 64, RM_TN = 128, RM_K = 32;
+// (in another order). A workgroup of WM x WN waves computes TM tokens x TN experts: per 32-row step the input tile
+// and the gate tile (split into the three bf16 planes on the way into LDS) are staged, the next step's loads are in
+// flight during the multiplies; wave (wm, wn) takes tokens TM / WM wm .. and experts TN / WN wn ... The launch uses
+// 128 tokens x 192 experts on 8 waves (2 x 6 tiles x 3 parts per wave): each gate element is split once per 128
+// tokens, and 16,384 tokens x 384 experts are 256 workgroups, one per CU (router call at that size: 64 x 128 on 4
+// waves 233-242 us, this shape 201-210 us; two LDS stages with one barrier per step 220-222 us).
+constexpr int RM_TM = 128, RM_TN = 192, RM_WM = 4, RM_WN = 2, RM_K = 32;
 constexpr int RM_ROW = 32;            // LDS row: 32 bf16 = four 16-byte chunks, chunk q of row r stored at q ^ ((r >> 2) & 3)
 // The swizzle puts the 16 rows of an operand read (one chunk each) and the 16 chunks of four rows that 16 lanes
 // write in 16 distinct 16-byte bank groups (the padded 80-byte rows read conflict-free but wrote with conflicts:
@@ -214,37 +217,52 @@ __device__ __forceinline__ int rm_at(int r, int q) { return r * RM_ROW + 8 * (q 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float rm_f4_t __attribute__((ext_vector_type(4)));
 
-__global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict__ x, const float* __restrict__ G,
-                                                     float* __restrict__ logits, int T, int H, int E)
+template <int TM, int TN, int WM, int WN>
+__global__ __launch_bounds__(64 * WM * WN) void k_router_mfma(const uint16_t* __restrict__ x, const float* __restrict__ G,
+                                                              float* __restrict__ logits, int T, int H, int E)
 {
-    __shared__ __align__(16) uint16_t xs[RM_TM * RM_ROW];
-    __shared__ __align__(16) uint16_t gs[3][RM_TN * RM_ROW];
+    constexpr int NT = 64 * WM * WN;                        // threads
+    constexpr int MI = TM / WM / 16, NJ = TN / WN / 16;      // 16 x 16 tiles per wave
+    constexpr int XL = 4 * TM / NT, GL = 8 * TN / NT;        // 16-byte loads per thread and step
+    static_assert(MI * WM * 16 == TM && NJ * WN * 16 == TN && XL * NT == 4 * TM && GL * NT == 8 * TN, "tile shape");
+    __shared__ __align__(16) uint16_t xs[TM * RM_ROW];
+    __shared__ __align__(16) uint16_t gs[3][TN * RM_ROW];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int t0 = blockIdx.y * RM_TM, e0 = blockIdx.x * RM_TN;
-    const int wm = wave >> 1, wn = wave & 1;
-    // this thread's loads of a step: one 16-byte chunk of the input tile (64 rows x 4 chunks), four of the gate tile
-    // (128 rows x 8 chunks of 4 floats); rows past T or E load zeros
-    const int xr = tid >> 2, xq = tid & 3;
-    const bool xin = t0 + xr < T;
-    const uint16_t* xp = x + (size_t)min(t0 + xr, T - 1) * H + 8 * xq;
-    int gr[4], gq[4];
-    bool gin[4];
-    const float* gp[4];
+    const int t0 = blockIdx.y * TM, e0 = blockIdx.x * TN;
+    const int wm = wave / WN, wn = wave % WN;
+    // this thread's loads of a step: XL 16-byte chunks of the input tile (TM rows x 4 chunks), GL of the gate tile
+    // (TN rows x 8 chunks of 4 floats); rows past T or E load zeros
+    int xr[XL], xq[XL];
+    bool xin[XL];
+    const uint16_t* xp[XL];
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < XL; ++j)
     {
-        const int c = tid + 256 * j;
+        const int c = tid + NT * j;
+        xr[j] = c >> 2;
+        xq[j] = c & 3;
+        xin[j] = t0 + xr[j] < T;
+        xp[j] = x + (size_t)min(t0 + xr[j], T - 1) * H + 8 * xq[j];
+    }
+    int gr[GL], gq[GL];
+    bool gin[GL];
+    const float* gp[GL];
+#pragma unroll
+    for (int j = 0; j < GL; ++j)
+    {
+        const int c = tid + NT * j;
         gr[j] = c >> 3;
         gq[j] = c & 7;
         gin[j] = e0 + gr[j] < E;
         gp[j] = G + (size_t)min(e0 + gr[j], E - 1) * H + 4 * gq[j];
     }
-    uint4 xv;
-    float4 gv[4];
+    uint4 xv[XL];
+    float4 gv[GL];
     auto load = [&](int k0) {
-        xv = xin ? *reinterpret_cast<const uint4*>(xp + k0) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) gv[j] = gin[j] ? *reinterpret_cast<const float4*>(gp[j] + k0) : make_float4(0, 0, 0, 0);
+        for (int j = 0; j < XL; ++j) xv[j] = xin[j] ? *reinterpret_cast<const uint4*>(xp[j] + k0) : make_uint4(0, 0, 0, 0);
+#pragma unroll
+        for (int j = 0; j < GL; ++j) gv[j] = gin[j] ? *reinterpret_cast<const float4*>(gp[j] + k0) : make_float4(0, 0, 0, 0);
     };
     auto split = [](float g, uint32_t& a, uint32_t& b, uint32_t& c) {
         const uint32_t h1 = __float_as_uint(g) & 0xffff0000u;
@@ -255,19 +273,20 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
         b = h2 >> 16;
         c = __float_as_uint(r2) >> 16;
     };
-    rm_f4_t acc[2][4];
+    rm_f4_t acc[MI][NJ];
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = rm_f4_t{ 0.f, 0.f, 0.f, 0.f };
+        for (int j = 0; j < NJ; ++j) acc[i][j] = rm_f4_t{ 0.f, 0.f, 0.f, 0.f };
     const int S = H / RM_K;
     load(0);
     for (int s = 0; s < S; ++s)
     {
         __syncthreads();                                       // the previous step's operand reads are done
-        *reinterpret_cast<uint4*>(&xs[rm_at(xr, xq)]) = xv;
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < XL; ++j) *reinterpret_cast<uint4*>(&xs[rm_at(xr[j], xq[j])]) = xv[j];
+#pragma unroll
+        for (int j = 0; j < GL; ++j)
         {
             uint32_t a[4], b[4], c[4];
             split(gv[j].x, a[0], b[0], c[0]);
@@ -281,34 +300,34 @@ __global__ __launch_bounds__(256) void k_router_mfma(const uint16_t* __restrict_
         }
         __syncthreads();
         if (s + 1 < S) load((s + 1) * RM_K);
-        bf16x8_t A[2], B[3][4];
+        bf16x8_t A[MI], B[3][NJ];
 #pragma unroll
-        for (int i = 0; i < 2; ++i)
-            A[i] = *reinterpret_cast<const bf16x8_t*>(&xs[rm_at(32 * wm + 16 * i + (lane & 15), lane >> 4)]);
-#pragma unroll
-        for (int p = 0; p < 3; ++p)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                B[p][j] = *reinterpret_cast<const bf16x8_t*>(&gs[p][rm_at(64 * wn + 16 * j + (lane & 15), lane >> 4)]);
+        for (int i = 0; i < MI; ++i)
+            A[i] = *reinterpret_cast<const bf16x8_t*>(&xs[rm_at(16 * (MI * wm + i) + (lane & 15), lane >> 4)]);
 #pragma unroll
         for (int p = 0; p < 3; ++p)
 #pragma unroll
-            for (int i = 0; i < 2; ++i)
+            for (int j = 0; j < NJ; ++j)
+                B[p][j] = *reinterpret_cast<const bf16x8_t*>(&gs[p][rm_at(16 * (NJ * wn + j) + (lane & 15), lane >> 4)]);
 #pragma unroll
-                for (int j = 0; j < 4; ++j)
+        for (int p = 0; p < 3; ++p)
+#pragma unroll
+            for (int i = 0; i < MI; ++i)
+#pragma unroll
+                for (int j = 0; j < NJ; ++j)
                     acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(A[i], B[p][j], acc[i][j], 0, 0, 0);
     }
     // D: lane (column l & 15, group l >> 4) holds rows 4 g .. 4 g + 3 of its column of each tile
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < MI; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j)
+        for (int j = 0; j < NJ; ++j)
         {
-            const int e = e0 + 64 * wn + 16 * j + (lane & 15);
+            const int e = e0 + 16 * (NJ * wn + j) + (lane & 15);
 #pragma unroll
             for (int r = 0; r < 4; ++r)
             {
-                const int t = t0 + 32 * wm + 16 * i + 4 * (lane >> 4) + r;
+                const int t = t0 + 16 * (MI * wm + i) + 4 * (lane >> 4) + r;
                 if (t < T && e < E) logits[(size_t)t * E + e] = acc[i][j][r];
             }
         }
@@ -1024,8 +1043,9 @@ int mm_router_topk(const void* x_bf16, int T, int H, const float* gate, int E, i
         hipLaunchKernelGGL(k_router_gemv<16>, dim3(E, (T + 15) / 16), dim3(256), 0, S(stream), (const uint16_t*)x_bf16,
                            gate, logits, T, H, E);
     else if (H % RM_K == 0 && ((uintptr_t)x_bf16 & 15) == 0 && ((uintptr_t)gate & 15) == 0)
-        hipLaunchKernelGGL(k_router_mfma, dim3((E + RM_TN - 1) / RM_TN, (T + RM_TM - 1) / RM_TM), dim3(256), 0,
-                           S(stream), (const uint16_t*)x_bf16, gate, logits, T, H, E);
+        hipLaunchKernelGGL((k_router_mfma<RM_TM, RM_TN, RM_WM, RM_WN>), dim3((E + RM_TN - 1) / RM_TN,
+                           (T + RM_TM - 1) / RM_TM), dim3(64 * RM_WM * RM_WN), 0, S(stream),
+                           (const uint16_t*)x_bf16, gate, logits, T, H, E);
     else
         hipLaunchKernelGGL(k_router_logits, dim3((E + 63) / 64, (T + 63) / 64), dim3(256), 0, S(stream),
                            (const uint16_t*)x_bf16, gate, logits, T, H, E);
