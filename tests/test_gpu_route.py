@@ -163,10 +163,12 @@ def test_combine_matches_oracle(dev, T, k):
 
 
 @pytest.mark.parametrize("T,H,E,k", [(1, 4096, 384, 8), (4, 4096, 384, 8), (16, 4096, 384, 8), (64, 5120, 384, 6),
-                                     (300, 4096, 384, 8), (4, 4096, 512, 8), (4, 2048, 1024, 8)])
+                                     (300, 4096, 384, 8), (4, 4096, 512, 8), (4, 2048, 1024, 8),
+                                     (300, 2080, 512, 8), (129, 4096, 200, 8)])
 def test_router_matches_oracle(dev, T, H, E, k):
-    """Decode sizes (up to 4 tokens per workgroup, then 16), the DSV41 shape, an MFMA-sized call, and the top-k
-    forms for up to 384, 512 and 1024 experts."""
+    """Decode sizes (up to 4 tokens per workgroup, then 16), the DSV41 shape, MFMA-sized calls (with partial token
+    and expert tiles and a hidden size that is an odd multiple of 32), and the top-k forms for up to 384, 512 and
+    1024 experts."""
     import torch
     from mi355moe import _lib, workload
     x = workload.activations(T, H, seed=T)
